@@ -1,0 +1,899 @@
+// Llama-dense prefill/decode runtime on one GPU.
+//
+// * LlamaModel   = ModelInstance + BackendSidecar of the reference
+//   (model_instance.h:10-32, backend_sidecar.h:14-32) for the device: weights are
+//   generated/repacked straight into one HBM slab, with a per-weight identity
+//   (layer, role) instead of the reference's (op, selector) dedup
+//   (weight_prepack_planner.cpp:79-90).
+// * Plans follow the per-layer node order of ModelGraphBuilder::BuildLlamaDense
+//   (model_graph_builder.cpp:133-290, 356-415).  Every step is a DeviceOperator
+//   resolved through the KernelRegistry at plan-build time (no hot-path lookups,
+//   test_no_hotpath_resolve.cpp), executed by LayerRunner on the session's HIP stream.
+//   The fused decode plan is the same node sequence after the gfx950 fusion pass:
+//     RmsNorm+Linear q/k/v+RoPE+KVCacheUpdate -> one kernel,
+//     Linear o + Add, Linear down + Add        -> GEMV with residual epilogue,
+//     RmsNorm+Linear gate/up+SiluMul           -> one kernel,
+//     RmsNorm+Linear lm_head+Argmax            -> one kernel.
+// * Session = PrepareSession/Prefill/DecodeStep of executor_design.md:226-256: the
+//   KV cache is reserved through KVCacheManager, decode state (token, position, step,
+//   token history) lives in device memory, and the decode plan is captured once as a
+//   HIP graph and replayed per token without host synchronisation.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <memory>
+#include <vector>
+
+#include "am_core.h"
+#include "am_runtime.h"
+#include "gfx950_backend.h"
+
+namespace am {
+am_status_code SetLastError(am_status_code code, const char* msg);
+int DeviceCUs();
+}  // namespace am
+
+namespace aethermind::llama {
+
+using gfx950::DeviceOperator;
+using gfx950::HipSelector;
+using gfx950::PackAttrs;
+
+#define AM_HIP_OK(expr)                                                              \
+  do {                                                                               \
+    hipError_t e_ = (expr);                                                          \
+    if (e_ != hipSuccess) return Status::Internal(std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+#define AM_C_OK(expr)                                                        \
+  do {                                                                       \
+    am_status_code c_ = (expr);                                              \
+    if (c_ != AM_STATUS_OK) return Status::FromC(c_, am_last_error_message()); \
+  } while (0)
+
+namespace {
+
+constexpr uint64_t kEmbedId = 0x01;
+constexpr uint64_t kLmHeadId = 0x02;
+enum SynthRole : uint64_t { kRQ = 1, kRK, kRV, kRO, kRGate, kRUp, kRDown };
+uint64_t LayerTensorId(int layer, SynthRole r) { return (static_cast<uint64_t>(layer + 1) << 8) | r; }
+
+DataType ActType(int32_t dt) { return dt == AM_DT_BF16 ? DataType::BFloat(16) : DataType::Float32(); }
+size_t ActBytes(int32_t dt) { return dt == AM_DT_BF16 ? 2 : 4; }
+
+DataType WeightDType(int32_t fmt) {
+  switch (fmt) {
+    case AM_WF_F32: return DataType::Float32();
+    case AM_WF_BF16: return DataType::BFloat(16);
+    case AM_WF_INT8: return DataType::Int(8);
+    default: return DataType::Int(4);
+  }
+}
+WeightFormat SelFormat(int32_t fmt) {
+  return fmt == AM_WF_INT8 ? WeightFormat::kQuantizedInt8
+                           : (fmt == AM_WF_INT4 ? WeightFormat::kQuantizedInt4 : WeightFormat::kPlain);
+}
+
+struct Slab {
+  void* base = nullptr;
+  size_t size = 0, off = 0;
+  void* Take(size_t bytes) {
+    off = (off + 255) & ~size_t{255};
+    void* p = static_cast<char*>(base) + off;
+    off += bytes;
+    return p;
+  }
+};
+
+}  // namespace
+
+class LlamaModel {
+ public:
+  am_model_config cfg{};
+  hipStream_t stream = nullptr;
+  Slab slab;
+  void* embed = nullptr;
+  std::vector<void*> in_norm, post_norm;
+  void* final_norm = nullptr;
+  std::vector<am_gfx950_weight> qkv, o, gate_up, down;
+  am_gfx950_weight lm_head{};
+  float* cos_tab = nullptr;
+  float* sin_tab = nullptr;
+  int64_t linear_bytes = 0;
+
+  ~LlamaModel() {
+    if (slab.base) (void)hipFree(slab.base);
+  }
+
+  int64_t KvRows() const { return static_cast<int64_t>(cfg.num_kv_heads) * cfg.head_dim; }
+  int64_t QRows() const { return static_cast<int64_t>(cfg.num_q_heads) * cfg.head_dim; }
+
+  am_gfx950_weight RowView(const am_gfx950_weight& w, int64_t row0, int64_t rows) const {
+    am_gfx950_weight v = w;
+    int64_t rb = 0;
+    switch (w.format) {
+      case AM_WF_F32: rb = w.k * 4; break;
+      case AM_WF_BF16: rb = w.k * 2; break;
+      case AM_WF_INT8: rb = w.k; break;
+      default: rb = w.k / 2; break;
+    }
+    v.data = static_cast<const char*>(w.data) + row0 * rb;
+    if (w.format == AM_WF_INT8) v.scales = static_cast<const float*>(w.scales) + row0;
+    if (w.format == AM_WF_INT4) v.scales = static_cast<const uint16_t*>(w.scales) + row0 * (w.k / w.group_size);
+    v.n = rows;
+    return v;
+  }
+
+  Status Validate() const {
+    const auto& c = cfg;
+    if (c.num_layers <= 0 || c.hidden <= 0 || c.num_q_heads <= 0 || c.num_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.ffn <= 0 || c.vocab <= 0)
+      return Status::InvalidArgument("model config dimensions must be positive");
+    if (c.num_q_heads % c.num_kv_heads != 0)
+      return Status::InvalidArgument("num_attention_heads must be divisible by num_key_value_heads");
+    if (c.act_dtype != AM_DT_F32 && c.act_dtype != AM_DT_BF16)
+      return Status::InvalidArgument("act_dtype must be f32 or bf16");
+    if (c.weight_format < AM_WF_F32 || c.weight_format > AM_WF_INT4) return Status::InvalidArgument("bad weight format");
+    if (c.max_tokens <= 0 || c.max_prefill_chunk <= 0) return Status::InvalidArgument("max_tokens/max_prefill_chunk");
+    if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0)) return Status::InvalidArgument("eps/theta must be positive");
+    if (c.weight_format == AM_WF_INT4 && (c.group_size <= 0 || c.hidden % c.group_size || c.ffn % c.group_size ||
+                                          (c.num_q_heads * c.head_dim) % c.group_size))
+      return Status::InvalidArgument("INT4 needs hidden/ffn/q width divisible by group_size");
+    return Status::Ok();
+  }
+
+  static int64_t WBytes(int64_t n, int64_t k, int32_t fmt, int32_t g) {
+    int64_t d = 0, s = 0;
+    (void)am_gfx950_weight_bytes(n, k, fmt, g, &d, &s);
+    return ((d + 255) & ~int64_t{255}) + ((s + 255) & ~int64_t{255});
+  }
+
+  Status AllocWeight(int64_t n, int64_t k, am_gfx950_weight* w) {
+    int64_t d = 0, s = 0;
+    AM_C_OK(am_gfx950_weight_bytes(n, k, cfg.weight_format, cfg.group_size, &d, &s));
+    w->n = n;
+    w->k = k;
+    w->format = cfg.weight_format;
+    w->group_size = cfg.group_size;
+    w->data = slab.Take(static_cast<size_t>(d));
+    w->scales = s > 0 ? slab.Take(static_cast<size_t>(s)) : nullptr;
+    linear_bytes += d + s;
+    return Status::Ok();
+  }
+
+  // Synthesize the logical weight (build SPEC stream of (seed, tensor_id)) into
+  // scratch, then pack/quantize it into rows [row_off, row_off + rows) of dst.
+  Status SynthInto(uint64_t seed, uint64_t tid, int64_t rows, int64_t k, void* scratch, const am_gfx950_weight& dst,
+                   int64_t row_off) {
+    const int32_t sdt = cfg.weight_format == AM_WF_F32 ? AM_DT_F32 : AM_DT_BF16;
+    am_gfx950_synth_args sa{seed, tid, 0.02, 0, rows * k, scratch, sdt};
+    AM_C_OK(am_gfx950_synth_normal(&sa, stream));
+    am_gfx950_quantize_args qa{};
+    qa.src = scratch;
+    qa.src_dtype = sdt;
+    qa.src_rows = rows;
+    qa.dst = dst;
+    qa.dst_row_offset = row_off;
+    qa.dst_row_stride = 1;
+    if (cfg.weight_format >= AM_WF_INT8)
+      AM_C_OK(am_gfx950_quantize(&qa, stream));
+    else
+      AM_C_OK(am_gfx950_pack_plain(&qa, stream));
+    return Status::Ok();
+  }
+
+  Status CreateSynthetic(uint64_t seed) {
+    AM_RETURN_IF_ERROR(Validate());
+    const auto& c = cfg;
+    const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers, d = c.head_dim;
+    const int64_t qkv_rows = QRows() + 2 * KvRows();
+    const int32_t fmt = c.weight_format, g = c.group_size;
+    const size_t ab = ActBytes(c.act_dtype);
+    int64_t total = 0;
+    total += V * H * static_cast<int64_t>(ab) + 256;
+    total += (2 * L + 1) * (H * static_cast<int64_t>(ab) + 256);
+    total += L * (WBytes(qkv_rows, H, fmt, g) + WBytes(H, QRows(), fmt, g) + WBytes(2 * F, H, fmt, g) +
+                  WBytes(H, F, fmt, g));
+    total += WBytes(V, H, fmt, g);
+    total += 2 * (static_cast<int64_t>(c.max_tokens) * (d / 2) * 4 + 256);
+    total += 4096;
+    AM_HIP_OK(hipMalloc(&slab.base, static_cast<size_t>(total)));
+    slab.size = static_cast<size_t>(total);
+
+    embed = slab.Take(static_cast<size_t>(V * H) * ab);
+    in_norm.resize(static_cast<size_t>(L));
+    post_norm.resize(static_cast<size_t>(L));
+    qkv.resize(static_cast<size_t>(L));
+    o.resize(static_cast<size_t>(L));
+    gate_up.resize(static_cast<size_t>(L));
+    down.resize(static_cast<size_t>(L));
+    for (int64_t l = 0; l < L; ++l) {
+      in_norm[l] = slab.Take(static_cast<size_t>(H) * ab);
+      post_norm[l] = slab.Take(static_cast<size_t>(H) * ab);
+      AM_RETURN_IF_ERROR(AllocWeight(qkv_rows, H, &qkv[l]));
+      AM_RETURN_IF_ERROR(AllocWeight(H, QRows(), &o[l]));
+      AM_RETURN_IF_ERROR(AllocWeight(2 * F, H, &gate_up[l]));
+      AM_RETURN_IF_ERROR(AllocWeight(H, F, &down[l]));
+    }
+    final_norm = slab.Take(static_cast<size_t>(H) * ab);
+    AM_RETURN_IF_ERROR(AllocWeight(V, H, &lm_head));
+    cos_tab = static_cast<float*>(slab.Take(static_cast<size_t>(c.max_tokens) * (d / 2) * 4));
+    sin_tab = static_cast<float*>(slab.Take(static_cast<size_t>(c.max_tokens) * (d / 2) * 4));
+    if (slab.off > slab.size) return Status::Internal("weight slab overflow");
+
+    // scratch for one logical source matrix (largest: lm_head / embedding)
+    const int64_t max_elems = std::max({V * H, F * H, QRows() * H});
+    void* scratch = nullptr;
+    AM_HIP_OK(hipMalloc(&scratch, static_cast<size_t>(max_elems) * 4));
+    Status st = [&]() -> Status {
+      am_gfx950_synth_args ea{seed, kEmbedId, 0.02, 0, V * H, embed, c.act_dtype};
+      AM_C_OK(am_gfx950_synth_normal(&ea, stream));
+      for (int64_t l = 0; l < L; ++l) {
+        const int li = static_cast<int>(l);
+        AM_C_OK(am_gfx950_fill(in_norm[l], c.act_dtype, H, 1.0f, stream));
+        AM_C_OK(am_gfx950_fill(post_norm[l], c.act_dtype, H, 1.0f, stream));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRQ), QRows(), H, scratch, qkv[l], 0));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRK), KvRows(), H, scratch, qkv[l], QRows()));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRV), KvRows(), H, scratch, qkv[l], QRows() + KvRows()));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRO), H, QRows(), scratch, o[l], 0));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRGate), F, H, scratch, gate_up[l], 0));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRUp), F, H, scratch, gate_up[l], F));
+        AM_RETURN_IF_ERROR(SynthInto(seed, LayerTensorId(li, kRDown), H, F, scratch, down[l], 0));
+      }
+      AM_C_OK(am_gfx950_fill(final_norm, c.act_dtype, H, 1.0f, stream));
+      AM_RETURN_IF_ERROR(SynthInto(seed, kLmHeadId, V, H, scratch, lm_head, 0));
+      std::vector<float> ct(static_cast<size_t>(c.max_tokens) * (d / 2)), stb(ct.size());
+      AM_C_OK(am_gfx950_rope_table(c.max_tokens, d, c.rope_theta, ct.data(), stb.data()));
+      AM_HIP_OK(hipMemcpyAsync(cos_tab, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, stream));
+      AM_HIP_OK(hipMemcpyAsync(sin_tab, stb.data(), stb.size() * 4, hipMemcpyHostToDevice, stream));
+      AM_HIP_OK(hipStreamSynchronize(stream));
+      return Status::Ok();
+    }();
+    (void)hipFree(scratch);
+    return st;
+  }
+};
+
+// ------------------------------------------------------------------ session
+class LlamaSession {
+ public:
+  LlamaModel* m = nullptr;
+  hipStream_t stream = nullptr;
+  std::unique_ptr<HipStream> hs;
+  BackendRegistry backends;
+  Backend* backend = nullptr;
+  KVCacheManager kv;
+  KVCacheView view;
+  am_session_options opt{1, 1};
+
+  // device buffers
+  void* act_slab = nullptr;
+  int64_t* ids = nullptr;
+  int64_t* positions = nullptr;
+  void *h = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *tmp = nullptr;
+  void *gate = nullptr, *up = nullptr, *act = nullptr;
+  float* logits = nullptr;
+  int64_t* state = nullptr;  // [0] token, [1] pos, [2] step, [3..] unused
+  int64_t* hist = nullptr;   // [max_tokens]
+  int32_t* err = nullptr;
+  void* attn_ws = nullptr;
+  size_t attn_ws_bytes = 0;
+  void* lm_ws = nullptr;
+  void* am_ws = nullptr;
+  int64_t am_ws_bytes = 0;
+
+  // decode plan
+  std::unique_ptr<ExecutionPlan> decode_plan;
+  RuntimeBindingContext decode_bind;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  int64_t host_pos = 0;   // mirrors state[1] after each host-visible sync point
+  int64_t host_step = 0;  // number of tokens generated in the current sequence
+
+  ~LlamaSession() {
+    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (act_slab) (void)hipFree(act_slab);
+  }
+
+  int64_t* token_ptr() const { return state; }
+  int64_t* pos_ptr() const { return state + 1; }
+  int64_t* step_ptr() const { return state + 2; }
+
+  Status Init(LlamaModel* model, const am_session_options* o) {
+    m = model;
+    stream = model->stream;
+    hs = std::make_unique<HipStream>(stream);
+    if (o) opt = *o;
+    AM_RETURN_IF_ERROR(backends.RegisterFactory(std::make_unique<gfx950::Gfx950BackendFactory>()));
+    auto b = backends.GetBackend(DeviceType::kHIP);
+    if (!b.ok()) return b.status();
+    backend = b.value();
+    (void)am::DeviceCUs();
+
+    const auto& c = m->cfg;
+    AM_RETURN_IF_ERROR(kv.Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype)));
+    auto vw = kv.ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+    if (!vw.ok()) return vw.status();
+    view = vw.value();
+
+    const int64_t S = c.max_prefill_chunk, H = c.hidden, F = c.ffn;
+    const size_t ab = ActBytes(c.act_dtype);
+    attn_ws_bytes = static_cast<size_t>(std::max(
+        am_gfx950_attention_workspace_bytes(1, S, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0),
+        am_gfx950_attention_workspace_bytes(1, 1, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0)));
+    am_ws_bytes = am_gfx950_argmax_workspace_bytes(1);
+    const size_t sizes[] = {
+        static_cast<size_t>(S) * 8,                   // ids
+        static_cast<size_t>(S) * 8,                   // positions
+        static_cast<size_t>(S * H) * ab,              // h
+        static_cast<size_t>(S * H) * ab,              // xn
+        static_cast<size_t>(S * m->QRows()) * ab,     // q
+        static_cast<size_t>(S * m->KvRows()) * ab,    // k
+        static_cast<size_t>(S * m->KvRows()) * ab,    // v
+        static_cast<size_t>(S * m->QRows()) * ab,     // attn
+        static_cast<size_t>(S * H) * ab,              // tmp
+        static_cast<size_t>(S * F) * ab,              // gate
+        static_cast<size_t>(S * F) * ab,              // up
+        static_cast<size_t>(S * F) * ab,              // act
+        static_cast<size_t>(c.vocab) * 4,             // logits
+        64,                                           // state
+        static_cast<size_t>(c.max_tokens + 1) * 8,    // hist
+        64,                                           // err
+        attn_ws_bytes,                                // attention workspace
+        static_cast<size_t>(am_gfx950_lm_head_workspace_bytes()),
+        static_cast<size_t>(am_ws_bytes)};
+    size_t total = 0;
+    for (size_t s : sizes) total += (s + 255) & ~size_t{255};
+    AM_HIP_OK(hipMalloc(&act_slab, total));
+    AM_HIP_OK(hipMemsetAsync(act_slab, 0, total, stream));
+    Slab sl{act_slab, total, 0};
+    void* ptrs[19];
+    for (int i = 0; i < 19; ++i) ptrs[i] = sl.Take(sizes[i]);
+    ids = static_cast<int64_t*>(ptrs[0]);
+    positions = static_cast<int64_t*>(ptrs[1]);
+    h = ptrs[2];
+    xn = ptrs[3];
+    q = ptrs[4];
+    k = ptrs[5];
+    v = ptrs[6];
+    attn = ptrs[7];
+    tmp = ptrs[8];
+    gate = ptrs[9];
+    up = ptrs[10];
+    act = ptrs[11];
+    logits = static_cast<float*>(ptrs[12]);
+    state = static_cast<int64_t*>(ptrs[13]);
+    hist = static_cast<int64_t*>(ptrs[14]);
+    err = static_cast<int32_t*>(ptrs[15]);
+    attn_ws = ptrs[16];
+    lm_ws = ptrs[17];
+    am_ws = ptrs[18];
+    decode_bind.SetStream(hs.get());
+    decode_bind.SetWorkspace(attn_ws, attn_ws_bytes);
+    AM_HIP_OK(hipStreamSynchronize(stream));
+    return BuildDecodePlan();
+  }
+
+  // ---------------------------------------------------------------- plan building
+  struct Builder {
+    LlamaSession* s;
+    ExecPhase phase;
+    std::vector<ExecutionStep> steps;
+    RuntimeBindingContext* bind;
+
+    Status Add(OpType op, std::vector<std::byte> attrs, KernelSelector sel, const void* packed,
+               std::vector<TensorView> ins, std::vector<MutableTensorView> outs, size_t ws_bytes = 0) {
+      auto opr = std::make_shared<DeviceOperator>(op, std::move(attrs));
+      AM_RETURN_IF_ERROR(opr->Prepare(*s->backend, sel));
+      ExecutionStep st;
+      st.selector = sel;
+      st.op = opr;
+      st.packed_weights = packed;
+      st.workspace_bytes = ws_bytes;
+      st.debug_name = opr->GetResolvedKernel().debug_name;
+      bind->SetStepTensorBinding(steps.size(), StepTensorBinding{std::move(ins), std::move(outs)});
+      steps.push_back(std::move(st));
+      return Status::Ok();
+    }
+  };
+
+  KernelSelector Sel(bool linear, ExecPhase ph) const {
+    const DataType a = ActType(m->cfg.act_dtype);
+    if (linear) return HipSelector(a, WeightDType(m->cfg.weight_format), SelFormat(m->cfg.weight_format), ph);
+    return HipSelector(a, a, WeightFormat::kPlain, ph);
+  }
+
+  // Unfused per-layer body (reference node order) for `S` rows starting at device
+  // position *start (positions[] holds per-row positions).
+  Status AddLayerUnfused(Builder& b, int64_t l, int64_t S, ExecPhase ph, const int64_t* pos_rows,
+                         const int64_t* start) {
+    const auto& c = m->cfg;
+    const DataType A = ActType(c.act_dtype);
+    const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, Q = m->QRows(), KV = m->KvRows();
+    auto kp = view.KeyPlane(static_cast<size_t>(l));
+    auto vp = view.ValuePlane(static_cast<size_t>(l));
+    if (!kp.ok()) return kp.status();
+    if (!vp.ok()) return vp.status();
+    const gfx950::NormAttrs na{c.rms_eps};
+    auto& W = s_views[static_cast<size_t>(l)];
+    const TensorView hv(h, A, {S, H}), xnv(xn, A, {S, H});
+    AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
+                             {hv, TensorView(m->in_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.q, {xnv}, {MutableTensorView(q, A, {S, Q})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.k, {xnv}, {MutableTensorView(k, A, {S, KV})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.v, {xnv}, {MutableTensorView(v, A, {S, KV})}));
+    const gfx950::RopeAttrs ra{c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
+    AM_RETURN_IF_ERROR(b.Add(OpType::kRoPE, PackAttrs(ra), Sel(false, ph), nullptr,
+                             {TensorView(q, A, {S, Q}), TensorView(k, A, {S, KV}),
+                              TensorView(pos_rows, DataType::Int(64), {S}),
+                              TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+                              TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2})},
+                             {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV})}));
+    const gfx950::KvAttrs ka{c.num_kv_heads, d, c.max_tokens};
+    const TensorView kplane(kp.value(), A, {c.num_kv_heads, c.max_tokens, d});
+    const TensorView vplane(vp.value(), A, {c.num_kv_heads, c.max_tokens, d});
+    AM_RETURN_IF_ERROR(b.Add(OpType::kKVCacheUpdate, PackAttrs(ka), Sel(false, ph), nullptr,
+                             {TensorView(k, A, {S, KV}), TensorView(v, A, {S, KV}), kplane, vplane,
+                              TensorView(start, DataType::Int(64), {1})},
+                             {}));
+    const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0};
+    AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
+                             {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},
+                             {MutableTensorView(attn, A, {S, Q})}, attn_ws_bytes));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
+                             {MutableTensorView(tmp, A, {S, H})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kAdd, {}, Sel(false, ph), nullptr, {hv, TensorView(tmp, A, {S, H})},
+                             {MutableTensorView(h, A, {S, H})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
+                             {hv, TensorView(m->post_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.gate, {xnv}, {MutableTensorView(gate, A, {S, F})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.up, {xnv}, {MutableTensorView(up, A, {S, F})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kSiluMul, {}, Sel(false, ph), nullptr,
+                             {TensorView(gate, A, {S, F}), TensorView(up, A, {S, F})},
+                             {MutableTensorView(act, A, {S, F})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {S, F})},
+                             {MutableTensorView(tmp, A, {S, H})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kAdd, {}, Sel(false, ph), nullptr, {hv, TensorView(tmp, A, {S, H})},
+                             {MutableTensorView(h, A, {S, H})}));
+    return Status::Ok();
+  }
+
+  // RmsNorm(final) -> Linear lm_head (fp32 logits) -> Argmax (+ advance decode state)
+  // on the row `row` of h.
+  Status AddHeadUnfused(Builder& b, int64_t row, ExecPhase ph) {
+    const auto& c = m->cfg;
+    const DataType A = ActType(c.act_dtype);
+    const int64_t H = c.hidden;
+    const size_t ab = ActBytes(c.act_dtype);
+    void* hrow = static_cast<char*>(h) + static_cast<size_t>(row * H) * ab;
+    const gfx950::NormAttrs na{c.rms_eps};
+    AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
+                             {TensorView(hrow, A, {1, H}), TensorView(m->final_norm, A, {H})},
+                             {MutableTensorView(xn, A, {1, H})}));
+    // lm_head GEMV for one row (decode-phase kernel: GEMV) with fp32 logits out.
+    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ExecPhase::kDecode), &m->lm_head,
+                             {TensorView(xn, A, {1, H})},
+                             {MutableTensorView(logits, DataType::Float32(), {1, c.vocab})}));
+    AM_RETURN_IF_ERROR(b.Add(OpType::kArgmax, {}, Sel(false, ph), nullptr,
+                             {TensorView(logits, DataType::Float32(), {1, c.vocab}),
+                              TensorView(am_ws, DataType::UInt(8), {am_ws_bytes})},
+                             {MutableTensorView(token_ptr(), DataType::Int(64), {1}),
+                              MutableTensorView(hist, DataType::Int(64), {c.max_tokens}),
+                              MutableTensorView(pos_ptr(), DataType::Int(64), {1}),
+                              MutableTensorView(step_ptr(), DataType::Int(64), {1})}));
+    return Status::Ok();
+  }
+
+  struct LayerViews {
+    am_gfx950_weight q, k, v, gate, up;
+  };
+  std::vector<LayerViews> s_views;
+
+  void MakeViews() {
+    const int64_t L = m->cfg.num_layers, Q = m->QRows(), KV = m->KvRows(), F = m->cfg.ffn;
+    s_views.resize(static_cast<size_t>(L));
+    for (int64_t l = 0; l < L; ++l) {
+      auto& w = s_views[static_cast<size_t>(l)];
+      w.q = m->RowView(m->qkv[l], 0, Q);
+      w.k = m->RowView(m->qkv[l], Q, KV);
+      w.v = m->RowView(m->qkv[l], Q + KV, KV);
+      w.gate = m->RowView(m->gate_up[l], 0, F);
+      w.up = m->RowView(m->gate_up[l], F, F);
+    }
+  }
+
+  Status BuildDecodePlan() {
+    MakeViews();
+    const auto& c = m->cfg;
+    const DataType A = ActType(c.act_dtype);
+    const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, Q = m->QRows();
+    decode_bind.ClearStepTensorBindings();
+    Builder b{this, ExecPhase::kDecode, {}, &decode_bind};
+    const auto ph = ExecPhase::kDecode;
+    AM_RETURN_IF_ERROR(b.Add(OpType::kEmbedToken, {}, Sel(false, ph), nullptr,
+                             {TensorView(token_ptr(), DataType::Int(64), {1}), TensorView(m->embed, A, {c.vocab, H}),
+                              TensorView(err, DataType::Int(32), {1})},
+                             {MutableTensorView(h, A, {1, H})}));
+    for (int64_t l = 0; l < c.num_layers; ++l) {
+      if (!opt.fused_decode) {
+        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, 1, ph, pos_ptr(), pos_ptr()));
+        continue;
+      }
+      auto kp = view.KeyPlane(static_cast<size_t>(l));
+      auto vp = view.ValuePlane(static_cast<size_t>(l));
+      if (!kp.ok()) return kp.status();
+      if (!vp.ok()) return vp.status();
+      const TensorView kplane(kp.value(), A, {c.num_kv_heads, c.max_tokens, d});
+      const TensorView vplane(vp.value(), A, {c.num_kv_heads, c.max_tokens, d});
+      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormQkvRoPEKVUpdate, PackAttrs(qa), Sel(true, ph), &m->qkv[l],
+                               {TensorView(h, A, {1, H}), TensorView(m->in_norm[l], A, {H}),
+                                TensorView(pos_ptr(), DataType::Int(64), {1}),
+                                TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+                                TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2}), kplane, vplane},
+                               {MutableTensorView(q, A, {1, Q})}));
+      const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
+                               {TensorView(q, A, {1, Q}), kplane, vplane, TensorView(pos_ptr(), DataType::Int(64), {1})},
+                               {MutableTensorView(attn, A, {1, Q})}, attn_ws_bytes));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {1, Q})},
+                               {MutableTensorView(h, A, {1, H})}));
+      const gfx950::NormAttrs na{c.rms_eps};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormGateUpSiluMul, PackAttrs(na), Sel(true, ph), &m->gate_up[l],
+                               {TensorView(h, A, {1, H}), TensorView(m->post_norm[l], A, {H})},
+                               {MutableTensorView(act, A, {1, F})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {1, F})},
+                               {MutableTensorView(h, A, {1, H})}));
+    }
+    if (opt.fused_decode) {
+      const gfx950::NormAttrs na{c.rms_eps};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormLmHeadArgmax, PackAttrs(na), Sel(true, ph), &m->lm_head,
+                               {TensorView(h, A, {1, H}), TensorView(m->final_norm, A, {H}),
+                                TensorView(lm_ws, DataType::UInt(8), {am_gfx950_lm_head_workspace_bytes()})},
+                               {MutableTensorView(logits, DataType::Float32(), {c.vocab}),
+                                MutableTensorView(token_ptr(), DataType::Int(64), {1}),
+                                MutableTensorView(hist, DataType::Int(64), {c.max_tokens}),
+                                MutableTensorView(pos_ptr(), DataType::Int(64), {1}),
+                                MutableTensorView(step_ptr(), DataType::Int(64), {1})}));
+    } else {
+      AM_RETURN_IF_ERROR(AddHeadUnfused(b, 0, ph));
+    }
+    auto plan = ExecutionPlan::Create(std::move(b.steps));
+    if (!plan.ok()) return plan.status();
+    decode_plan = std::make_unique<ExecutionPlan>(std::move(plan.value()));
+    return Status::Ok();
+  }
+
+  // ---------------------------------------------------------------- execution
+  Status Prefill(const int64_t* prompt, int64_t n, int64_t* first_token) {
+    const auto& c = m->cfg;
+    if (n <= 0) return Status::InvalidArgument("prompt must contain at least one token");
+    if (n + 1 > c.max_tokens) return Status::OutOfRange("KV session reservation exceeds physical KV capacity");
+    for (int64_t i = 0; i < n; ++i)
+      if (prompt[i] < 0 || prompt[i] >= c.vocab) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
+    AM_RETURN_IF_ERROR(kv.ReleaseSession(view));
+    auto vw = kv.ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+    if (!vw.ok()) return vw.status();
+    view = vw.value();
+    if (graph_exec) {  // KV planes are unchanged (same slab), the graph stays valid
+    }
+    const int64_t chunk = c.max_prefill_chunk;
+    std::vector<int64_t> pos_host(static_cast<size_t>(chunk));
+    for (int64_t p0 = 0; p0 < n; p0 += chunk) {
+      const int64_t S = std::min(chunk, n - p0);
+      for (int64_t i = 0; i < S; ++i) pos_host[static_cast<size_t>(i)] = p0 + i;
+      AM_HIP_OK(hipMemcpyAsync(ids, prompt + p0, static_cast<size_t>(S) * 8, hipMemcpyHostToDevice, stream));
+      AM_HIP_OK(hipMemcpyAsync(positions, pos_host.data(), static_cast<size_t>(S) * 8, hipMemcpyHostToDevice, stream));
+      RuntimeBindingContext bind;
+      bind.SetStream(hs.get());
+      bind.SetWorkspace(attn_ws, attn_ws_bytes);
+      Builder b{this, ExecPhase::kPrefill, {}, &bind};
+      const DataType A = ActType(c.act_dtype);
+      AM_RETURN_IF_ERROR(b.Add(OpType::kEmbedding, {}, Sel(false, ExecPhase::kPrefill), nullptr,
+                               {TensorView(ids, DataType::Int(64), {S}), TensorView(m->embed, A, {c.vocab, c.hidden}),
+                                TensorView(err, DataType::Int(32), {1})},
+                               {MutableTensorView(h, A, {S, c.hidden})}));
+      for (int64_t l = 0; l < c.num_layers; ++l)
+        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, S, ExecPhase::kPrefill, positions, positions));
+      const bool last = p0 + S == n;
+      if (last) {
+        // decode state before the head: pos = n-1, step = 0 (the head advances both)
+        const int64_t st[3] = {0, n - 1, 0};
+        AM_HIP_OK(hipMemcpyAsync(state, st, sizeof(st), hipMemcpyHostToDevice, stream));
+        AM_RETURN_IF_ERROR(AddHeadUnfused(b, S - 1, ExecPhase::kPrefill));
+      }
+      auto plan = ExecutionPlan::Create(std::move(b.steps));
+      if (!plan.ok()) return plan.status();
+      AM_RETURN_IF_ERROR(Executor::Execute(plan.value(), bind));
+      AM_HIP_OK(hipStreamSynchronize(stream));  // pos_host / state staging reuse
+    }
+    AM_RETURN_IF_ERROR(view.CommitUntil(static_cast<size_t>(n)));
+    int64_t tok = 0;
+    AM_HIP_OK(hipMemcpy(&tok, token_ptr(), 8, hipMemcpyDeviceToHost));
+    int32_t e = 0;
+    AM_HIP_OK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
+    if (e != 0) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
+    host_pos = n;
+    host_step = 1;
+    if (first_token) *first_token = tok;
+    return Status::Ok();
+  }
+
+  Status EnqueueDecode(int64_t n) {
+    const auto& c = m->cfg;
+    if (host_step == 0) return Status::FailedPrecondition("decode requires a prefilled session");
+    if (host_pos + n > c.max_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
+    if (opt.use_graph) {
+      if (!graph_exec) {
+        AM_HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
+        Status st = Executor::Execute(*decode_plan, decode_bind);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(stream, &g);
+        if (!st.ok()) {
+          if (g) (void)hipGraphDestroy(g);
+          return st;
+        }
+        if (e != hipSuccess) return Status::Internal(std::string("graph capture failed: ") + hipGetErrorString(e));
+        graph = g;
+        AM_HIP_OK(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
+      }
+      for (int64_t i = 0; i < n; ++i) AM_HIP_OK(hipGraphLaunch(graph_exec, stream));
+    } else {
+      for (int64_t i = 0; i < n; ++i) AM_RETURN_IF_ERROR(Executor::Execute(*decode_plan, decode_bind));
+    }
+    host_pos += n;
+    AM_RETURN_IF_ERROR(view.CommitUntil(static_cast<size_t>(host_pos)));
+    return Status::Ok();
+  }
+
+  Status Decode(int64_t n, int64_t* out) {
+    const int64_t first_step = host_step;
+    AM_RETURN_IF_ERROR(EnqueueDecode(n));
+    host_step += n;
+    if (out) AM_HIP_OK(hipMemcpyAsync(out, hist + first_step, static_cast<size_t>(n) * 8, hipMemcpyDeviceToHost, stream));
+    AM_HIP_OK(hipStreamSynchronize(stream));
+    int32_t e = 0;
+    AM_HIP_OK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
+    if (e != 0) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
+    return Status::Ok();
+  }
+
+  Status Profile(int64_t n, double* ms_by_op, int64_t* count_by_op) {
+    if (host_step == 0) return Status::FailedPrecondition("decode requires a prefilled session");
+    if (host_pos + n > m->cfg.max_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
+    const auto& steps = decode_plan->steps();
+    std::vector<hipEvent_t> ev(steps.size() + 1);
+    for (auto& e : ev) AM_HIP_OK(hipEventCreate(&e));
+    Status st;
+    for (int64_t it = 0; it < n && st.ok(); ++it) {
+      AM_HIP_OK(hipEventRecord(ev[0], stream));
+      for (size_t i = 0; i < steps.size() && st.ok(); ++i) {
+        st = LayerRunner::RunStep(i, steps[i], decode_bind);
+        (void)hipEventRecord(ev[i + 1], stream);
+      }
+      if (!st.ok()) break;
+      AM_HIP_OK(hipEventSynchronize(ev[steps.size()]));
+      for (size_t i = 0; i < steps.size(); ++i) {
+        float ms = 0.f;
+        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+        const int op = static_cast<int>(steps[i].op->Type());
+        if (op < 64) {
+          ms_by_op[op] += ms;
+          count_by_op[op] += 1;
+        }
+      }
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    if (st.ok()) {
+      host_pos += n;
+      host_step += n;
+      st = view.CommitUntil(static_cast<size_t>(host_pos));
+    }
+    return st;
+  }
+};
+
+}  // namespace aethermind::llama
+
+// ------------------------------------------------------------------ C ABI
+using aethermind::Status;
+using aethermind::llama::LlamaModel;
+using aethermind::llama::LlamaSession;
+
+struct am_runtime {
+  int device = 0;
+  hipStream_t stream = nullptr;
+};
+struct am_model {
+  am_runtime* rt = nullptr;
+  std::unique_ptr<LlamaModel> impl;
+};
+struct am_session {
+  std::unique_ptr<LlamaSession> impl;
+};
+
+namespace {
+am_status_code Ret(const Status& s) {
+  if (s.ok()) return AM_STATUS_OK;
+  return am::SetLastError(s.c_code(), s.message().c_str());
+}
+}  // namespace
+
+extern "C" {
+
+am_status_code am_runtime_create(int32_t device, am_runtime** out) {
+  if (out == nullptr) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "runtime: null out");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return am::SetLastError(AM_STATUS_UNAVAILABLE, "no HIP device available");
+  if (device < 0 || device >= n) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "runtime: bad device index");
+  if (hipSetDevice(device) != hipSuccess) return am::SetLastError(AM_STATUS_INTERNAL, "hipSetDevice failed");
+  auto* rt = new am_runtime();
+  rt->device = device;
+  if (hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete rt;
+    return am::SetLastError(AM_STATUS_INTERNAL, "hipStreamCreate failed");
+  }
+  *out = rt;
+  return AM_STATUS_OK;
+}
+
+void am_runtime_destroy(am_runtime* rt) {
+  if (!rt) return;
+  (void)hipStreamSynchronize(rt->stream);
+  (void)hipStreamDestroy(rt->stream);
+  delete rt;
+}
+
+void* am_runtime_stream(am_runtime* rt) { return rt ? rt->stream : nullptr; }
+
+am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* cfg, uint64_t seed, am_model** out) {
+  if (!rt || !cfg || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model: null argument");
+  auto m = std::make_unique<am_model>();
+  m->rt = rt;
+  m->impl = std::make_unique<LlamaModel>();
+  m->impl->cfg = *cfg;
+  m->impl->stream = rt->stream;
+  const Status s = m->impl->CreateSynthetic(seed);
+  if (!s.ok()) return Ret(s);
+  *out = m.release();
+  return AM_STATUS_OK;
+}
+
+void am_model_destroy(am_model* m) {
+  if (!m) return;
+  (void)hipStreamSynchronize(m->rt->stream);
+  delete m;
+}
+
+int64_t am_model_weight_bytes_total(am_model* m) { return m ? m->impl->linear_bytes : 0; }
+
+am_status_code am_model_weight(am_model* m, int32_t layer, int32_t role, am_gfx950_weight* out) {
+  if (!m || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_weight: null argument");
+  LlamaModel& M = *m->impl;
+  if (role != AM_ROLE_LM_HEAD && (layer < 0 || layer >= M.cfg.num_layers))
+    return am::SetLastError(AM_STATUS_OUT_OF_RANGE, "model_weight: layer out of range");
+  const int64_t Q = M.QRows(), KV = M.KvRows(), F = M.cfg.ffn;
+  const size_t l = static_cast<size_t>(layer);
+  switch (role) {
+    case AM_ROLE_QKV: *out = M.qkv[l]; break;
+    case AM_ROLE_O: *out = M.o[l]; break;
+    case AM_ROLE_GATE_UP: *out = M.gate_up[l]; break;
+    case AM_ROLE_DOWN: *out = M.down[l]; break;
+    case AM_ROLE_LM_HEAD: *out = M.lm_head; break;
+    case AM_ROLE_Q: *out = M.RowView(M.qkv[l], 0, Q); break;
+    case AM_ROLE_K: *out = M.RowView(M.qkv[l], Q, KV); break;
+    case AM_ROLE_V: *out = M.RowView(M.qkv[l], Q + KV, KV); break;
+    case AM_ROLE_GATE: *out = M.RowView(M.gate_up[l], 0, F); break;
+    case AM_ROLE_UP: *out = M.RowView(M.gate_up[l], F, F); break;
+    default: return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_weight: unknown role");
+  }
+  return AM_STATUS_OK;
+}
+
+am_status_code am_model_buffer(am_model* m, int32_t kind, int32_t layer, void** ptr, int64_t* bytes) {
+  if (!m || !ptr || !bytes) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_buffer: null argument");
+  LlamaModel& M = *m->impl;
+  const int64_t ab = M.cfg.act_dtype == AM_DT_BF16 ? 2 : 4;
+  const int64_t H = M.cfg.hidden;
+  const bool per_layer = kind == AM_BUF_IN_NORM || kind == AM_BUF_POST_NORM;
+  if (per_layer && (layer < 0 || layer >= M.cfg.num_layers))
+    return am::SetLastError(AM_STATUS_OUT_OF_RANGE, "model_buffer: layer out of range");
+  switch (kind) {
+    case AM_BUF_EMBED: *ptr = M.embed; *bytes = static_cast<int64_t>(M.cfg.vocab) * H * ab; break;
+    case AM_BUF_IN_NORM: *ptr = M.in_norm[static_cast<size_t>(layer)]; *bytes = H * ab; break;
+    case AM_BUF_POST_NORM: *ptr = M.post_norm[static_cast<size_t>(layer)]; *bytes = H * ab; break;
+    case AM_BUF_FINAL_NORM: *ptr = M.final_norm; *bytes = H * ab; break;
+    case AM_BUF_ROPE_COS: *ptr = M.cos_tab; *bytes = static_cast<int64_t>(M.cfg.max_tokens) * (M.cfg.head_dim / 2) * 4; break;
+    case AM_BUF_ROPE_SIN: *ptr = M.sin_tab; *bytes = static_cast<int64_t>(M.cfg.max_tokens) * (M.cfg.head_dim / 2) * 4; break;
+    default: return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_buffer: unknown kind");
+  }
+  return AM_STATUS_OK;
+}
+
+am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out) {
+  if (!m || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "session: null argument");
+  auto s = std::make_unique<am_session>();
+  s->impl = std::make_unique<LlamaSession>();
+  const Status st = s->impl->Init(m->impl.get(), opt);
+  if (!st.ok()) return Ret(st);
+  *out = s.release();
+  return AM_STATUS_OK;
+}
+
+void am_session_destroy(am_session* s) {
+  if (!s) return;
+  (void)hipStreamSynchronize(s->impl->stream);
+  delete s;
+}
+
+am_status_code am_session_prefill(am_session* s, const int64_t* prompt, int64_t n, int64_t* first_token) {
+  if (!s || !prompt) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "prefill: null argument");
+  return Ret(s->impl->Prefill(prompt, n, first_token));
+}
+
+am_status_code am_session_decode(am_session* s, int64_t n, int64_t* tokens_out) {
+  if (!s || n < 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "decode: bad argument");
+  if (n == 0) return AM_STATUS_OK;
+  return Ret(s->impl->Decode(n, tokens_out));
+}
+
+am_status_code am_session_decode_async(am_session* s, int64_t n) {
+  if (!s || n < 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "decode_async: bad argument");
+  const Status st = s->impl->EnqueueDecode(n);
+  if (st.ok()) s->impl->host_step += n;
+  return Ret(st);
+}
+
+am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new, int64_t eos,
+                                   int64_t* tokens_out, int64_t* n_out) {
+  if (!s || !prompt || !tokens_out || max_new <= 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "generate: bad argument");
+  int64_t first = 0;
+  Status st = s->impl->Prefill(prompt, n_prompt, &first);
+  if (!st.ok()) return Ret(st);
+  tokens_out[0] = first;
+  int64_t produced = 1;
+  // EOS is checked every `chunk` steps: decode runs ahead without per-token syncs.
+  const int64_t chunk = 16;
+  while (produced < max_new && (eos < 0 || tokens_out[produced - 1] != eos)) {
+    const int64_t n = std::min(chunk, max_new - produced);
+    st = s->impl->Decode(n, tokens_out + produced);
+    if (!st.ok()) return Ret(st);
+    int64_t keep = n;
+    if (eos >= 0)
+      for (int64_t i = 0; i < n; ++i)
+        if (tokens_out[produced + i] == eos) {
+          keep = i + 1;
+          break;
+        }
+    produced += keep;
+    if (keep < n) break;
+  }
+  if (n_out) *n_out = produced;
+  return AM_STATUS_OK;
+}
+
+am_status_code am_session_logits(am_session* s, float* out) {
+  if (!s || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "logits: null argument");
+  auto& S = *s->impl;
+  if (hipStreamSynchronize(S.stream) != hipSuccess ||
+      hipMemcpy(out, S.logits, static_cast<size_t>(S.m->cfg.vocab) * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return am::SetLastError(AM_STATUS_INTERNAL, "logits copy failed");
+  return AM_STATUS_OK;
+}
+
+int64_t am_session_position(am_session* s) { return s ? s->impl->host_pos : -1; }
+
+int64_t am_session_decode_plan_size(am_session* s) {
+  return s && s->impl->decode_plan ? static_cast<int64_t>(s->impl->decode_plan->size()) : 0;
+}
+
+am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by_op, int64_t* count_by_op) {
+  if (!s || !ms_by_op || !count_by_op || n <= 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "profile: bad argument");
+  return Ret(s->impl->Profile(n, ms_by_op, count_by_op));
+}
+
+}  // extern "C"

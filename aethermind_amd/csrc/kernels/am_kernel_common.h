@@ -1,0 +1,88 @@
+// Shared device helpers and host-side launch utilities for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "am_gfx950.h"
+
+namespace am {
+
+// ---- host: error reporting (defined in host/c_api.cpp) ----
+am_status_code SetLastError(am_status_code code, const char* msg);
+
+#define AM_CHECK_ARG(cond, msg)                                              \
+  do {                                                                       \
+    if (!(cond)) return ::am::SetLastError(AM_STATUS_INVALID_ARGUMENT, msg); \
+  } while (0)
+
+#define AM_RETURN_IF_LAUNCH_FAILED(what)                                                 \
+  do {                                                                                   \
+    hipError_t e_ = hipGetLastError();                                                   \
+    if (e_ != hipSuccess) return ::am::SetLastError(AM_STATUS_INTERNAL, hipGetErrorString(e_)); \
+  } while (0)
+
+inline hipStream_t AsStream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Number of compute units of the current device (cached per device).
+int DeviceCUs();
+
+// ---- device: numeric helpers ----
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// float -> bf16 round-to-nearest-even, NaN -> 0x7FC0 (the reference's conversion,
+// bfloat16.cpp:20-32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+  const uint32_t x = __float_as_uint(v);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return static_cast<uint16_t>((x + (((x >> 16) & 1u) + 0x7FFFu)) >> 16);
+}
+
+struct ActF32 {
+  using T = float;
+  static constexpr int kDtype = AM_DT_F32;
+  __device__ static __forceinline__ float load(const T* p, int64_t i) { return p[i]; }
+  __device__ static __forceinline__ void store(T* p, int64_t i, float v) { p[i] = v; }
+  __device__ static __forceinline__ float round(float v) { return v; }
+};
+
+struct ActBF16 {
+  using T = uint16_t;
+  static constexpr int kDtype = AM_DT_BF16;
+  __device__ static __forceinline__ float load(const T* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  __device__ static __forceinline__ void store(T* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+  __device__ static __forceinline__ float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Sum over a 256-thread block; every thread gets the result.  `red` holds >= 4 floats.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// Argmax tie rule (build SPEC): larger value wins; equal values -> lower index;
+// NaN never wins.  (v, i) is "better" than (bv, bi)?
+__device__ __forceinline__ bool argmax_better(float v, int64_t i, float bv, int64_t bi) {
+  if (v != v) return false;
+  if (bi < 0) return true;
+  return v > bv || (v == bv && i < bi);
+}
+
+}  // namespace am

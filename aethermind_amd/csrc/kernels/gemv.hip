@@ -1,0 +1,557 @@
+// Decode-time (m = 1) weight-only GEMV for gfx950, HBM-bound.
+//
+// Layout of one launch:
+//   * 256-thread blocks (4 wave64s).  The block stages the activation vector x (K
+//     values) in LDS once, optionally applying the fused RMSNorm prologue, plus the
+//     per-32-k partial sums of x used to undo the weight offset encoding.
+//   * Work unit = 2 output rows.  Each wave takes units u = gw, gw+TW, ... and reads
+//     both rows with all 64 lanes: lane l owns the 16-byte chunks l, l+64, ... of a
+//     row, so every load instruction of the wave covers 1 KiB of contiguous weights
+//     (fully coalesced 128-bit loads).  Up to 4 chunk-steps x 2 rows are issued
+//     before any arithmetic to keep bytes in flight.
+//   * Unpack is in registers: INT4 nibbles hold q+8, and (word >> 4t) & 0x000F000F
+//     | 0x43004300 is the bf16 pair (136+q_even, 136+q_odd), fed to
+//     v_dot2c_f32_bf16 with the bf16 activations; sum(x*(136+q)) - 136*sum(x) gives
+//     sum(x*q) in fp32.  INT8 bytes hold q+128 and go through byte->float converts.
+//   * The two row sums are reduced across the wave with xor shuffles; the epilogue
+//     applies the reference op-boundary roundings of whatever nodes were fused.
+
+#include <cmath>
+
+#include "am_kernel_common.h"
+
+namespace am {
+namespace {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+enum Epi { kEpiStore = 0, kEpiResidual = 1, kEpiQkv = 2, kEpiGateUp = 3, kEpiLmHead = 4 };
+
+struct GemvArgs {
+  const void* x;
+  const void* norm_w;
+  float eps;
+  const uint8_t* w;
+  const void* scales;
+  int64_t n, k;
+  int32_t group;
+  int64_t units;
+  int64_t row_bytes;
+  void* out;
+  const void* residual;
+  const float* cos_tab;
+  const float* sin_tab;
+  const int64_t* pos;
+  void* q_out;
+  void* k_cache;
+  void* v_cache;
+  int32_t hq, hkv, d;
+  int64_t cap;
+  int64_t* token_out;
+  int64_t* tokens_hist;
+  int64_t* pos_inc;
+  int64_t* step;
+  unsigned* ticket;
+  float* pv;
+  int64_t* pi;
+  int32_t out_f32;
+};
+
+constexpr int kJB = 4;  // chunk-steps issued together
+
+// k values per 16-byte chunk of a weight row
+template <int WF> struct Fmt;
+template <> struct Fmt<AM_WF_F32> { static constexpr int kc = 4; static constexpr float off = 0.0f; };
+template <> struct Fmt<AM_WF_BF16> { static constexpr int kc = 8; static constexpr float off = 0.0f; };
+template <> struct Fmt<AM_WF_INT8> { static constexpr int kc = 16; static constexpr float off = 128.0f; };
+template <> struct Fmt<AM_WF_INT4> { static constexpr int kc = 32; static constexpr float off = 8.0f; };
+
+// LDS holds x as bf16 only where the dot uses v_dot2c_f32_bf16 (bf16 act with
+// bf16 or INT4 weights); elsewhere as fp32.
+template <class A, int WF> struct XStore {
+  static constexpr bool kBF16 = A::kDtype == AM_DT_BF16 && (WF == AM_WF_INT4 || WF == AM_WF_BF16);
+  static constexpr int kBytes = kBF16 ? 2 : 4;
+  // effective offset subtracted per chunk: the bf16 INT4 path adds the 128 exponent bias
+  static constexpr float kOff = (kBF16 && WF == AM_WF_INT4) ? 136.0f : Fmt<WF>::off;
+};
+
+__device__ __forceinline__ bf16x2_t as_bf2(uint32_t u) { return __builtin_bit_cast(bf16x2_t, u); }
+
+// Dot of one 16-byte weight chunk with the matching x values in LDS (chunk c).
+template <class A, int WF>
+__device__ __forceinline__ float chunk_dot(const uint4 w, const uint8_t* xl, int64_t c) {
+  using XS = XStore<A, WF>;
+  constexpr int kc = Fmt<WF>::kc;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  float acc = 0.0f;
+  if constexpr (XS::kBF16) {
+    const uint4* xp = reinterpret_cast<const uint4*>(xl + c * kc * 2);
+    if constexpr (WF == AM_WF_INT4) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint4 xv = xp[t];
+        const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t pair = ((ws[t] >> (4 * pp)) & 0x000F000Fu) | 0x43004300u;
+          acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[pp]), as_bf2(pair), acc, false);
+        }
+      }
+    } else {  // BF16 weights
+      const uint4 xv = xp[0];
+      const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[t]), as_bf2(ws[t]), acc, false);
+    }
+  } else {
+    const float* xf = reinterpret_cast<const float*>(xl) + c * kc;
+    if constexpr (WF == AM_WF_F32) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc = fmaf(xf[t], __uint_as_float(ws[t]), acc);
+    } else if constexpr (WF == AM_WF_BF16) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc = fmaf(xf[2 * t], __uint_as_float(ws[t] << 16), acc);
+        acc = fmaf(xf[2 * t + 1], __uint_as_float(ws[t] & 0xFFFF0000u), acc);
+      }
+    } else if constexpr (WF == AM_WF_INT8) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc = fmaf(xf[4 * t + b], static_cast<float>((ws[t] >> (8 * b)) & 0xFFu), acc);
+    } else {  // INT4, fp32 activations: nibble j of word t is k = 8t + {0,2,4,6,1,3,5,7}[j]
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int kk = 8 * t + ((j < 4) ? 2 * j : 2 * (j - 4) + 1);
+          acc = fmaf(xf[kk], static_cast<float>((ws[t] >> (4 * j)) & 0xFu), acc);
+        }
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float silu_ref(float g) {
+  if (g >= 0.0f) return g / (1.0f + expf(-g));
+  const float e = expf(g);
+  return g * e / (1.0f + e);
+}
+
+template <class A, int WF, bool NORM, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
+  using XS = XStore<A, WF>;
+  using T = typename A::T;
+  constexpr int kc = Fmt<WF>::kc;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[4];
+  const int64_t K = p.k;
+  uint8_t* xl = smem;                                                     // x (LDS)
+  float* xsum = reinterpret_cast<float*>(smem + ((K * XS::kBytes + 15) / 16) * 16);  // per-chunk sums
+
+  // ---- prologue: x (optionally RMSNorm'd) -> LDS, per-chunk sums ----
+  const T* xin = static_cast<const T*>(p.x);
+  float inv = 1.0f;
+  if constexpr (NORM) {
+    float ss = 0.0f;
+    for (int64_t j = threadIdx.x; j < K; j += 256) {
+      const float v = A::load(xin, j);
+      ss = fmaf(v, v, ss);
+    }
+    ss = block_sum_256(ss, red);
+    inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
+  }
+  const T* nw = static_cast<const T*>(p.norm_w);
+  for (int64_t j = threadIdx.x; j < K; j += 256) {
+    float v = A::load(xin, j);
+    if constexpr (NORM) v = A::round((v * inv) * A::load(nw, j));
+    if constexpr (XS::kBF16)
+      reinterpret_cast<uint16_t*>(xl)[j] = f32_to_bf16_bits(v);
+    else
+      reinterpret_cast<float*>(xl)[j] = v;
+  }
+  __syncthreads();
+  const int64_t C = p.row_bytes / 16;  // chunks per row
+  if constexpr (WF == AM_WF_INT4 || WF == AM_WF_INT8) {
+    for (int64_t c = threadIdx.x; c < C; c += 256) {
+      float s = 0.0f;
+      for (int i = 0; i < kc; ++i) {
+        const int64_t j = c * kc + i;
+        s += XS::kBF16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xl)[j])
+                       : reinterpret_cast<const float*>(xl)[j];
+      }
+      xsum[c] = s;
+    }
+    __syncthreads();
+  }
+
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
+  const int J = static_cast<int>((C + 63) / 64);
+  const int ng = (WF == AM_WF_INT4) ? static_cast<int>(K / p.group) : 1;
+  const int chunks_per_group = (WF == AM_WF_INT4) ? p.group / kc : 1;
+
+  float best_v = 0.0f;
+  int64_t best_i = -1;
+  int64_t posv = 0;
+  if constexpr (EPI == kEpiQkv) posv = *p.pos;
+
+  for (int64_t u = gw; u < p.units; u += TW) {
+    int64_t r0, r1;
+    if constexpr (EPI == kEpiQkv) {
+      const int64_t half = p.d / 2;
+      const int64_t head = u / half, i = u % half;
+      r0 = head * p.d + i;
+      r1 = r0 + half;
+    } else if constexpr (EPI == kEpiGateUp) {
+      r0 = u;  // gate row u, up row u (rows [0,F) gate then [F,2F) up)
+      r1 = u + p.n / 2;
+    } else {
+      r0 = 2 * u;
+      r1 = 2 * u + 1;
+    }
+    const bool v1 = r1 < p.n;
+    const uint8_t* w0 = p.w + r0 * p.row_bytes;
+    const uint8_t* w1 = p.w + (v1 ? r1 : r0) * p.row_bytes;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int j0 = 0; j0 < J; j0 += kJB) {
+      uint4 wa[kJB], wb[kJB];
+      float sa[kJB], sb[kJB];
+#pragma unroll
+      for (int jj = 0; jj < kJB; ++jj) {
+        const int64_t c = lane + 64 * static_cast<int64_t>(j0 + jj);
+        const bool ok = (j0 + jj < J) && c < C;
+        wa[jj] = ok ? *reinterpret_cast<const uint4*>(w0 + c * 16) : make_uint4(0, 0, 0, 0);
+        wb[jj] = ok ? *reinterpret_cast<const uint4*>(w1 + c * 16) : make_uint4(0, 0, 0, 0);
+        if constexpr (WF == AM_WF_INT4) {
+          const uint16_t* sc = static_cast<const uint16_t*>(p.scales);
+          const int64_t g = c / chunks_per_group;
+          sa[jj] = ok ? static_cast<float>(__builtin_bit_cast(_Float16, sc[r0 * ng + g])) : 0.0f;
+          sb[jj] = ok ? static_cast<float>(__builtin_bit_cast(_Float16, sc[(v1 ? r1 : r0) * ng + g])) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < kJB; ++jj) {
+        const int64_t c = lane + 64 * static_cast<int64_t>(j0 + jj);
+        if ((j0 + jj < J) && c < C) {
+          float da = chunk_dot<A, WF>(wa[jj], xl, c);
+          float db = chunk_dot<A, WF>(wb[jj], xl, c);
+          if constexpr (XS::kOff != 0.0f) {
+            const float xs = xsum[c];
+            da = fmaf(-XS::kOff, xs, da);
+            db = fmaf(-XS::kOff, xs, db);
+          }
+          if constexpr (WF == AM_WF_INT4) {
+            acc0 = fmaf(sa[jj], da, acc0);
+            acc1 = fmaf(sb[jj], db, acc1);
+          } else {
+            acc0 += da;
+            acc1 += db;
+          }
+        }
+      }
+    }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if constexpr (WF == AM_WF_INT8) {
+      const float* sc = static_cast<const float*>(p.scales);
+      acc0 *= sc[r0];
+      acc1 *= sc[v1 ? r1 : r0];
+    }
+
+    // ---- epilogue ----
+    if constexpr (EPI == kEpiLmHead) {
+      if (lane == 0) {
+        float* lg = static_cast<float*>(p.out);
+        if (lg != nullptr) {
+          lg[r0] = acc0;
+          if (v1) lg[r1] = acc1;
+        }
+        if (argmax_better(acc0, r0, best_v, best_i)) { best_v = acc0; best_i = r0; }
+        if (v1 && argmax_better(acc1, r1, best_v, best_i)) { best_v = acc1; best_i = r1; }
+      }
+    } else if (lane == 0) {
+      T* out = static_cast<T*>(p.out);
+      if constexpr (EPI == kEpiStore) {
+        if (p.out_f32) {
+          float* of = static_cast<float*>(p.out);
+          of[r0] = acc0;
+          if (v1) of[r1] = acc1;
+        } else {
+          A::store(out, r0, acc0);
+          if (v1) A::store(out, r1, acc1);
+        }
+      } else if constexpr (EPI == kEpiResidual) {
+        const T* res = static_cast<const T*>(p.residual);
+        A::store(out, r0, A::load(res, r0) + A::round(acc0));
+        if (v1) A::store(out, r1, A::load(res, r1) + A::round(acc1));
+      } else if constexpr (EPI == kEpiGateUp) {
+        const float g = A::round(acc0), up = A::round(acc1);
+        A::store(out, u, silu_ref(g) * up);
+      } else if constexpr (EPI == kEpiQkv) {
+        const int64_t half = p.d / 2;
+        const int64_t head = u / half, i = u % half;
+        const float y0 = A::round(acc0), y1 = A::round(acc1);
+        if (head < p.hq + p.hkv) {
+          const float c = p.cos_tab[posv * half + i], s = p.sin_tab[posv * half + i];
+          const float o0 = y0 * c - y1 * s;
+          const float o1 = y1 * c + y0 * s;
+          if (head < p.hq) {
+            T* q = static_cast<T*>(p.q_out);
+            A::store(q, head * p.d + i, o0);
+            A::store(q, head * p.d + i + half, o1);
+          } else if (posv < p.cap) {
+            T* kc = static_cast<T*>(p.k_cache);
+            const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
+            A::store(kc, base + i, o0);
+            A::store(kc, base + i + half, o1);
+          }
+        } else if (posv < p.cap) {
+          T* vc = static_cast<T*>(p.v_cache);
+          const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
+          A::store(vc, base + i, y0);
+          A::store(vc, base + i + half, y1);
+        }
+      }
+    }
+  }
+
+  if constexpr (EPI == kEpiLmHead) {
+    // block-level best -> partials; the last block reduces and publishes the token.
+    __shared__ float bv_s[4];
+    __shared__ int64_t bi_s[4];
+    __shared__ bool last;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 0) {
+      bv_s[wave] = best_v;
+      bi_s[wave] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = 0.0f;
+      int64_t bi = -1;
+      for (int w = 0; w < 4; ++w)
+        if (bi_s[w] >= 0 && argmax_better(bv_s[w], bi_s[w], bv, bi)) { bv = bv_s[w]; bi = bi_s[w]; }
+      p.pv[blockIdx.x] = bv;
+      p.pi[blockIdx.x] = bi;
+      __threadfence();
+      const unsigned t = atomicAdd(p.ticket, 1u);
+      last = (t == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (last) {
+      __threadfence();
+      float bv = 0.0f;
+      int64_t bi = -1;
+      for (int64_t b = threadIdx.x; b < gridDim.x; b += 256) {
+        const float v = __hip_atomic_load(&p.pv[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t i = __hip_atomic_load(&p.pi[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (i >= 0 && argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int64_t oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && argmax_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+      }
+      if (lane == 0) {
+        bv_s[wave] = bv;
+        bi_s[wave] = bi;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float fv = 0.0f;
+        int64_t fi = -1;
+        for (int w = 0; w < 4; ++w)
+          if (bi_s[w] >= 0 && argmax_better(bv_s[w], bi_s[w], fv, fi)) { fv = bv_s[w]; fi = bi_s[w]; }
+        const int64_t tok = fi < 0 ? 0 : fi;
+        p.token_out[0] = tok;
+        if (p.tokens_hist != nullptr) {
+          const int64_t st = *p.step;
+          p.tokens_hist[st] = tok;
+          *p.step = st + 1;
+          *p.pos_inc = *p.pos_inc + 1;
+        }
+        *p.ticket = 0u;
+      }
+    }
+  }
+}
+
+// ---- host-side launch ----
+int64_t RowBytes(int32_t fmt, int64_t k) {
+  switch (fmt) {
+    case AM_WF_F32: return k * 4;
+    case AM_WF_BF16: return k * 2;
+    case AM_WF_INT8: return k;
+    default: return k / 2;
+  }
+}
+
+am_status_code ValidateWeight(const am_gfx950_weight& w) {
+  AM_CHECK_ARG(w.data != nullptr && w.n > 0 && w.k > 0, "weight: null data or empty shape");
+  AM_CHECK_ARG(w.format >= AM_WF_F32 && w.format <= AM_WF_INT4, "weight: unknown format");
+  const int kc[4] = {4, 8, 16, 32};
+  AM_CHECK_ARG(w.k % kc[w.format] == 0, "weight: in_features must fill whole 16-byte chunks");
+  if (w.format == AM_WF_INT4) {
+    AM_CHECK_ARG(w.group_size > 0 && w.group_size % 32 == 0 && w.k % w.group_size == 0,
+                 "weight: INT4 group_size must be a multiple of 32 dividing in_features");
+  }
+  if (w.format >= AM_WF_INT8) AM_CHECK_ARG(w.scales != nullptr, "weight: quantized weight needs scales");
+  AM_CHECK_ARG((reinterpret_cast<uintptr_t>(w.data) & 15u) == 0, "weight: data must be 16-byte aligned");
+  return AM_STATUS_OK;
+}
+
+template <class A, int WF, bool NORM, int EPI>
+am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
+  using XS = XStore<A, WF>;
+  const int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (g.row_bytes / 16) * 4;
+  if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
+  // Balanced persistent-style grid: at most ~8 resident blocks per CU.
+  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * 8 * 4;
+  const int64_t upw = CeilDiv(g.units, max_waves);
+  int64_t waves = CeilDiv(g.units, upw);
+  int64_t blocks = CeilDiv(waves, 4);
+  if (EPI == kEpiLmHead && blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                     static_cast<size_t>(lds), s, g);
+  AM_RETURN_IF_LAUNCH_FAILED("gemv");
+  return AM_STATUS_OK;
+}
+
+template <bool NORM, int EPI>
+am_status_code Dispatch(int32_t act, int32_t fmt, const GemvArgs& g, hipStream_t s) {
+  if (act == AM_DT_F32) {
+    switch (fmt) {
+      case AM_WF_F32: return LaunchT<ActF32, AM_WF_F32, NORM, EPI>(g, s);
+      case AM_WF_BF16: return LaunchT<ActF32, AM_WF_BF16, NORM, EPI>(g, s);
+      case AM_WF_INT8: return LaunchT<ActF32, AM_WF_INT8, NORM, EPI>(g, s);
+      default: return LaunchT<ActF32, AM_WF_INT4, NORM, EPI>(g, s);
+    }
+  }
+  switch (fmt) {
+    case AM_WF_F32: return LaunchT<ActBF16, AM_WF_F32, NORM, EPI>(g, s);
+    case AM_WF_BF16: return LaunchT<ActBF16, AM_WF_BF16, NORM, EPI>(g, s);
+    case AM_WF_INT8: return LaunchT<ActBF16, AM_WF_INT8, NORM, EPI>(g, s);
+    default: return LaunchT<ActBF16, AM_WF_INT4, NORM, EPI>(g, s);
+  }
+}
+
+GemvArgs BaseArgs(const am_gfx950_weight& w) {
+  GemvArgs g{};
+  g.w = static_cast<const uint8_t*>(w.data);
+  g.scales = w.scales;
+  g.n = w.n;
+  g.k = w.k;
+  g.group = w.group_size;
+  g.row_bytes = RowBytes(w.format, w.k);
+  g.units = CeilDiv(w.n, 2);
+  return g;
+}
+
+}  // namespace
+
+// Used by linear.cpp-equivalent entry (am_gfx950_linear) for m = 1 rows.
+am_status_code GemvLinearRow(const void* x, int32_t act, const am_gfx950_weight& w, void* out, int32_t out_dtype,
+                             const void* residual, hipStream_t s) {
+  if (auto st = ValidateWeight(w); st != AM_STATUS_OK) return st;
+  GemvArgs g = BaseArgs(w);
+  g.x = x;
+  g.out = out;
+  g.residual = residual;
+  g.out_f32 = (out_dtype == AM_DT_F32 && act != AM_DT_F32) ? 1 : 0;
+  if (residual != nullptr && g.out_f32)
+    return SetLastError(AM_STATUS_INVALID_ARGUMENT, "linear: residual needs out dtype == activation dtype");
+  if (residual != nullptr) return Dispatch<false, kEpiResidual>(act, w.format, g, s);
+  return Dispatch<false, kEpiStore>(act, w.format, g, s);
+}
+
+}  // namespace am
+
+using namespace am;
+
+extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a, void* stream) {
+  AM_CHECK_ARG(a != nullptr, "fused_qkv: null args");
+  if (auto st = ValidateWeight(a->w_qkv); st != AM_STATUS_OK) return st;
+  AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_qkv: dtype");
+  AM_CHECK_ARG(a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0 && a->head_dim > 0 && a->head_dim % 2 == 0,
+               "fused_qkv: bad head configuration");
+  AM_CHECK_ARG(a->w_qkv.n == (a->hq + 2 * a->hkv) * a->head_dim, "fused_qkv: weight rows != (hq+2hkv)*d");
+  AM_CHECK_ARG(a->h && a->norm_w && a->cos_tab && a->sin_tab && a->pos && a->q_out && a->k_cache && a->v_cache,
+               "fused_qkv: null pointer");
+  AM_CHECK_ARG(a->eps > 0.0f, "fused_qkv: eps must be positive");
+  GemvArgs g = BaseArgs(a->w_qkv);
+  g.units = a->w_qkv.n / 2;
+  g.x = a->h;
+  g.norm_w = a->norm_w;
+  g.eps = a->eps;
+  g.cos_tab = a->cos_tab;
+  g.sin_tab = a->sin_tab;
+  g.pos = a->pos;
+  g.q_out = a->q_out;
+  g.k_cache = a->k_cache;
+  g.v_cache = a->v_cache;
+  g.hq = static_cast<int32_t>(a->hq);
+  g.hkv = static_cast<int32_t>(a->hkv);
+  g.d = static_cast<int32_t>(a->head_dim);
+  g.cap = a->capacity;
+  return Dispatch<true, kEpiQkv>(a->dtype, a->w_qkv.format, g, AsStream(stream));
+}
+
+extern "C" am_status_code am_gfx950_fused_linear_residual(const am_gfx950_fused_linear_residual_args* a,
+                                                          void* stream) {
+  AM_CHECK_ARG(a != nullptr, "fused_linear_residual: null args");
+  if (auto st = ValidateWeight(a->w); st != AM_STATUS_OK) return st;
+  AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_linear_residual: dtype");
+  AM_CHECK_ARG(a->x && a->h, "fused_linear_residual: null pointer");
+  GemvArgs g = BaseArgs(a->w);
+  g.x = a->x;
+  g.out = a->h;
+  g.residual = a->h;
+  return Dispatch<false, kEpiResidual>(a->dtype, a->w.format, g, AsStream(stream));
+}
+
+extern "C" am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_args* a, void* stream) {
+  AM_CHECK_ARG(a != nullptr, "fused_gate_up: null args");
+  if (auto st = ValidateWeight(a->w_gate_up); st != AM_STATUS_OK) return st;
+  AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_gate_up: dtype");
+  AM_CHECK_ARG(a->w_gate_up.n % 2 == 0, "fused_gate_up: interleaved weight needs an even row count");
+  AM_CHECK_ARG(a->h && a->norm_w && a->act_out && a->eps > 0.0f, "fused_gate_up: bad pointer/eps");
+  GemvArgs g = BaseArgs(a->w_gate_up);
+  g.x = a->h;
+  g.norm_w = a->norm_w;
+  g.eps = a->eps;
+  g.out = a->act_out;
+  return Dispatch<true, kEpiGateUp>(a->dtype, a->w_gate_up.format, g, AsStream(stream));
+}
+
+extern "C" int64_t am_gfx950_lm_head_workspace_bytes(void) {
+  // ticket (256 B) + up to 65536 block partials (value + index)
+  return 256 + 65536LL * (4 + 8);
+}
+
+extern "C" am_status_code am_gfx950_fused_lm_head(const am_gfx950_fused_lm_head_args* a, void* stream) {
+  AM_CHECK_ARG(a != nullptr, "fused_lm_head: null args");
+  if (auto st = ValidateWeight(a->w); st != AM_STATUS_OK) return st;
+  AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_lm_head: dtype");
+  AM_CHECK_ARG(a->h && a->norm_w && a->token_out && a->workspace && a->eps > 0.0f, "fused_lm_head: bad args");
+  AM_CHECK_ARG(a->workspace_bytes >= am_gfx950_lm_head_workspace_bytes(), "fused_lm_head: workspace too small");
+  AM_CHECK_ARG(a->tokens_hist == nullptr || (a->pos != nullptr && a->step != nullptr),
+               "fused_lm_head: tokens_hist needs pos and step");
+  GemvArgs g = BaseArgs(a->w);
+  g.x = a->h;
+  g.norm_w = a->norm_w;
+  g.eps = a->eps;
+  g.out = a->logits;
+  g.token_out = a->token_out;
+  g.tokens_hist = a->tokens_hist;
+  g.pos_inc = a->pos;
+  g.step = a->step;
+  uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+  g.ticket = reinterpret_cast<unsigned*>(ws);
+  g.pi = reinterpret_cast<int64_t*>(ws + 256);
+  g.pv = reinterpret_cast<float*>(ws + 256 + 65536LL * 8);
+  return Dispatch<true, kEpiLmHead>(a->dtype, a->w.format, g, AsStream(stream));
+}

@@ -1,0 +1,239 @@
+"""ctypes bindings of the gfx950 C ABI (include/am_c_api.h, am_gfx950.h, am_runtime.h).
+
+Struct layouts mirror the C headers field for field.  Nothing here computes: every
+call goes to ``libaethermind_gfx950.so`` and a missing library is an error.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+AM_DT_F32, AM_DT_BF16, AM_DT_F16, AM_DT_I8, AM_DT_I4, AM_DT_I32, AM_DT_I64, AM_DT_U32, AM_DT_U8 = range(9)
+AM_WF_F32, AM_WF_BF16, AM_WF_INT8, AM_WF_INT4 = range(4)
+(AM_ROLE_QKV, AM_ROLE_O, AM_ROLE_GATE_UP, AM_ROLE_DOWN, AM_ROLE_LM_HEAD, AM_ROLE_Q, AM_ROLE_K, AM_ROLE_V,
+ AM_ROLE_GATE, AM_ROLE_UP) = range(10)
+AM_BUF_EMBED, AM_BUF_IN_NORM, AM_BUF_POST_NORM, AM_BUF_FINAL_NORM, AM_BUF_ROPE_COS, AM_BUF_ROPE_SIN = range(6)
+
+STATUS_NAMES = ["OK", "CANCELLED", "UNKNOWN", "INVALID_ARGUMENT", "DEADLINE_EXCEEDED", "NOT_FOUND",
+                "ALREADY_EXISTS", "PERMISSION_DENIED", "RESOURCE_EXHAUSTED", "FAILED_PRECONDITION", "ABORTED",
+                "OUT_OF_RANGE", "UNIMPLEMENTED", "INTERNAL", "UNAVAILABLE", "DATA_LOSS", "OVERFLOW",
+                "UNAUTHENTICATED"]
+
+vp, i32, i64, u64, f32, f64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
+
+
+class Weight(C.Structure):
+    _fields_ = [("data", vp), ("scales", vp), ("n", i64), ("k", i64), ("format", i32), ("group_size", i32)]
+
+
+class EmbeddingArgs(C.Structure):
+    _fields_ = [("ids", vp), ("ids_dtype", i32), ("n_tokens", i64), ("table", vp), ("table_dtype", i32),
+                ("vocab", i64), ("hidden", i64), ("out", vp), ("out_dtype", i32), ("err_flag", vp), ("check", i32)]
+
+
+class RmsNormArgs(C.Structure):
+    _fields_ = [("x", vp), ("w", vp), ("out", vp), ("rows", i64), ("hidden", i64), ("x_stride", i64),
+                ("out_stride", i64), ("eps", f32), ("x_dtype", i32), ("w_dtype", i32), ("out_dtype", i32)]
+
+
+class LinearArgs(C.Structure):
+    _fields_ = [("x", vp), ("x_dtype", i32), ("m", i64), ("w", Weight), ("out", vp), ("out_dtype", i32),
+                ("residual", vp), ("mode", i32)]
+
+
+class RopeArgs(C.Structure):
+    _fields_ = [("q", vp), ("k", vp), ("q_out", vp), ("k_out", vp), ("pos", vp), ("cos_tab", vp), ("sin_tab", vp),
+                ("seq", i64), ("hq", i64), ("hkv", i64), ("head_dim", i64), ("max_pos", i64), ("dtype", i32)]
+
+
+class KvUpdateArgs(C.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("k_cache", vp), ("v_cache", vp), ("seq", i64), ("hkv", i64),
+                ("head_dim", i64), ("capacity", i64), ("start_pos", i64), ("start_pos_dev", vp), ("dtype", i32),
+                ("err_flag", vp)]
+
+
+class AttentionArgs(C.Structure):
+    _fields_ = [("q", vp), ("k_cache", vp), ("v_cache", vp), ("out", vp), ("seq", i64), ("hq", i64), ("hkv", i64),
+                ("head_dim", i64), ("capacity", i64), ("start_pos", i64), ("start_pos_dev", vp), ("batch", i64),
+                ("cache_batch_stride", i64), ("dtype", i32), ("num_splits", i32), ("workspace", vp),
+                ("workspace_bytes", i64)]
+
+
+class SiluMulArgs(C.Structure):
+    _fields_ = [("gate", vp), ("up", vp), ("out", vp), ("n", i64), ("dtype", i32)]
+
+
+class AddArgs(C.Structure):
+    _fields_ = [("a", vp), ("b", vp), ("out", vp), ("n", i64), ("dtype", i32)]
+
+
+class ArgmaxArgs(C.Structure):
+    _fields_ = [("x", vp), ("dtype", i32), ("rows", i64), ("n", i64), ("out", vp), ("workspace", vp),
+                ("workspace_bytes", i64)]
+
+
+class QuantizeArgs(C.Structure):
+    _fields_ = [("src", vp), ("src_dtype", i32), ("src_rows", i64), ("dst", Weight), ("dst_row_offset", i64),
+                ("dst_row_stride", i64)]
+
+
+class PackInt4Args(C.Structure):
+    _fields_ = [("logical", vp), ("scales", vp), ("dst", Weight)]
+
+
+class DequantArgs(C.Structure):
+    _fields_ = [("w", Weight), ("out", vp)]
+
+
+class SynthArgs(C.Structure):
+    _fields_ = [("seed", u64), ("tensor_id", u64), ("stddev", f64), ("offset", i64), ("n", i64), ("out", vp),
+                ("dtype", i32)]
+
+
+class FusedQkvArgs(C.Structure):
+    _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_qkv", Weight), ("cos_tab", vp), ("sin_tab", vp),
+                ("pos", vp), ("q_out", vp), ("k_cache", vp), ("v_cache", vp), ("hq", i64), ("hkv", i64),
+                ("head_dim", i64), ("capacity", i64), ("dtype", i32)]
+
+
+class FusedLinearResidualArgs(C.Structure):
+    _fields_ = [("x", vp), ("w", Weight), ("h", vp), ("dtype", i32)]
+
+
+class FusedGateUpArgs(C.Structure):
+    _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_gate_up", Weight), ("act_out", vp), ("dtype", i32)]
+
+
+class FusedLmHeadArgs(C.Structure):
+    _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w", Weight), ("logits", vp), ("token_out", vp),
+                ("tokens_hist", vp), ("pos", vp), ("step", vp), ("dtype", i32), ("workspace", vp),
+                ("workspace_bytes", i64)]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("num_layers", i32), ("hidden", i32), ("num_q_heads", i32), ("num_kv_heads", i32),
+                ("head_dim", i32), ("ffn", i32), ("vocab", i32), ("rms_eps", f32), ("rope_theta", f64),
+                ("act_dtype", i32), ("weight_format", i32), ("group_size", i32), ("max_tokens", i32),
+                ("max_prefill_chunk", i32)]
+
+
+class SessionOptions(C.Structure):
+    _fields_ = [("fused_decode", i32), ("use_graph", i32)]
+
+
+_SIGS = {
+    # name: (restype, argtypes)
+    "am_last_error_message": (C.c_char_p, []),
+    "am_error_create": (vp, [i32, C.c_char_p]),
+    "am_error_destroy": (None, [vp]),
+    "am_error_code": (i32, [vp]),
+    "am_error_message": (C.c_char_p, [vp]),
+    "am_gfx950_device_count": (i32, []),
+    "am_gfx950_version": (C.c_char_p, []),
+    "am_gfx950_embedding": (i32, [C.POINTER(EmbeddingArgs), vp]),
+    "am_gfx950_embed_token": (i32, [vp, vp, i32, i64, i64, vp, vp, vp]),
+    "am_gfx950_rmsnorm": (i32, [C.POINTER(RmsNormArgs), vp]),
+    "am_gfx950_linear": (i32, [C.POINTER(LinearArgs), vp]),
+    "am_gfx950_rope": (i32, [C.POINTER(RopeArgs), vp]),
+    "am_gfx950_rope_table": (i32, [i64, i64, f64, vp, vp]),
+    "am_gfx950_kv_update": (i32, [C.POINTER(KvUpdateArgs), vp]),
+    "am_gfx950_attention": (i32, [C.POINTER(AttentionArgs), vp]),
+    "am_gfx950_attention_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64, i32]),
+    "am_gfx950_silu_mul": (i32, [C.POINTER(SiluMulArgs), vp]),
+    "am_gfx950_add": (i32, [C.POINTER(AddArgs), vp]),
+    "am_gfx950_argmax": (i32, [C.POINTER(ArgmaxArgs), vp]),
+    "am_gfx950_argmax_workspace_bytes": (i64, [i64]),
+    "am_gfx950_quantize": (i32, [C.POINTER(QuantizeArgs), vp]),
+    "am_gfx950_pack_plain": (i32, [C.POINTER(QuantizeArgs), vp]),
+    "am_gfx950_pack_int4": (i32, [C.POINTER(PackInt4Args), vp]),
+    "am_gfx950_dequant": (i32, [C.POINTER(DequantArgs), vp]),
+    "am_gfx950_weight_bytes": (i32, [i64, i64, i32, i32, C.POINTER(i64), C.POINTER(i64)]),
+    "am_gfx950_synth_normal": (i32, [C.POINTER(SynthArgs), vp]),
+    "am_gfx950_synth_token_ids": (i32, [u64, u64, i64, i64, vp, vp]),
+    "am_gfx950_fill": (i32, [vp, i32, i64, f32, vp]),
+    "am_gfx950_fused_qkv": (i32, [C.POINTER(FusedQkvArgs), vp]),
+    "am_gfx950_fused_linear_residual": (i32, [C.POINTER(FusedLinearResidualArgs), vp]),
+    "am_gfx950_fused_gate_up": (i32, [C.POINTER(FusedGateUpArgs), vp]),
+    "am_gfx950_fused_lm_head": (i32, [C.POINTER(FusedLmHeadArgs), vp]),
+    "am_gfx950_lm_head_workspace_bytes": (i64, []),
+    "am_gfx950_decode_advance": (i32, [vp, vp, vp, vp, vp]),
+    "am_runtime_create": (i32, [i32, C.POINTER(vp)]),
+    "am_runtime_destroy": (None, [vp]),
+    "am_runtime_stream": (vp, [vp]),
+    "am_model_create_synthetic": (i32, [vp, C.POINTER(ModelConfig), u64, C.POINTER(vp)]),
+    "am_model_destroy": (None, [vp]),
+    "am_model_weight": (i32, [vp, i32, i32, C.POINTER(Weight)]),
+    "am_model_buffer": (i32, [vp, i32, i32, C.POINTER(vp), C.POINTER(i64)]),
+    "am_model_weight_bytes_total": (i64, [vp]),
+    "am_session_create": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
+    "am_session_destroy": (None, [vp]),
+    "am_session_prefill": (i32, [vp, vp, i64, C.POINTER(i64)]),
+    "am_session_decode": (i32, [vp, i64, vp]),
+    "am_session_decode_async": (i32, [vp, i64]),
+    "am_session_generate": (i32, [vp, vp, i64, i64, i64, vp, C.POINTER(i64)]),
+    "am_session_logits": (i32, [vp, vp]),
+    "am_session_position": (i64, [vp]),
+    "am_session_decode_plan_size": (i64, [vp]),
+    "am_session_profile_decode": (i32, [vp, i64, vp, vp]),
+}
+
+
+class NativeError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        name = STATUS_NAMES[code] if 0 <= code < len(STATUS_NAMES) else str(code)
+        super().__init__(f"{fn} -> {name}: {msg}")
+        self.code = code
+        self.status = name
+
+
+def lib_path() -> str:
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "libaethermind_gfx950.so")
+
+
+class Lib:
+    """Loaded library with typed functions; ``call`` raises NativeError on non-OK."""
+
+    def __init__(self, path: str | None = None):
+        path = path or lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"gfx950 library not built ({path}); run __graft_entry__.build()")
+        self.path = path
+        self.dll = C.CDLL(path)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(self.dll, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    def __getattr__(self, name):
+        return getattr(self.dll, name)
+
+    def call(self, name: str, *args) -> None:
+        rc = getattr(self.dll, name)(*args)
+        if rc != 0:
+            msg = self.dll.am_last_error_message()
+            raise NativeError(name, rc, msg.decode() if msg else "")
+
+
+_LIB: Lib | None = None
+
+
+def lib() -> Lib:
+    global _LIB
+    if _LIB is None:
+        _LIB = Lib()
+    return _LIB
+
+
+def header_functions(include_dir: str) -> list[str]:
+    """Names of every function declared in the C headers (for the export check)."""
+    import re
+    names = []
+    for fn in sorted(os.listdir(include_dir)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(include_dir, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(am_\w+)\s*\(", text, flags=re.M):
+            names.append(m.group(1))
+    return sorted(set(names))

@@ -1,0 +1,362 @@
+/*
+ * gfx950 (MI355X) kernel C ABI for the AetherMind Llama prefill/decode path.
+ *
+ * Every entry point has the shape
+ *     am_status_code am_gfx950_<op>(const am_gfx950_<op>_args* args, void* hip_stream);
+ * All pointers inside the args are DEVICE pointers unless a field says otherwise.
+ * Work is enqueued on `hip_stream` (NULL = the default stream) and the call returns
+ * without synchronising, except where a field asks for a checked (synchronous) mode.
+ * Argument validation happens on the host before any launch; a rejected call enqueues
+ * nothing.  These functions replace the reference's CPU KernelFunc bodies: the C++
+ * backend in aethermind_amd/csrc/host registers one KernelFunc per op through the
+ * reference's KernelRegistry shape (kernel_descriptor.h:12-21) that unpacks its
+ * params and calls the matching function here.
+ *
+ * Data layouts (row-major unless stated):
+ *   activations  [rows][cols], dtype AM_DT_F32 or AM_DT_BF16
+ *   KV cache     one plane per layer and K/V: [kv_heads][capacity][head_dim]
+ *                (the reference KVCacheLayout, kv_cache_view.cpp:41-75)
+ *   weights      see am_gfx950_weight
+ */
+#ifndef AM_GFX950_H
+#define AM_GFX950_H
+
+#include <stdint.h>
+
+#include "am_c_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum am_dtype {
+  AM_DT_F32 = 0,
+  AM_DT_BF16 = 1,
+  AM_DT_F16 = 2,
+  AM_DT_I8 = 3,
+  AM_DT_I4 = 4,
+  AM_DT_I32 = 5,
+  AM_DT_I64 = 6,
+  AM_DT_U32 = 7,
+  AM_DT_U8 = 8
+} am_dtype;
+
+/* Device weight formats (WeightFormat of kernel_selector.h:26-31 of the reference,
+ * with the two quantized formats given a concrete layout). */
+typedef enum am_weight_format {
+  AM_WF_F32 = 0,  /* fp32 [n][k]                                                  */
+  AM_WF_BF16 = 1, /* bf16 [n][k]                                                  */
+  AM_WF_INT8 = 2, /* uint8 [n][k] holding q+128, fp32 scale per row [n]           */
+  AM_WF_INT4 = 3  /* uint8 [n][k/2] nibbles holding q+8 (device tile order below), */
+                  /* fp16 scales [n][k/group]                                     */
+} am_weight_format;
+
+/* INT4 device tile order: each 32-bit word of a row holds k = 8w..8w+7 with
+ * nibble j (bits 4j..4j+3) = k 8w + {0,2,4,6,1,3,5,7}[j], so that
+ * (word >> 4t) & 0x000F000F yields the pair (k 8w+2t, k 8w+2t+1).  The logical
+ * interchange format (low nibble = even k, two's complement) converts to it with
+ * am_gfx950_pack_int4 and back with am_gfx950_dequant. */
+typedef struct am_gfx950_weight {
+  const void* data;
+  const void* scales; /* NULL for F32/BF16 */
+  int64_t n;          /* out_features */
+  int64_t k;          /* in_features  */
+  int32_t format;     /* am_weight_format */
+  int32_t group_size; /* INT4 only (SPEC: 128) */
+} am_gfx950_weight;
+
+/* ---------------- per-op kernels (one reference OpType each) ---------------- */
+
+/* OpType::kEmbedding (embedding_entry.cpp:32-126): out[t,:] = table[ids[t],:].
+ * ids dtype I32/I64/U32.  An id outside [0, vocab) writes a zero row and sets
+ * *err_flag (if non-NULL) to 1; with check != 0 the call synchronises the stream
+ * and returns AM_STATUS_OUT_OF_RANGE in that case, like the reference kernel. */
+typedef struct am_gfx950_embedding_args {
+  const void* ids;
+  int32_t ids_dtype;
+  int64_t n_tokens;
+  const void* table;
+  int32_t table_dtype; /* F32 / BF16 */
+  int64_t vocab, hidden;
+  void* out;
+  int32_t out_dtype;
+  int32_t* err_flag;
+  int32_t check;
+} am_gfx950_embedding_args;
+am_status_code am_gfx950_embedding(const am_gfx950_embedding_args* args, void* hip_stream);
+
+/* OpType::kRmsNorm (rmsnorm_fp32_avx2.cpp:15-122): y = x * rsqrt(mean(x^2)+eps) * w,
+ * fp32 accumulation, one rounding to out_dtype. */
+typedef struct am_gfx950_rmsnorm_args {
+  const void* x;
+  const void* w;
+  void* out;
+  int64_t rows, hidden;
+  int64_t x_stride, out_stride; /* elements between rows */
+  float eps;
+  int32_t x_dtype, w_dtype, out_dtype;
+} am_gfx950_rmsnorm_args;
+am_status_code am_gfx950_rmsnorm(const am_gfx950_rmsnorm_args* args, void* hip_stream);
+
+/* OpType::kLinear (linear_op.h:87-92): out[m,:] = x[m,:] @ W^T (+ residual[m,:]).
+ * fp32 accumulation; out rounded once to out_dtype, and with a residual the sum is
+ * rounded again (two op boundaries: Linear then Add).  residual may alias out.
+ * mode: 0 auto (m <= 8 -> GEMV, else MFMA GEMM), 1 GEMV, 2 GEMM. */
+typedef struct am_gfx950_linear_args {
+  const void* x;
+  int32_t x_dtype;
+  int64_t m;
+  am_gfx950_weight w;
+  void* out;
+  int32_t out_dtype;
+  const void* residual; /* optional, out_dtype */
+  int32_t mode;
+} am_gfx950_linear_args;
+am_status_code am_gfx950_linear(const am_gfx950_linear_args* args, void* hip_stream);
+
+/* OpType::kRoPE (rope_op.cpp:202-223; RoPEOp design :588-622): split-half rotation of
+ * q [seq][hq*d] and k [seq][hkv*d] at positions pos[seq] (I64, device) using the
+ * fp32 tables cos_tab/sin_tab [max_pos][d/2] built by am_gfx950_rope_table.
+ * Outputs may alias inputs. */
+typedef struct am_gfx950_rope_args {
+  const void* q;
+  const void* k;
+  void* q_out;
+  void* k_out;
+  const int64_t* pos;
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t seq, hq, hkv, head_dim, max_pos;
+  int32_t dtype;
+} am_gfx950_rope_args;
+am_status_code am_gfx950_rope(const am_gfx950_rope_args* args, void* hip_stream);
+
+/* Host-side helper: fills the host arrays cos_tab/sin_tab [max_pos][d/2] with
+ * inv_freq = 1/theta^(2i/d), angle = pos*inv_freq (double), cast to float. */
+am_status_code am_gfx950_rope_table(int64_t max_pos, int64_t head_dim, double theta,
+                                    float* cos_tab_host, float* sin_tab_host);
+
+/* OpType::kKVCacheUpdate (kvcache_update_op.cpp:50-138): writes k/v [seq][hkv*d]
+ * into the layer planes at positions [start, start+seq), start = *start_pos_dev if
+ * start_pos_dev != NULL else start_pos.  Rows past capacity are rejected on the host
+ * when start is a host value, and skipped (err_flag set) when it is a device value. */
+typedef struct am_gfx950_kv_update_args {
+  const void* k;
+  const void* v;
+  void* k_cache;
+  void* v_cache;
+  int64_t seq, hkv, head_dim, capacity;
+  int64_t start_pos;
+  const int64_t* start_pos_dev;
+  int32_t dtype;
+  int32_t* err_flag;
+} am_gfx950_kv_update_args;
+am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* args, void* hip_stream);
+
+/* OpType::kAttention (attention_op.cpp:11-169): causal GQA SDPA.  Query row s sits at
+ * position start+s and attends to cache positions [0, start+s]; q head h reads kv
+ * head h/(hq/hkv); scale 1/sqrt(d); fp32 online softmax.  The cache rows for the new
+ * positions must already be written (KVCacheUpdate precedes Attention).
+ * workspace: device scratch of am_gfx950_attention_workspace_bytes(...) bytes, whose
+ * first 4*hkv*batch bytes must be zero before the first call (the kernel leaves them
+ * zero).  batch > 1 stacks independent sequences: q [batch][seq][hq*d], caches
+ * [batch] planes of cache_batch_stride elements, start positions start_pos_dev[b]. */
+typedef struct am_gfx950_attention_args {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* out;
+  int64_t seq, hq, hkv, head_dim, capacity;
+  int64_t start_pos;
+  const int64_t* start_pos_dev;
+  int64_t batch;
+  int64_t cache_batch_stride;
+  int32_t dtype;
+  int32_t num_splits; /* 0 = choose */
+  void* workspace;
+  int64_t workspace_bytes;
+} am_gfx950_attention_args;
+am_status_code am_gfx950_attention(const am_gfx950_attention_args* args, void* hip_stream);
+int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
+                                            int64_t head_dim, int64_t capacity, int32_t num_splits);
+
+/* OpType::kSiluMul (silu_mul_op.cpp:32-61; formula const_eval_silu_mul.cpp:18-31). */
+typedef struct am_gfx950_silu_mul_args {
+  const void* gate;
+  const void* up;
+  void* out;
+  int64_t n;
+  int32_t dtype;
+} am_gfx950_silu_mul_args;
+am_status_code am_gfx950_silu_mul(const am_gfx950_silu_mul_args* args, void* hip_stream);
+
+/* OpType::kAdd (add_entry.cpp): out = a + b, same shape (no broadcast on this path). */
+typedef struct am_gfx950_add_args {
+  const void* a;
+  const void* b;
+  void* out;
+  int64_t n;
+  int32_t dtype;
+} am_gfx950_add_args;
+am_status_code am_gfx950_add(const am_gfx950_add_args* args, void* hip_stream);
+
+/* OpType::kArgmax (argmax_op.cpp:6-45), axis -1: out[r] = first index of the maximum
+ * of x[r,:] (NaN never selected; an all-NaN row gives 0).  x dtype F32/BF16, out I64.
+ * workspace: am_gfx950_argmax_workspace_bytes(rows) bytes, first 4*rows bytes zero
+ * before the first call (left zero). */
+typedef struct am_gfx950_argmax_args {
+  const void* x;
+  int32_t dtype;
+  int64_t rows, n;
+  int64_t* out;
+  void* workspace;
+  int64_t workspace_bytes;
+} am_gfx950_argmax_args;
+am_status_code am_gfx950_argmax(const am_gfx950_argmax_args* args, void* hip_stream);
+int64_t am_gfx950_argmax_workspace_bytes(int64_t rows);
+
+/* ---------------- weight loader / repack (WeightPrepackPlanner + prepacker) -------- */
+
+/* Quantize a device fp32/bf16 matrix src [n][k] into a device weight of `format`
+ * (INT8 per-channel or INT4 group) following the build SPEC:
+ *   INT8: s = max|w|/127 (1 for an all-zero row), q = clamp(rint(w/s), -127, 127)
+ *   INT4: s = fp16(max|w|/7) per group, q = clamp(rint(w/s), -8, 7), q = 0 if s == 0
+ * dst->data / dst->scales must point at buffers of am_gfx950_weight_bytes(...). */
+typedef struct am_gfx950_quantize_args {
+  const void* src;
+  int32_t src_dtype;
+  int64_t src_rows;     /* rows of src, each dst.k long */
+  am_gfx950_weight dst; /* data/scales written through (cast away const) */
+  int64_t dst_row_offset; /* src row r goes to dst row offset + r * stride */
+  int64_t dst_row_stride; /* 1 = contiguous rows; 2 = interleave (gate/up pairs) */
+} am_gfx950_quantize_args;
+am_status_code am_gfx950_quantize(const am_gfx950_quantize_args* args, void* hip_stream);
+
+/* Copies a device fp32/bf16 matrix into an F32/BF16 device weight, same row mapping
+ * as am_gfx950_quantize (dst_row_offset / dst_row_stride). */
+am_status_code am_gfx950_pack_plain(const am_gfx950_quantize_args* args, void* hip_stream);
+
+/* Converts the logical INT4 interchange format (uint8 [n][k/2], low nibble = even k,
+ * two's complement; fp16 scales [n][k/group]) into the device tile order. */
+typedef struct am_gfx950_pack_int4_args {
+  const uint8_t* logical;
+  const uint16_t* scales;
+  am_gfx950_weight dst;
+} am_gfx950_pack_int4_args;
+am_status_code am_gfx950_pack_int4(const am_gfx950_pack_int4_args* args, void* hip_stream);
+
+/* Dequantizes a device weight to fp32 [n][k] in logical k order:
+ * w = float(q) * float(scale), one fp32 multiply (bit-exact SPEC). */
+typedef struct am_gfx950_dequant_args {
+  am_gfx950_weight w;
+  float* out;
+} am_gfx950_dequant_args;
+am_status_code am_gfx950_dequant(const am_gfx950_dequant_args* args, void* hip_stream);
+
+/* Bytes of data and scales for a weight of this shape/format. */
+am_status_code am_gfx950_weight_bytes(int64_t n, int64_t k, int32_t format, int32_t group_size,
+                                      int64_t* data_bytes, int64_t* scale_bytes);
+
+/* Synthetic N(0, stddev) data of the build SPEC (SplitMix64 + Box-Muller with
+ * portable arithmetic), elements [offset, offset+n) of stream (seed, tensor_id).
+ * out dtype F32 or BF16 (RNE of the fp32 value). */
+typedef struct am_gfx950_synth_args {
+  uint64_t seed, tensor_id;
+  double stddev;
+  int64_t offset, n;
+  void* out;
+  int32_t dtype;
+} am_gfx950_synth_args;
+am_status_code am_gfx950_synth_normal(const am_gfx950_synth_args* args, void* hip_stream);
+
+/* Synthetic token ids (I64) of the build SPEC, uniform in [0, vocab). */
+am_status_code am_gfx950_synth_token_ids(uint64_t seed, uint64_t stream, int64_t vocab,
+                                         int64_t n, int64_t* out, void* hip_stream);
+
+/* Fill `n` elements of dtype F32/BF16 with a constant (norm gains = 1.0). */
+am_status_code am_gfx950_fill(void* out, int32_t dtype, int64_t n, float value,
+                              void* hip_stream);
+
+/* ---------------- fused decode kernels (fusion of reference node runs) ------------- */
+
+/* RmsNorm(input_layernorm) -> Linear q|k|v (one concatenated weight, rows q then k
+ * then v) -> RoPE(q, k) -> KVCacheUpdate(k_rope, v), for m = 1 token at position
+ * *pos (device).  Rounds at every reference op boundary. */
+typedef struct am_gfx950_fused_qkv_args {
+  const void* h;
+  const void* norm_w;
+  float eps;
+  am_gfx950_weight w_qkv;
+  const float* cos_tab;
+  const float* sin_tab;
+  const int64_t* pos;
+  void* q_out;
+  void* k_cache;
+  void* v_cache;
+  int64_t hq, hkv, head_dim, capacity;
+  int32_t dtype;
+} am_gfx950_fused_qkv_args;
+am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* args, void* hip_stream);
+
+/* Linear (x @ W^T) -> Add(residual): h = round(h + round(W x)), in place on h. */
+typedef struct am_gfx950_fused_linear_residual_args {
+  const void* x;
+  am_gfx950_weight w;
+  void* h;
+  int32_t dtype;
+} am_gfx950_fused_linear_residual_args;
+am_status_code am_gfx950_fused_linear_residual(const am_gfx950_fused_linear_residual_args* a,
+                                               void* hip_stream);
+
+/* RmsNorm(post_attention_layernorm) -> Linear gate, up (one weight: rows [0, F) are
+ * gate, rows [F, 2F) are up) -> SiluMul. */
+typedef struct am_gfx950_fused_gate_up_args {
+  const void* h;
+  const void* norm_w;
+  float eps;
+  am_gfx950_weight w_gate_up;
+  void* act_out;
+  int32_t dtype;
+} am_gfx950_fused_gate_up_args;
+am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_args* a, void* hip_stream);
+
+/* RmsNorm(final) -> Linear lm_head (fp32 logits) -> Argmax.  Writes logits [vocab]
+ * (if non-NULL) and token_out[0]; with tokens_hist != NULL also tokens_hist[*step]
+ * = token and increments *pos and *step (device-resident decode state).
+ * workspace: am_gfx950_lm_head_workspace_bytes() bytes, first 4 bytes zero before
+ * the first call (left zero). */
+typedef struct am_gfx950_fused_lm_head_args {
+  const void* h;
+  const void* norm_w;
+  float eps;
+  am_gfx950_weight w;
+  float* logits;
+  int64_t* token_out;
+  int64_t* tokens_hist;
+  int64_t* pos;
+  int64_t* step;
+  int32_t dtype;
+  void* workspace;
+  int64_t workspace_bytes;
+} am_gfx950_fused_lm_head_args;
+am_status_code am_gfx950_fused_lm_head(const am_gfx950_fused_lm_head_args* a, void* hip_stream);
+int64_t am_gfx950_lm_head_workspace_bytes(void);
+
+/* Embedding of the single token *token (device) into h (decode step input). */
+am_status_code am_gfx950_embed_token(const int64_t* token, const void* table, int32_t dtype,
+                                     int64_t vocab, int64_t hidden, void* h, int32_t* err_flag,
+                                     void* hip_stream);
+
+/* End of an unfused decode step (after Argmax): tokens_hist[*step] = *token,
+ * ++*step, ++*pos.  The fused lm_head kernel does the same in its epilogue. */
+am_status_code am_gfx950_decode_advance(const int64_t* token, int64_t* tokens_hist, int64_t* pos,
+                                        int64_t* step, void* hip_stream);
+
+/* Library / device information. */
+int32_t am_gfx950_device_count(void);
+const char* am_gfx950_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,110 @@
+/*
+ * Session-level C ABI for the gfx950 Llama prefill/decode path.
+ *
+ * No counterpart exists in the reference code: its generate API is design-only
+ * (docs/products/aethermind_prd.md:298-320 sketches am_runtime_create /
+ * am_model_load / am_session_generate; docs/designs/executor_design.md:226-256
+ * describes PrepareSession / Prefill / DecodeStep).  These entry points implement that
+ * design on one GPU: one HIP stream per runtime, weights repacked into HBM at model
+ * creation, a device-resident static KV cache, and a frozen decode plan replayed as a
+ * HIP graph with device-resident position/token state (no host sync per token).
+ * Token ids are int64 (the graph input dtype, model_graph_builder.cpp:339-342).
+ */
+#ifndef AM_RUNTIME_H
+#define AM_RUNTIME_H
+
+#include <stdint.h>
+
+#include "am_c_api.h"
+#include "am_gfx950.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct am_runtime am_runtime;
+typedef struct am_model am_model;
+typedef struct am_session am_session;
+
+typedef struct am_model_config {
+  int32_t num_layers, hidden, num_q_heads, num_kv_heads, head_dim, ffn, vocab;
+  float rms_eps;
+  double rope_theta;
+  int32_t act_dtype;         /* AM_DT_F32 or AM_DT_BF16 */
+  int32_t weight_format;     /* am_weight_format */
+  int32_t group_size;        /* INT4 group (SPEC: 128) */
+  int32_t max_tokens;        /* static KV capacity (positions) */
+  int32_t max_prefill_chunk; /* rows per prefill pass; prompts are chunked to this */
+} am_model_config;
+
+/* Weight roles for am_model_weight (per-weight identity = (layer, role)). */
+typedef enum am_weight_role {
+  AM_ROLE_QKV = 0,     /* rows q (hq*d), k (hkv*d), v (hkv*d) */
+  AM_ROLE_O = 1,
+  AM_ROLE_GATE_UP = 2, /* rows gate (ffn) then up (ffn) */
+  AM_ROLE_DOWN = 3,
+  AM_ROLE_LM_HEAD = 4, /* layer ignored */
+  AM_ROLE_Q = 5,       /* row views into QKV / GATE_UP */
+  AM_ROLE_K = 6,
+  AM_ROLE_V = 7,
+  AM_ROLE_GATE = 8,
+  AM_ROLE_UP = 9
+} am_weight_role;
+
+typedef enum am_model_buffer_kind {
+  AM_BUF_EMBED = 0,     /* [vocab][hidden] act dtype */
+  AM_BUF_IN_NORM = 1,   /* [hidden] act dtype, per layer */
+  AM_BUF_POST_NORM = 2, /* per layer */
+  AM_BUF_FINAL_NORM = 3,
+  AM_BUF_ROPE_COS = 4, /* [max_tokens][d/2] f32 */
+  AM_BUF_ROPE_SIN = 5
+} am_model_buffer_kind;
+
+am_status_code am_runtime_create(int32_t device, am_runtime** out);
+void am_runtime_destroy(am_runtime* rt);
+void* am_runtime_stream(am_runtime* rt); /* hipStream_t */
+
+/* Synthetic Llama-dense weights of the build SPEC (seeded normal(0, 0.02), norm gains
+ * 1.0) generated and repacked on the device. */
+am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* cfg, uint64_t seed,
+                                         am_model** out);
+void am_model_destroy(am_model* m);
+am_status_code am_model_weight(am_model* m, int32_t layer, int32_t role, am_gfx950_weight* out);
+am_status_code am_model_buffer(am_model* m, int32_t kind, int32_t layer, void** ptr, int64_t* bytes);
+int64_t am_model_weight_bytes_total(am_model* m); /* repacked linear weights incl. scales */
+
+typedef struct am_session_options {
+  int32_t fused_decode; /* 1: fused decode plan (default), 0: one kernel per reference node */
+  int32_t use_graph;    /* 1: replay decode steps as a HIP graph */
+} am_session_options;
+
+am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out);
+void am_session_destroy(am_session* s);
+/* Prefill the prompt (host ids) from position 0; returns the first generated token. */
+am_status_code am_session_prefill(am_session* s, const int64_t* prompt, int64_t n, int64_t* first_token);
+/* Run n decode steps (enqueued, no host sync between steps); copies the n generated
+ * tokens to tokens_out (host) at the end. */
+am_status_code am_session_decode(am_session* s, int64_t n, int64_t* tokens_out);
+/* Enqueue n decode steps without reading anything back (benchmark timing). */
+am_status_code am_session_decode_async(am_session* s, int64_t n);
+/* Prefill + greedy decode up to max_new tokens (stops after eos if eos >= 0). */
+am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
+                                   int64_t eos, int64_t* tokens_out, int64_t* n_out);
+/* fp32 logits [vocab] of the most recent step (host copy). */
+am_status_code am_session_logits(am_session* s, float* out);
+/* Current position (tokens committed to the KV cache). */
+int64_t am_session_position(am_session* s);
+/* Number of kernels launched per decode step by the active decode plan. */
+int64_t am_session_decode_plan_size(am_session* s);
+
+/* Per-op-type kernel time of eager decode steps, measured with HIP events on the
+ * session stream around every step of the decode plan.  Runs n steps eagerly and
+ * writes, for each executed step type, total milliseconds into ms_by_op[op_type]
+ * (array of at least 64 doubles, indexed by OpType) and launch counts into
+ * count_by_op. */
+am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by_op, int64_t* count_by_op);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

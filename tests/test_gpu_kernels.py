@@ -1,0 +1,353 @@
+"""Per-op parity of the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bars: bit-exact for synthetic data, quantize/dequantize, embedding gather, KV update
+and argmax; fp32 paths within 1e-3 relative and bf16 paths within 2e-2 relative of
+the oracle on the same inputs, measured against the largest
+reference magnitude of the tensor.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+import aethermind_amd.native as N  # noqa: E402
+import oracle_lib as O  # noqa: E402
+from gpu_util import (alloc_weight, bf16_dev, bits_host, dequant, dev, empty, host, p, pack_weight,  # noqa: E402
+                      stream, zeros)
+
+L = N.lib()
+TOL = {"f32": 1e-3, "bf16": 2e-2}
+
+
+def close(got, ref, tol, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.max(np.abs(ref)), 1e-30)
+    err = np.max(np.abs(got - ref)) / scale
+    assert err <= tol, f"{what}: max rel err {err:.3e} > {tol}"
+
+
+# ---------------------------------------------------------------- synthetic data
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_synth_normal_bitexact(dtype):
+    seed, tid, n, off = 1, (3 << 8) | 5, 100003, 7
+    out = empty((n,), torch.float32 if dtype == "f32" else torch.int16)
+    a = N.SynthArgs(seed, tid, 0.02, off, n, p(out), N.AM_DT_F32 if dtype == "f32" else N.AM_DT_BF16)
+    L.call("am_gfx950_synth_normal", a, stream())
+    if dtype == "f32":
+        ref = O.synth_f32(seed, tid, n, off)
+        assert np.array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+    else:
+        ref = O.synth_bf16(seed, tid, n, off)
+        assert np.array_equal(bits_host(out), ref)
+
+
+def test_synth_token_ids_bitexact():
+    out = empty((5000,), torch.int64)
+    L.call("am_gfx950_synth_token_ids", 1, 3, 128256, 5000, p(out), stream())
+    assert np.array_equal(host(out), O.token_ids(1, 3, 128256, 5000))
+
+
+# ---------------------------------------------------------------- quantization
+def _test_matrix(n, k, seed=11):
+    bits = O.synth_bf16(seed, 0x77, n * k).reshape(n, k)
+    w = O.bf16_to_f32(bits).copy()
+    w[3, :] = 0.0                      # all-zero row / groups
+    w[5, :128] = 0.0                   # one zero group
+    w[7, :] *= 1e-4                    # tiny scales (fp16 subnormal range)
+    w[9, 5] = 0.5                      # outlier
+    return O.round_bf16(w)
+
+
+@pytest.mark.parametrize("fmt", [N.AM_WF_INT8, N.AM_WF_INT4])
+def test_quantize_dequant_bitexact(fmt):
+    w = _test_matrix(48, 1024)
+    dw, _ = pack_weight(w, fmt, 128, src_bf16_bits=O.bf16_bits(w))
+    got = dequant(dw)
+    if fmt == N.AM_WF_INT8:
+        ref = O.dequant_int8(*O.quant_int8(w))
+    else:
+        pk, sc = O.quant_int4(w, 128)
+        ref = O.dequant_int4(pk, sc, 1024, 128)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_pack_int4_from_logical_matches_device_quantizer():
+    w = _test_matrix(32, 512)
+    pk, sc = O.quant_int4(w, 128)
+    w2, data, scales = alloc_weight(32, 512, N.AM_WF_INT4, 128)
+    lg, scd = dev(pk), dev(sc.view(np.int16))
+    L.call("am_gfx950_pack_int4", N.PackInt4Args(p(lg), p(scd), w2), stream())
+    assert np.array_equal(dequant(w2).view(np.uint32), O.dequant_int4(pk, sc, 512, 128).view(np.uint32))
+    # the device quantizer and the logical->tile conversion agree byte for byte
+    dq, keep = pack_weight(w, N.AM_WF_INT4, 128)
+    assert np.array_equal(host(keep[0]), host(data))
+    assert np.array_equal(host(keep[1]), host(scales))
+
+
+# ---------------------------------------------------------------- embedding
+@pytest.mark.parametrize("ids_dt", ["i32", "i64", "u32"])
+def test_embedding_kat_and_exact(ids_dt):
+    # reference KAT: ids {2,0,3} over a 4x3 table -> rows 7-9, 1-3, 10-12
+    table = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    npdt = {"i32": np.int32, "i64": np.int64, "u32": np.uint32}[ids_dt]
+    am = {"i32": N.AM_DT_I32, "i64": N.AM_DT_I64, "u32": N.AM_DT_U32}[ids_dt]
+    ids = dev(np.array([2, 0, 3], npdt)) if ids_dt != "u32" else dev(np.array([2, 0, 3], np.int32))
+    t = dev(table)
+    out = zeros((3, 3), torch.float32)
+    flag = zeros((1,), torch.int32)
+    L.call("am_gfx950_embedding", N.EmbeddingArgs(p(ids), am, 3, p(t), N.AM_DT_F32, 4, 3, p(out), N.AM_DT_F32,
+                                                  p(flag), 1), stream())
+    assert np.array_equal(host(out), table[[2, 0, 3]])
+
+
+def test_embedding_out_of_range_and_empty():
+    t = dev(np.ones((4, 8), np.float32))
+    out = zeros((2, 8), torch.float32)
+    flag = zeros((1,), torch.int32)
+    ids = dev(np.array([1, 4], np.int64))
+    with pytest.raises(N.NativeError) as e:
+        L.call("am_gfx950_embedding", N.EmbeddingArgs(p(ids), N.AM_DT_I64, 2, p(t), N.AM_DT_F32, 4, 8, p(out),
+                                                      N.AM_DT_F32, p(flag), 1), stream())
+    assert e.value.status == "OUT_OF_RANGE"
+    L.call("am_gfx950_embedding", N.EmbeddingArgs(None, N.AM_DT_I64, 0, p(t), N.AM_DT_F32, 4, 8, None, N.AM_DT_F32,
+                                                  None, 0), stream())
+
+
+def test_embedding_bf16_large_exact():
+    V, H = 1000, 4096
+    bits = O.synth_bf16(2, 0x01, V * H).reshape(V, H)
+    ids = O.token_ids(2, 0, V, 37)
+    out = empty((37, H), torch.int16)
+    idd, tab = dev(ids), bf16_dev(bits)
+    L.call("am_gfx950_embedding", N.EmbeddingArgs(p(idd), N.AM_DT_I64, 37, p(tab), N.AM_DT_BF16, V,
+                                                  H, p(out), N.AM_DT_BF16, None, 0), stream())
+    assert np.array_equal(bits_host(out), bits[ids])
+
+
+# ---------------------------------------------------------------- rmsnorm
+def test_rmsnorm_reference_kats():
+    x = dev(np.array([[1, 2, 3, 4], [0.5, 1, 1.5, 2], [4, 3, 2, 1]], np.float32))
+    for wv, exp in [([1, 1, 1, 1], [[0.365148, 0.730297, 1.095445, 1.460593]] * 2 + [[1.460593, 1.095445, 0.730297,
+                                                                                        0.365148]]),
+                    ([1, .5, 1.5, 2], None)]:
+        w = dev(np.array(wv, np.float32))
+        out = zeros((3, 4), torch.float32)
+        L.call("am_gfx950_rmsnorm", N.RmsNormArgs(p(x), p(w), p(out), 3, 4, 4, 4, 1e-5, 0, 0, 0), stream())
+        got = host(out)
+        if exp is not None:
+            np.testing.assert_allclose(got, np.array(exp), atol=1e-5)
+        else:
+            np.testing.assert_allclose(got[0], [0.365148, 0.365148, 1.643168, 2.921186], atol=1e-5)
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_rmsnorm_random(act):
+    rows, H = 7, 4096
+    x = O.synth_f32(3, 9, rows * H, std=1.0).reshape(rows, H)
+    w = 1.0 + O.synth_f32(3, 10, H, std=0.1)
+    if act == "bf16":
+        x, w = O.round_bf16(x), O.round_bf16(w)
+        xd, wd, out, dt = bf16_dev(O.bf16_bits(x)), bf16_dev(O.bf16_bits(w)), empty((rows, H), torch.int16), 1
+    else:
+        xd, wd, out, dt = dev(x), dev(w), empty((rows, H), torch.float32), 0
+    L.call("am_gfx950_rmsnorm", N.RmsNormArgs(p(xd), p(wd), p(out), rows, H, H, H, 1e-5, dt, dt, dt), stream())
+    got = O.bf16_to_f32(bits_host(out)) if act == "bf16" else host(out)
+    close(got, O.rmsnorm(x, w, 1e-5), TOL[act], "rmsnorm")
+
+
+# ---------------------------------------------------------------- linear
+def _weights(n, k, fmt, seed):
+    bits = O.synth_bf16(seed, 0x55, n * k).reshape(n, k)
+    if fmt == N.AM_WF_F32:
+        w = O.synth_f32(seed, 0x55, n * k).reshape(n, k)
+        dw, keep = pack_weight(w, fmt)
+        return w, dw, keep
+    w = O.bf16_to_f32(bits).copy()
+    dw, keep = pack_weight(w, fmt, 128, src_bf16_bits=bits)
+    if fmt == N.AM_WF_INT8:
+        w = O.dequant_int8(*O.quant_int8(w))
+    elif fmt == N.AM_WF_INT4:
+        pk, sc = O.quant_int4(w, 128)
+        w = O.dequant_int4(pk, sc, k, 128)
+    return w, dw, keep
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [N.AM_WF_F32, N.AM_WF_BF16, N.AM_WF_INT8, N.AM_WF_INT4])
+@pytest.mark.parametrize("nk", [(1376, 512), (1026, 4096), (512, 1536)])
+def test_linear_gemv(act, fmt, nk):
+    n, k = nk
+    wref, dw, keep = _weights(n, k, fmt, seed=5)
+    x = O.synth_f32(6, 1, k, std=1.0).reshape(1, k)
+    if act == "bf16":
+        x = O.round_bf16(x)
+        xd, out, dt = bf16_dev(O.bf16_bits(x)), empty((1, n), torch.int16), N.AM_DT_BF16
+    else:
+        xd, out, dt = dev(x), empty((1, n), torch.float32), N.AM_DT_F32
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), dt, 1, dw, p(out), dt, None, 1), stream())
+    got = O.bf16_to_f32(bits_host(out)) if act == "bf16" else host(out)
+    close(got, O.linear(x, wref), TOL[act], f"gemv act={act} fmt={fmt} {n}x{k}")
+
+
+@pytest.mark.parametrize("fmt", [N.AM_WF_BF16, N.AM_WF_INT8, N.AM_WF_INT4])
+@pytest.mark.parametrize("mnk", [(200, 384, 1024), (512, 1024, 4096), (17, 130, 256)])
+def test_linear_gemm_mfma(fmt, mnk):
+    m, n, k = mnk
+    wref, dw, keep = _weights(n, k, fmt, seed=7)
+    x = O.round_bf16(O.synth_f32(8, 2, m * k, std=1.0).reshape(m, k))
+    out = empty((m, n), torch.int16)
+    xd = bf16_dev(O.bf16_bits(x))
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2), stream())
+    got = O.bf16_to_f32(bits_host(out))
+    ref = O.linear(x, wref)
+    close(got, ref, TOL["bf16"], f"gemm fmt={fmt} {m}x{n}x{k}")
+    # per-row check so a transposed/misplaced tile cannot hide behind the global max
+    for r in (0, m // 2, m - 1):
+        close(got[r], ref[r], 3e-2, f"row {r}")
+
+
+def test_linear_residual_and_f32_logits():
+    n, k = 640, 512
+    wref, dw, keep = _weights(n, k, N.AM_WF_INT4, seed=9)
+    x = O.round_bf16(O.synth_f32(9, 3, k, std=1.0).reshape(1, k))
+    res = O.round_bf16(O.synth_f32(9, 4, n, std=1.0).reshape(1, n))
+    rd = bf16_dev(O.bf16_bits(res))
+    out = empty((1, n), torch.int16)
+    xd = bf16_dev(O.bf16_bits(x))
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), 1, 1, dw, p(out), 1, p(rd), 1), stream())
+    ref = O.round_bf16(res + O.round_bf16(O.linear(x, wref)))
+    close(O.bf16_to_f32(bits_host(out)), ref, TOL["bf16"], "residual")
+    lo = empty((1, n), torch.float32)
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), 1, 1, dw, p(lo), 0, None, 1), stream())
+    close(host(lo), O.linear(x, wref), 1e-3, "fp32 logits")
+
+
+# ---------------------------------------------------------------- rope / kv / attention
+def test_rope_tables_match_oracle_and_rotation():
+    P, d = 300, 128
+    c = np.empty((P, d // 2), np.float32)
+    s = np.empty((P, d // 2), np.float32)
+    L.call("am_gfx950_rope_table", P, d, 500000.0, c.ctypes.data, s.ctypes.data)
+    co, so = O.rope_tables(P, d, 500000.0)
+    assert np.array_equal(c, co) and np.array_equal(s, so)
+    S, hq, hkv = 5, 4, 2
+    q = O.synth_f32(4, 1, S * hq * d, std=1.0).reshape(S, hq * d)
+    k = O.synth_f32(4, 2, S * hkv * d, std=1.0).reshape(S, hkv * d)
+    pos = np.array([0, 1, 17, 200, 299], np.int64)
+    for act in ("f32", "bf16"):
+        qq, kk = (q, k) if act == "f32" else (O.round_bf16(q), O.round_bf16(k))
+        if act == "f32":
+            qd, kd = dev(qq), dev(kk)
+        else:
+            qd, kd = bf16_dev(O.bf16_bits(qq)), bf16_dev(O.bf16_bits(kk))
+        posd, cd, sd = dev(pos), dev(c), dev(s)
+        a = N.RopeArgs(p(qd), p(kd), p(qd), p(kd), p(posd), p(cd), p(sd), S, hq, hkv, d, P, 0 if act == "f32" else 1)
+        L.call("am_gfx950_rope", a, stream())
+        gq = host(qd) if act == "f32" else O.bf16_to_f32(bits_host(qd))
+        gk = host(kd) if act == "f32" else O.bf16_to_f32(bits_host(kd))
+        close(gq, O.rope(qq, hq, d, pos, co, so), TOL[act], "rope q")
+        close(gk, O.rope(kk, hkv, d, pos, co, so), TOL[act], "rope k")
+
+
+def test_kv_update_exact():
+    S, hkv, d, cap = 6, 2, 64, 32
+    k = O.synth_f32(5, 1, S * hkv * d).reshape(S, hkv * d)
+    v = O.synth_f32(5, 2, S * hkv * d).reshape(S, hkv * d)
+    kc = zeros((hkv, cap, d), torch.float32)
+    vc = zeros((hkv, cap, d), torch.float32)
+    kd, vd = dev(k), dev(v)
+    a = N.KvUpdateArgs(p(kd), p(vd), p(kc), p(vc), S, hkv, d, cap, 10, None, 0, None)
+    L.call("am_gfx950_kv_update", a, stream())
+    gk = host(kc)
+    for s in range(S):
+        for h in range(hkv):
+            assert np.array_equal(gk[h, 10 + s], k[s, h * d:(h + 1) * d])
+    assert not gk[:, :10].any() and not gk[:, 16:].any()
+    with pytest.raises(N.NativeError) as e:
+        L.call("am_gfx950_kv_update", N.KvUpdateArgs(p(kd), p(vd), p(kc), p(vc), S, hkv, d, cap, 30, None, 0, None),
+               stream())
+    assert e.value.status == "OUT_OF_RANGE"
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("case", [("decode", 1, 300, 0), ("decode_splits", 1, 777, 16), ("prefill", 37, 0, 0),
+                                  ("chunk", 29, 50, 0)])
+def test_attention(act, d, case):
+    name, S, start, splits = case
+    hq, hkv, cap = 8, 2, 1024
+    q = O.synth_f32(6, 1, S * hq * d, std=1.0).reshape(S, hq * d)
+    kc = O.synth_f32(6, 2, hkv * cap * d, std=1.0).reshape(hkv, cap, d)
+    vc = O.synth_f32(6, 3, hkv * cap * d, std=1.0).reshape(hkv, cap, d)
+    if act == "bf16":
+        q, kc, vc = O.round_bf16(q), O.round_bf16(kc), O.round_bf16(vc)
+        qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+        out = empty((S, hq * d), torch.int16)
+    else:
+        qd, kd, vd = dev(q), dev(kc), dev(vc)
+        out = empty((S, hq * d), torch.float32)
+    wsb = L.am_gfx950_attention_workspace_bytes(1, S, hq, hkv, d, cap, splits)
+    ws = zeros((wsb,), torch.uint8)
+    a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), S, hq, hkv, d, cap, start, None, 1, 0, 0 if act == "f32" else 1,
+                        splits, p(ws), wsb)
+    for _ in range(2):  # second call checks the tickets were left at zero
+        L.call("am_gfx950_attention", a, stream())
+        got = host(out) if act == "f32" else O.bf16_to_f32(bits_host(out))
+        close(got, O.attention(q, kc, vc, S, hq, hkv, d, cap, start), TOL[act], f"attention {name}")
+
+
+def test_attention_special_cases():
+    # one position -> out = V row; identical keys -> out = mean of V over the window
+    hq, hkv, d, cap = 4, 1, 64, 64
+    q = O.synth_f32(7, 1, hq * d, std=1.0).reshape(1, hq * d)
+    kc = np.zeros((hkv, cap, d), np.float32)
+    vc = O.synth_f32(7, 2, hkv * cap * d, std=1.0).reshape(hkv, cap, d)
+    out = empty((1, hq * d), torch.float32)
+    ws = zeros((1 << 20,), torch.uint8)
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    for start, expect in [(0, np.tile(vc[0, 0], hq)), (9, np.tile(vc[0, :10].mean(0), hq))]:
+        a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), 1, hq, hkv, d, cap, start, None, 1, 0, 0, 3, p(ws), 1 << 20)
+        L.call("am_gfx950_attention", a, stream())
+        np.testing.assert_allclose(host(out)[0], expect, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- elementwise / argmax
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_silu_mul_and_add(act):
+    n = 14336
+    g = O.synth_f32(8, 1, n, std=3.0)
+    u = O.synth_f32(8, 2, n, std=1.0)
+    g[:4] = [0.0, -100.0, 100.0, -1e-8]
+    if act == "bf16":
+        g, u = O.round_bf16(g), O.round_bf16(u)
+        gd, ud, out, dt = bf16_dev(O.bf16_bits(g)), bf16_dev(O.bf16_bits(u)), empty((n,), torch.int16), 1
+        cv = lambda t: O.bf16_to_f32(bits_host(t))  # noqa: E731
+    else:
+        gd, ud, out, dt = dev(g), dev(u), empty((n,), torch.float32), 0
+        cv = host
+    L.call("am_gfx950_silu_mul", N.SiluMulArgs(p(gd), p(ud), p(out), n, dt), stream())
+    close(cv(out), O.silu_mul(g, u), TOL[act] if act == "bf16" else 1e-6, "silu_mul")
+    L.call("am_gfx950_add", N.AddArgs(p(gd), p(ud), p(out), n, dt), stream())
+    close(cv(out), g + u, TOL[act] if act == "bf16" else 1e-7, "add")
+
+
+def test_argmax_exact_ties_nan():
+    rows, n = 3, 128256
+    x = O.synth_f32(9, 1, rows * n, std=1.0).reshape(rows, n)
+    x[0, 5000] = x[0, 100000] = 50.0           # tie -> lowest index
+    x[1, :] = np.nan
+    x[1, 77] = -3.0                            # NaN never selected
+    x[2, 0] = np.inf                           # +inf is a value
+    xd = dev(x)
+    out = empty((rows,), torch.int64)
+    wsb = L.am_gfx950_argmax_workspace_bytes(rows)
+    ws = zeros((wsb,), torch.uint8)
+    for _ in range(2):
+        L.call("am_gfx950_argmax", N.ArgmaxArgs(p(xd), 0, rows, n, p(out), p(ws), wsb), stream())
+        assert list(host(out)) == [O.argmax(x[r]) for r in range(rows)] == [5000, 77, 0]
