@@ -750,6 +750,28 @@ void am_runtime_destroy(am_runtime* rt) {
 
 void* am_runtime_stream(am_runtime* rt) { return rt ? rt->stream : nullptr; }
 
+am_status_code am_runtime_synchronize(am_runtime* rt) {
+  if (!rt) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "runtime: null");
+  const hipError_t e = hipStreamSynchronize(rt->stream);
+  if (e != hipSuccess) return am::SetLastError(AM_STATUS_INTERNAL, hipGetErrorString(e));
+  return AM_STATUS_OK;
+}
+
+am_status_code am_synth_token_ids_host(uint64_t seed, uint64_t stream, int64_t vocab, int64_t n, int64_t* out) {
+  if (vocab <= 0 || n < 0 || (n > 0 && out == nullptr))
+    return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "synth_token_ids_host: bad argument");
+  auto mix = [](uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  };
+  const uint64_t key = mix(mix(seed) ^ (0xF00D0000ull + stream));
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = static_cast<int64_t>(((mix(key + static_cast<uint64_t>(i)) >> 32) * static_cast<uint64_t>(vocab)) >> 32);
+  return AM_STATUS_OK;
+}
+
 am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* cfg, uint64_t seed, am_model** out) {
   if (!rt || !cfg || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model: null argument");
   auto m = std::make_unique<am_model>();

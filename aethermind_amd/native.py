@@ -161,6 +161,8 @@ _SIGS = {
     "am_runtime_create": (i32, [i32, C.POINTER(vp)]),
     "am_runtime_destroy": (None, [vp]),
     "am_runtime_stream": (vp, [vp]),
+    "am_runtime_synchronize": (i32, [vp]),
+    "am_synth_token_ids_host": (i32, [u64, u64, i64, i64, vp]),
     "am_model_create_synthetic": (i32, [vp, C.POINTER(ModelConfig), u64, C.POINTER(vp)]),
     "am_model_destroy": (None, [vp]),
     "am_model_weight": (i32, [vp, i32, i32, C.POINTER(Weight)]),

@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark: batch-1 greedy decode tokens/s of the Llama-3-8B-shaped INT4 model on one
+MI355X (32 layers, hidden 4096, 32/8 heads, head_dim 128,
+FFN 14336, vocab 128256, theta 5e5, INT4 group-128 fp16 scales, batch 1, prompt 512,
+decode 256), plus the weight-GEMV HBM roofline and the CPU oracle baseline.
+
+One "step" = one decode token through the fused decode plan (embedding, 32 x
+[norm+qkv+rope+kv, attention, o+add, norm+gate/up+silu, down+add], norm+lm_head+argmax),
+replayed as a HIP graph from device-resident state.  Inputs (weights, KV cache, prompt
+state) are resident in HBM before the timed region; the timed region is K graph replays
+bracketed by device synchronisation.
+
+Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+CONFIGS = {
+    "int4": dict(weight_format=3, name="llama3-8b-shape-int4-g128", decode=256),
+    "int8": dict(weight_format=2, name="llama3-8b-shape-int8-perchannel", decode=128),
+    "bf16": dict(weight_format=1, name="llama3-8b-shape-bf16", decode=128),
+}
+SHAPE = dict(num_layers=32, hidden=4096, num_q_heads=32, num_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+             rms_eps=1e-5, rope_theta=500000.0)
+# OpType values of the fused decode steps (host/am_core.h)
+OP_NAMES = {1: "Embedding", 2: "RmsNorm", 3: "Linear", 5: "RoPE", 6: "Attention", 8: "SiluMul", 10: "KVCacheUpdate",
+            11: "Add", 13: "Argmax", 17: "FusedRmsNormQkvRoPEKVUpdate", 18: "FusedLinearAdd",
+            19: "FusedRmsNormGateUpSiluMul", 20: "FusedRmsNormLmHeadArgmax", 21: "EmbedToken"}
+GEMV_OPS = (17, 18, 19, 20)
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(weight_format: int, seconds_budget: float = 20.0):
+    """Oracle restatement of the reference CPU path (AVX2 dot product inner loop,
+    dequantize-on-the-fly rows), 1 thread, on a bounded sample of the same decode
+    workload: one 8B-shape layer + the full lm_head, timed per decode token at
+    position ~512, then scaled to the 32-layer token (t_token = t_rest + 32 * t_layer)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+
+    import oracle_lib as O
+
+    L = O.lib()
+    res = {}
+    for layers in (1, 2):
+        cfg = dict(SHAPE, num_layers=layers, act="bf16", weight_format=weight_format, group_size=128, max_tokens=600)
+        L.orc_set_threads(min(16, os.cpu_count() or 1))     # weight generation only (untimed)
+        m = O.OracleModel(cfg, 1)
+        m.set_fast(True)
+        L.orc_set_threads(1)
+        prompt = O.token_ids(1, 0, SHAPE["vocab"], 4)
+        m.forward(prompt, 508)                                # fill a few cache rows near position 512
+        times = []
+        t_start = time.perf_counter()
+        tok = np.array([int(prompt[-1])], np.int64)
+        pos = 512
+        while len(times) < 3 and time.perf_counter() - t_start < seconds_budget / 2:
+            t0 = time.perf_counter()
+            m.forward(tok, pos)
+            times.append(time.perf_counter() - t0)
+            pos += 1
+        res[layers] = min(times)
+        m.close()
+    t_layer = max(res[2] - res[1], 1e-9)
+    t_rest = max(res[1] - t_layer, 0.0)
+    t_token = t_rest + SHAPE["num_layers"] * t_layer
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(1.0 / t_token, 4),
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"oracle AVX2 path, 1 thread on {cpu} (nproc={os.cpu_count()}): decode tokens at pos 512 of "
+                   f"1-layer and 2-layer 8B-shape models with the full lm_head; t_layer={t_layer*1e3:.1f} ms, "
+                   f"t_rest={t_rest*1e3:.1f} ms, scaled to 32 layers = {t_token*1e3:.0f} ms/token"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: config decode length)")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="int4", choices=sorted(CONFIGS))
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs the decode path on one GPU only; --gpus must be 1 "
+              "(multi-GPU sharding is described in DESIGN.md, not implemented)", file=sys.stderr)
+        sys.exit(2)
+
+    import aethermind_amd.native as N
+
+    L = N.lib()
+    cfgd = CONFIGS[args.config]
+    steps = args.steps if args.steps is not None else cfgd["decode"]
+    max_tokens = 4096
+    if args.prompt + args.warmup + steps + args.profile_steps + 2 > max_tokens:
+        raise SystemExit("prompt + warmup + steps + profile exceed the 4096-token KV cache")
+
+    rt = N.vp()
+    L.call("am_runtime_create", 0, C.byref(rt))
+    mc = N.ModelConfig(SHAPE["num_layers"], SHAPE["hidden"], SHAPE["num_q_heads"], SHAPE["num_kv_heads"],
+                       SHAPE["head_dim"], SHAPE["ffn"], SHAPE["vocab"], SHAPE["rms_eps"], SHAPE["rope_theta"],
+                       N.AM_DT_BF16, cfgd["weight_format"], 128, max_tokens, 512)
+    t0 = time.perf_counter()
+    m = N.vp()
+    L.call("am_model_create_synthetic", rt, C.byref(mc), 1, C.byref(m))
+    log(f"model {cfgd['name']} created in {time.perf_counter() - t0:.1f}s; linear weight bytes/token "
+        f"{L.am_model_weight_bytes_total(m)}")
+    s = N.vp()
+    L.call("am_session_create", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
+
+    import numpy as np
+    prompt = np.empty(args.prompt, np.int64)
+    # prompt ids of the build SPEC (seed 1, stream 0)
+    L.call("am_synth_token_ids_host", 1, 0, SHAPE["vocab"], args.prompt, prompt.ctypes.data)
+
+    def sync():
+        L.call("am_runtime_synchronize", rt)
+
+    first = N.i64()
+    L.call("am_session_prefill", s, prompt.ctypes.data, prompt.size, C.byref(first))  # warm (JIT/caches)
+    t0 = time.perf_counter()
+    L.call("am_session_prefill", s, prompt.ctypes.data, prompt.size, C.byref(first))
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {args.prompt} tokens: {prefill_s*1e3:.1f} ms ({args.prompt/prefill_s:.0f} tok/s), first token "
+        f"{first.value}")
+
+    warm = np.zeros(max(args.warmup, 1), np.int64)
+    L.call("am_session_decode", s, max(args.warmup, 1), warm.ctypes.data)  # captures + replays the graph
+    L.call("am_session_decode", s, 0, None)
+    sync()
+
+    t0 = time.perf_counter()
+    L.call("am_session_decode_async", s, steps)
+    sync()
+    L.call("am_session_decode", s, 0, None)
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / steps
+    tok_s = steps / dt
+    log(f"decode: {steps} tokens in {dt*1e3:.1f} ms -> {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/token), "
+        f"{L.am_session_decode_plan_size(s)} kernels/token")
+
+    # Per-kernel durations: HIP events around every step of the same decode plan on the
+    # session stream (eager replay of the plan, adjacent to the timed region).
+    ms_by_op = (C.c_double * 64)()
+    cnt_by_op = (C.c_int64 * 64)()
+    L.call("am_session_profile_decode", s, args.profile_steps, ms_by_op, cnt_by_op)
+    breakdown = {OP_NAMES.get(i, str(i)): {"ms_per_token": round(ms_by_op[i] / args.profile_steps, 4),
+                                           "launches_per_token": cnt_by_op[i] // args.profile_steps}
+                 for i in range(64) if cnt_by_op[i]}
+    gemv_ms = sum(ms_by_op[i] for i in GEMV_OPS) / args.profile_steps
+    gemv_launches = sum(cnt_by_op[i] for i in GEMV_OPS) // args.profile_steps
+    weight_bytes = L.am_model_weight_bytes_total(m)
+    achieved = weight_bytes / (gemv_ms * 1e-3) / 1e9
+    log(f"weight GEMVs: {gemv_ms:.3f} ms/token over {gemv_launches} launches -> {achieved:.0f} GB/s "
+        f"({achieved / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f})")
+    for k, v in breakdown.items():
+        log(f"  {k:32s} {v['ms_per_token']:8.4f} ms/token  x{v['launches_per_token']}")
+
+    plan_size = L.am_session_decode_plan_size(s)
+    L.am_session_destroy(s)
+    L.am_model_destroy(m)
+    L.am_runtime_destroy(rt)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(cfgd["weight_format"])
+            log(f"cpu baseline: {cpu['value']} tok/s ({cpu['sample']})")
+        except Exception as e:  # the GPU figures stand without it
+            log(f"cpu baseline failed: {e}")
+
+    out = {
+        "metric": "batch-1 decode tokens/sec, Llama-3-8B-shape INT4; GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"int4": "int4-w/bf16-act/fp32-acc", "int8": "int8-w/bf16-act/fp32-acc",
+                  "bf16": "bf16"}[args.config],
+        "data": "synthetic (seeded N(0,0.02) weights generated on device, seeded uniform prompt ids)",
+        "config": {"workload": f"{cfgd['name']} batch-1 greedy decode, prompt {args.prompt}, "
+                               f"{steps} timed decode tokens after {args.warmup} warmup, KV cache 4096 bf16",
+                   "model": cfgd["name"], "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
+                   "prefill_ms": round(prefill_s * 1e3, 2), "kernels_per_token": plan_size},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel (weight-only INT4 dequant GEMV, all 4 fused epilogues)",
+                     "bytes_per_token": weight_bytes, "gemv_ms_per_token": round(gemv_ms, 4),
+                     "launches_per_token": gemv_launches},
+        "breakdown": breakdown,
+        "cpu_baseline": cpu,
+        "host": platform.node(),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

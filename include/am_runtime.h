@@ -63,6 +63,13 @@ typedef enum am_model_buffer_kind {
 am_status_code am_runtime_create(int32_t device, am_runtime** out);
 void am_runtime_destroy(am_runtime* rt);
 void* am_runtime_stream(am_runtime* rt); /* hipStream_t */
+/* Blocks until all work enqueued on the runtime's stream has finished; reports an
+ * asynchronous device error as AM_STATUS_INTERNAL. */
+am_status_code am_runtime_synchronize(am_runtime* rt);
+
+/* Prompt ids of the synthetic-data SPEC computed on the host (same integer stream
+ * as am_gfx950_synth_token_ids): uniform in [0, vocab). */
+am_status_code am_synth_token_ids_host(uint64_t seed, uint64_t stream, int64_t vocab, int64_t n, int64_t* out);
 
 /* Synthetic Llama-dense weights of the build SPEC (seeded normal(0, 0.02), norm gains
  * 1.0) generated and repacked on the device. */

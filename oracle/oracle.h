@@ -121,6 +121,8 @@ int orc_model_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, in
 int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, float* logits);
 /* use the AVX2 fp32 kernels (the reference's fast path) instead of the fp64 scalar forms */
 void orc_model_set_fast(orc_model* m, int32_t fast);
+/* OpenMP threads used by the oracle's parallel loops (cpu_baseline uses 1). */
+void orc_set_threads(int32_t n);
 
 #ifdef __cplusplus
 }

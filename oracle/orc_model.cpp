@@ -11,6 +11,8 @@
 
 #include "oracle.h"
 
+#include <omp.h>
+
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -71,14 +73,18 @@ QWeight MakeWeight(uint64_t seed, uint64_t tid, int64_t n, int64_t k, int fmt, i
   }
   std::vector<float> f(count);
   for (size_t i = 0; i < count; ++i) f[i] = orc_bf16_to_f32(b[i]);
+  // Rows are independent: quantize them in parallel (same result as one call).
   if (fmt == 2) {
     w.q8.resize(count);
     w.s8.resize(static_cast<size_t>(n));
-    orc_quant_int8(f.data(), n, k, w.q8.data(), w.s8.data());
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n; ++r) orc_quant_int8(f.data() + r * k, 1, k, w.q8.data() + r * k, w.s8.data() + r);
   } else {
     w.q4.resize(count / 2);
     w.s4.resize(static_cast<size_t>(n * (k / group)));
-    orc_quant_int4(f.data(), n, k, group, w.q4.data(), w.s4.data());
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n; ++r)
+      orc_quant_int4(f.data() + r * k, 1, k, group, w.q4.data() + r * (k / 2), w.s4.data() + r * (k / group));
   }
   return w;
 }
@@ -190,6 +196,8 @@ orc_model* orc_model_create_synthetic(const orc_model_config* cfg, uint64_t seed
 void orc_model_destroy(orc_model* m) { delete m; }
 
 void orc_model_set_fast(orc_model* m, int32_t fast) { m->fast = fast; }
+
+void orc_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, float* logits) {
   const orc_model_config& c = m->cfg;

@@ -55,6 +55,7 @@ _SIGS = {
     "orc_model_generate": (i32, [vp, vp, i64, i64, vp, vp]),
     "orc_model_forward": (i32, [vp, vp, i64, i64, vp]),
     "orc_model_set_fast": (None, [vp, i32]),
+    "orc_set_threads": (None, [i32]),
 }
 
 _lib = None
