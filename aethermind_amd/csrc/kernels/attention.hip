@@ -34,6 +34,9 @@ struct AttnArgs {
   unsigned* tickets;
 };
 
+// Fewest cache positions one split block handles (short contexts use fewer splits).
+constexpr int64_t kMinPerSplit = 32;
+
 template <class A>
 __device__ __forceinline__ void load8(const typename A::T* p, float* out) {
   if constexpr (A::kDtype == AM_DT_BF16) {
@@ -80,7 +83,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const int split = blockIdx.x;
   const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
   const int64_t n_keys = start + s + 1 <= p.cap ? start + s + 1 : p.cap;
-  const int64_t per = (n_keys + p.splits - 1) / p.splits;
+  // Splits actually used for this row: at least kMinPerSplit positions each, so
+  // short contexts do not pay for merging many near-empty partials.  Every block of
+  // the (row, kv head) group computes the same count; surplus blocks leave at once.
+  int64_t nsplit = (n_keys + kMinPerSplit - 1) / kMinPerSplit;
+  if (nsplit > p.splits) nsplit = p.splits;
+  if (nsplit < 1) nsplit = 1;
+  if (split >= nsplit) return;
+  const int64_t per = (n_keys + nsplit - 1) / nsplit;
   const int64_t lo = split * per;
   const int64_t hi = lo + per < n_keys ? lo + per : n_keys;
 
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     for (int w = 1; w < 4; ++w)
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) merge_state(m[hh], l[hh], o[hh], sm_m[w][hh], sm_l[w][hh], &sm_o[w][hh][sub * 8]);
-    if (p.splits == 1) {
+    if (nsplit == 1) {
       T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G) * D + sub * 8;
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) {
@@ -177,48 +187,45 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
       __threadfence();
     }
   }
-  if (p.splits == 1) return;
+  if (nsplit == 1) return;
   __syncthreads();
   if (threadIdx.x == 0) {
     __threadfence();
     const unsigned t = atomicAdd(&p.tickets[qr * p.hkv + g], 1u);
-    last = (t == static_cast<unsigned>(p.splits - 1));
+    last = (t == static_cast<unsigned>(nsplit - 1));
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
-  if (wave == 0 && ps == 0) {
-    float fm[G], fl[G], fo[G][8];
+  __threadfence();  // acquire: the other blocks' partial records are visible now
+  // Parallel merge: thread t owns head t / (D / DPT) and DPT consecutive dims; every
+  // split's record is read with plain (pipelined) loads.
+  constexpr int DPT = (D * G) / 256 > 0 ? (D * G) / 256 : 1;
+  constexpr int TPH = D / DPT;  // threads per head
+  const int hh = threadIdx.x / TPH;
+  const int d0 = (threadIdx.x % TPH) * DPT;
+  if (hh < G) {
+    const float* base = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2) + hh * (D + 2);
+    float mx = -INFINITY;
+    for (int64_t sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, base[sp * G * (D + 2)]);
+    float den = 0.0f;
+    float acc[DPT];
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      fm[hh] = -INFINITY;
-      fl[hh] = 0.0f;
+    for (int i = 0; i < DPT; ++i) acc[i] = 0.0f;
+    if (mx != -INFINITY) {
+      for (int64_t sp = 0; sp < nsplit; ++sp) {
+        const float* rec = base + sp * G * (D + 2);
+        const float c = expf(rec[0] - mx);
+        den = fmaf(rec[1], c, den);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) fo[hh][i] = 0.0f;
-    }
-    const float* base = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
-    for (int sp = 0; sp < p.splits; ++sp) {
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        const float* rec = base + (sp * G + hh) * (D + 2);
-        const float m2 = __hip_atomic_load(rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float l2 = __hip_atomic_load(rec + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float o2[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          o2[i] = __hip_atomic_load(rec + 2 + sub * 8 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        merge_state(fm[hh], fl[hh], fo[hh], m2, l2, o2);
+        for (int i = 0; i < DPT; ++i) acc[i] = fmaf(rec[2 + d0 + i], c, acc[i]);
       }
     }
-    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G) * D + sub * 8;
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D + d0;
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      const float inv = fl[hh] > 0.0f ? 1.0f / fl[hh] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) A::store(out + hh * D, i, fo[hh][i] * inv);
-    }
-    if (sub == 0) p.tickets[qr * p.hkv + g] = 0u;
+    for (int i = 0; i < DPT; ++i) A::store(out, i, acc[i] * inv);
   }
+  if (threadIdx.x == 0) p.tickets[qr * p.hkv + g] = 0u;
 }
 
 int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {

@@ -2,19 +2,23 @@
 //
 // Layout of one launch:
 //   * 256-thread blocks (4 wave64s).  The block stages the activation vector x (K
-//     values) in LDS once, optionally applying the fused RMSNorm prologue, plus the
-//     per-32-k partial sums of x used to undo the weight offset encoding.
-//   * Work unit = 2 output rows.  Each wave takes units u = gw, gw+TW, ... and reads
-//     both rows with all 64 lanes: lane l owns the 16-byte chunks l, l+64, ... of a
-//     row, so every load instruction of the wave covers 1 KiB of contiguous weights
-//     (fully coalesced 128-bit loads).  Up to 4 chunk-steps x 2 rows are issued
-//     before any arithmetic to keep bytes in flight.
+//     values) in LDS once, optionally applying the fused RMSNorm prologue, together
+//     with one offset-correction term per 16-byte weight chunk.
+//   * Work unit = a pair of output rows (RoPE pair, gate/up pair or two plain rows);
+//     an iteration of a wave handles P pairs.  All 64 lanes of the wave read every
+//     row: lane l owns the 16-byte chunks l, l+64, ... of each row, so each load
+//     instruction moves 1 KiB of contiguous weights.  The lane -> chunk map is fixed,
+//     so each lane copies its share of x from LDS into registers once and the inner
+//     loop touches no LDS at all.
+//   * For short rows (K <= 8192 INT4) the next iteration's weight loads are issued
+//     before the current one is reduced (two register buffers), so every wave keeps
+//     its rows' bytes in flight; long rows keep all their chunks in flight instead.
 //   * Unpack is in registers: INT4 nibbles hold q+8, and (word >> 4t) & 0x000F000F
 //     | 0x43004300 is the bf16 pair (136+q_even, 136+q_odd), fed to
 //     v_dot2c_f32_bf16 with the bf16 activations; sum(x*(136+q)) - 136*sum(x) gives
-//     sum(x*q) in fp32.  INT8 bytes hold q+128 and go through byte->float converts.
-//   * The two row sums are reduced across the wave with xor shuffles; the epilogue
-//     applies the reference op-boundary roundings of whatever nodes were fused.
+//     sum(x*q) in fp32, then the fp16 group scale is applied per chunk.
+//   * Row sums are reduced with DPP row rotations plus four readlanes; the epilogue
+//     applies the reference op-boundary roundings of the nodes that were fused.
 
 #include <cmath>
 
@@ -35,7 +39,7 @@ struct GemvArgs {
   const void* scales;
   int64_t n, k;
   int32_t group;
-  int64_t units;
+  int64_t units;  // row pairs
   int64_t row_bytes;
   void* out;
   const void* residual;
@@ -57,8 +61,6 @@ struct GemvArgs {
   int32_t out_f32;
 };
 
-constexpr int kJB = 4;  // chunk-steps issued together
-
 // k values per 16-byte chunk of a weight row
 template <int WF> struct Fmt;
 template <> struct Fmt<AM_WF_F32> { static constexpr int kc = 4; static constexpr float off = 0.0f; };
@@ -66,45 +68,39 @@ template <> struct Fmt<AM_WF_BF16> { static constexpr int kc = 8; static constex
 template <> struct Fmt<AM_WF_INT8> { static constexpr int kc = 16; static constexpr float off = 128.0f; };
 template <> struct Fmt<AM_WF_INT4> { static constexpr int kc = 32; static constexpr float off = 8.0f; };
 
-// LDS holds x as bf16 only where the dot uses v_dot2c_f32_bf16 (bf16 act with
+// x is kept as bf16 only where the dot uses v_dot2c_f32_bf16 (bf16 activations with
 // bf16 or INT4 weights); elsewhere as fp32.
 template <class A, int WF> struct XStore {
   static constexpr bool kBF16 = A::kDtype == AM_DT_BF16 && (WF == AM_WF_INT4 || WF == AM_WF_BF16);
   static constexpr int kBytes = kBF16 ? 2 : 4;
-  // effective offset subtracted per chunk: the bf16 INT4 path adds the 128 exponent bias
+  static constexpr int kDW = Fmt<WF>::kc * kBytes / 4;  // dwords of x per weight chunk
+  // offset subtracted per chunk: the bf16 INT4 path also carries the 128 exponent bias
   static constexpr float kOff = (kBF16 && WF == AM_WF_INT4) ? 136.0f : Fmt<WF>::off;
 };
 
 __device__ __forceinline__ bf16x2_t as_bf2(uint32_t u) { return __builtin_bit_cast(bf16x2_t, u); }
 
-// Dot of one 16-byte weight chunk with the matching x values in LDS (chunk c).
+// Dot of one 16-byte weight chunk with its x values (kDW dwords at xd).
 template <class A, int WF>
-__device__ __forceinline__ float chunk_dot(const uint4 w, const uint8_t* xl, int64_t c) {
+__device__ __forceinline__ float chunk_dot(const uint4 w, const uint32_t* xd) {
   using XS = XStore<A, WF>;
-  constexpr int kc = Fmt<WF>::kc;
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
   float acc = 0.0f;
   if constexpr (XS::kBF16) {
-    const uint4* xp = reinterpret_cast<const uint4*>(xl + c * kc * 2);
     if constexpr (WF == AM_WF_INT4) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint4 xv = xp[t];
-        const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
           const uint32_t pair = ((ws[t] >> (4 * pp)) & 0x000F000Fu) | 0x43004300u;
-          acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[pp]), as_bf2(pair), acc, false);
+          acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[4 * t + pp]), as_bf2(pair), acc, false);
         }
-      }
     } else {  // BF16 weights
-      const uint4 xv = xp[0];
-      const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[t]), as_bf2(ws[t]), acc, false);
     }
   } else {
-    const float* xf = reinterpret_cast<const float*>(xl) + c * kc;
+    const float* xf = reinterpret_cast<const float*>(xd);
     if constexpr (WF == AM_WF_F32) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc = fmaf(xf[t], __uint_as_float(ws[t]), acc);
@@ -133,24 +129,118 @@ __device__ __forceinline__ float chunk_dot(const uint4 w, const uint8_t* xl, int
   return acc;
 }
 
+// Sum over the 64 lanes: DPP inside each 16-lane row (quad swaps, then row
+// rotations by 4 and 8), then the four row sums through readlane.  The result is
+// wave-uniform.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+  const int b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
 __device__ __forceinline__ float silu_ref(float g) {
   if (g >= 0.0f) return g / (1.0f + expf(-g));
   const float e = expf(g);
   return g * e / (1.0f + e);
 }
 
-template <class A, int WF, bool NORM, int EPI>
+// rows of pair u
+template <int EPI>
+__device__ __forceinline__ void pair_rows(const GemvArgs& p, int64_t u, int64_t& r0, int64_t& r1) {
+  if constexpr (EPI == kEpiQkv) {
+    const int64_t half = p.d / 2;
+    const int64_t head = u / half, i = u % half;
+    r0 = head * p.d + i;
+    r1 = r0 + half;
+  } else if constexpr (EPI == kEpiGateUp) {
+    r0 = u;  // gate row u, up row u: rows [0, F) are gate, [F, 2F) are up
+    r1 = u + p.n / 2;
+  } else {
+    r0 = 2 * u;
+    r1 = 2 * u + 1;
+  }
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// One load block: JB chunk-steps of both rows of P pairs (+ INT4 group scales).
+template <int JB, int P, bool SC>
+struct Frag {
+  uint4 w[P][2][JB];
+  float s[P][2][SC ? JB : 1];
+};
+
+// Streaming 16-byte weight load (read once per token: non-temporal hint).
+__device__ __forceinline__ uint4 ld_stream(const uint8_t* row, int64_t c) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(row) + c);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <class A, int WF, bool NORM, int EPI, int JM, int P>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   using XS = XStore<A, WF>;
   using T = typename A::T;
   constexpr int kc = Fmt<WF>::kc;
+  constexpr int XDW = XS::kDW;
+  constexpr bool SC = WF == AM_WF_INT4;
+  constexpr int JB = JM < 8 ? JM : 8;  // chunk-steps per load block
+  constexpr int NB = JM / JB;          // load blocks per row
+  constexpr bool PIPE = NB == 1 && JM <= 4;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
   const int64_t K = p.k;
-  uint8_t* xl = smem;                                                     // x (LDS)
-  float* xsum = reinterpret_cast<float*>(smem + ((K * XS::kBytes + 15) / 16) * 16);  // per-chunk sums
+  const int64_t C = p.row_bytes / 16;  // chunks per row
+  const int J = static_cast<int>((C + 63) / 64);
+  uint8_t* xl = smem;
+  float* corr_lds = reinterpret_cast<float*>(smem + ((K * XS::kBytes + 15) / 16) * 16);
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t niter = (p.units + P - 1) / P;
+  const int ng = (WF == AM_WF_INT4) ? static_cast<int>(K / p.group) : 1;
+  const int chunks_per_group = (WF == AM_WF_INT4) ? p.group / kc : 1;
+  const uint16_t* sc16 = static_cast<const uint16_t*>(p.scales);
 
-  // ---- prologue: x (optionally RMSNorm'd) -> LDS, per-chunk sums ----
+  // Loads chunk-steps [jb*JB, jb*JB + JB) of iteration `it` into f.
+  auto issue = [&](Frag<JB, P, SC>& f, int64_t it, int jb) {
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+      const int64_t u = it * P + pp;
+      int64_t r0, r1;
+      pair_rows<EPI>(p, u, r0, r1);
+      const bool v0 = u < p.units;
+      const bool v1 = v0 && r1 < p.n;
+      const uint8_t* row0 = p.w + r0 * p.row_bytes;
+      const uint8_t* row1 = p.w + (v1 ? r1 : r0) * p.row_bytes;
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const int j = jb * JB + jj;
+        const int64_t c = lane + 64 * j;
+        const bool ok = j < J && c < C;
+        f.w[pp][0][jj] = (ok && v0) ? ld_stream(row0, c) : make_uint4(0, 0, 0, 0);
+        f.w[pp][1][jj] = (ok && v1) ? ld_stream(row1, c) : make_uint4(0, 0, 0, 0);
+        if constexpr (SC) {
+          const int64_t g = c / chunks_per_group;
+          f.s[pp][0][jj] = (ok && v0) ? static_cast<float>(__builtin_bit_cast(_Float16, sc16[r0 * ng + g])) : 0.0f;
+          f.s[pp][1][jj] = (ok && v1) ? static_cast<float>(__builtin_bit_cast(_Float16, sc16[r1 * ng + g])) : 0.0f;
+        }
+      }
+    }
+  };
+
+  // Issue the first iteration's first load block before the prologue so HBM latency
+  // overlaps the activation staging.
+  Frag<JB, P, SC> fa, fb;
+  int64_t it = gw;
+  if (it < niter) issue(fa, it, 0);
+
+  // ---- prologue: x (optionally RMSNorm'd) -> LDS, per-chunk offset corrections ----
   const T* xin = static_cast<const T*>(p.x);
   float inv = 1.0f;
   if constexpr (NORM) {
@@ -172,8 +262,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       reinterpret_cast<float*>(xl)[j] = v;
   }
   __syncthreads();
-  const int64_t C = p.row_bytes / 16;  // chunks per row
-  if constexpr (WF == AM_WF_INT4 || WF == AM_WF_INT8) {
+  if constexpr (XS::kOff != 0.0f) {
     for (int64_t c = threadIdx.x; c < C; c += 256) {
       float s = 0.0f;
       for (int i = 0; i < kc; ++i) {
@@ -181,145 +270,160 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
         s += XS::kBF16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xl)[j])
                        : reinterpret_cast<const float*>(xl)[j];
       }
-      xsum[c] = s;
+      corr_lds[c] = XS::kOff * s;
     }
     __syncthreads();
   }
-
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
-  const int J = static_cast<int>((C + 63) / 64);
-  const int ng = (WF == AM_WF_INT4) ? static_cast<int>(K / p.group) : 1;
-  const int chunks_per_group = (WF == AM_WF_INT4) ? p.group / kc : 1;
+  // this lane's x chunks into registers
+  uint32_t xr[JM][XDW];
+  float corr[JM];
+#pragma unroll
+  for (int j = 0; j < JM; ++j) {
+    const int64_t c = lane + 64 * j;
+    const bool ok = j < J && c < C;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(xl) + c * XDW;
+#pragma unroll
+    for (int t = 0; t < XDW; ++t) xr[j][t] = ok ? src[t] : 0u;
+    corr[j] = (XS::kOff != 0.0f && ok) ? corr_lds[c] : 0.0f;
+  }
 
   float best_v = 0.0f;
   int64_t best_i = -1;
   int64_t posv = 0;
   if constexpr (EPI == kEpiQkv) posv = *p.pos;
 
-  for (int64_t u = gw; u < p.units; u += TW) {
-    int64_t r0, r1;
-    if constexpr (EPI == kEpiQkv) {
-      const int64_t half = p.d / 2;
-      const int64_t head = u / half, i = u % half;
-      r0 = head * p.d + i;
-      r1 = r0 + half;
-    } else if constexpr (EPI == kEpiGateUp) {
-      r0 = u;  // gate row u, up row u (rows [0,F) gate then [F,2F) up)
-      r1 = u + p.n / 2;
-    } else {
-      r0 = 2 * u;
-      r1 = 2 * u + 1;
-    }
-    const bool v1 = r1 < p.n;
-    const uint8_t* w0 = p.w + r0 * p.row_bytes;
-    const uint8_t* w1 = p.w + (v1 ? r1 : r0) * p.row_bytes;
-    float acc0 = 0.0f, acc1 = 0.0f;
-    for (int j0 = 0; j0 < J; j0 += kJB) {
-      uint4 wa[kJB], wb[kJB];
-      float sa[kJB], sb[kJB];
+  // Accumulates load block jb of f into acc.
+  auto accum = [&](const Frag<JB, P, SC>& f, int jb, float (&acc)[P][2]) {
 #pragma unroll
-      for (int jj = 0; jj < kJB; ++jj) {
-        const int64_t c = lane + 64 * static_cast<int64_t>(j0 + jj);
-        const bool ok = (j0 + jj < J) && c < C;
-        wa[jj] = ok ? *reinterpret_cast<const uint4*>(w0 + c * 16) : make_uint4(0, 0, 0, 0);
-        wb[jj] = ok ? *reinterpret_cast<const uint4*>(w1 + c * 16) : make_uint4(0, 0, 0, 0);
-        if constexpr (WF == AM_WF_INT4) {
-          const uint16_t* sc = static_cast<const uint16_t*>(p.scales);
-          const int64_t g = c / chunks_per_group;
-          sa[jj] = ok ? static_cast<float>(__builtin_bit_cast(_Float16, sc[r0 * ng + g])) : 0.0f;
-          sb[jj] = ok ? static_cast<float>(__builtin_bit_cast(_Float16, sc[(v1 ? r1 : r0) * ng + g])) : 0.0f;
-        }
-      }
+    for (int pp = 0; pp < P; ++pp) {
 #pragma unroll
-      for (int jj = 0; jj < kJB; ++jj) {
-        const int64_t c = lane + 64 * static_cast<int64_t>(j0 + jj);
-        if ((j0 + jj < J) && c < C) {
-          float da = chunk_dot<A, WF>(wa[jj], xl, c);
-          float db = chunk_dot<A, WF>(wb[jj], xl, c);
-          if constexpr (XS::kOff != 0.0f) {
-            const float xs = xsum[c];
-            da = fmaf(-XS::kOff, xs, da);
-            db = fmaf(-XS::kOff, xs, db);
-          }
-          if constexpr (WF == AM_WF_INT4) {
-            acc0 = fmaf(sa[jj], da, acc0);
-            acc1 = fmaf(sb[jj], db, acc1);
-          } else {
-            acc0 += da;
-            acc1 += db;
-          }
+      for (int jj = 0; jj < JB; ++jj) {
+        const int j = jb * JB + jj;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float dv = chunk_dot<A, WF>(f.w[pp][rr][jj], xr[j]);
+          if constexpr (XS::kOff != 0.0f) dv -= corr[j];
+          if constexpr (SC)
+            acc[pp][rr] = fmaf(f.s[pp][rr][jj], dv, acc[pp][rr]);
+          else
+            acc[pp][rr] += dv;
         }
       }
     }
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
-    if constexpr (WF == AM_WF_INT8) {
-      const float* sc = static_cast<const float*>(p.scales);
-      acc0 *= sc[r0];
-      acc1 *= sc[v1 ? r1 : r0];
-    }
+  };
 
-    // ---- epilogue ----
-    if constexpr (EPI == kEpiLmHead) {
-      if (lane == 0) {
-        float* lg = static_cast<float*>(p.out);
-        if (lg != nullptr) {
-          lg[r0] = acc0;
-          if (v1) lg[r1] = acc1;
-        }
-        if (argmax_better(acc0, r0, best_v, best_i)) { best_v = acc0; best_i = r0; }
-        if (v1 && argmax_better(acc1, r1, best_v, best_i)) { best_v = acc1; best_i = r1; }
+  // Reduces acc across the wave and applies the epilogue of iteration itc.
+  auto finish = [&](float (&acc)[P][2], int64_t itc) {
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+      acc[pp][0] = wave_sum_dpp(acc[pp][0]);
+      acc[pp][1] = wave_sum_dpp(acc[pp][1]);
+    }
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) {
+      const int64_t u = itc * P + pp;
+      if (u >= p.units) break;
+      int64_t r0, r1;
+      pair_rows<EPI>(p, u, r0, r1);
+      const bool v1 = r1 < p.n;
+      float a0 = acc[pp][0], a1 = acc[pp][1];
+      if constexpr (WF == AM_WF_INT8) {
+        const float* s8 = static_cast<const float*>(p.scales);
+        a0 *= s8[r0];
+        a1 *= v1 ? s8[r1] : 0.0f;
       }
-    } else if (lane == 0) {
-      T* out = static_cast<T*>(p.out);
-      if constexpr (EPI == kEpiStore) {
-        if (p.out_f32) {
-          float* of = static_cast<float*>(p.out);
-          of[r0] = acc0;
-          if (v1) of[r1] = acc1;
-        } else {
-          A::store(out, r0, acc0);
-          if (v1) A::store(out, r1, acc1);
-        }
-      } else if constexpr (EPI == kEpiResidual) {
-        const T* res = static_cast<const T*>(p.residual);
-        A::store(out, r0, A::load(res, r0) + A::round(acc0));
-        if (v1) A::store(out, r1, A::load(res, r1) + A::round(acc1));
-      } else if constexpr (EPI == kEpiGateUp) {
-        const float g = A::round(acc0), up = A::round(acc1);
-        A::store(out, u, silu_ref(g) * up);
-      } else if constexpr (EPI == kEpiQkv) {
-        const int64_t half = p.d / 2;
-        const int64_t head = u / half, i = u % half;
-        const float y0 = A::round(acc0), y1 = A::round(acc1);
-        if (head < p.hq + p.hkv) {
-          const float c = p.cos_tab[posv * half + i], s = p.sin_tab[posv * half + i];
-          const float o0 = y0 * c - y1 * s;
-          const float o1 = y1 * c + y0 * s;
-          if (head < p.hq) {
-            T* q = static_cast<T*>(p.q_out);
-            A::store(q, head * p.d + i, o0);
-            A::store(q, head * p.d + i + half, o1);
-          } else if (posv < p.cap) {
-            T* kc = static_cast<T*>(p.k_cache);
-            const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
-            A::store(kc, base + i, o0);
-            A::store(kc, base + i + half, o1);
+      if constexpr (EPI == kEpiLmHead) {
+        if (lane == 0) {
+          float* lg = static_cast<float*>(p.out);
+          if (lg != nullptr) {
+            lg[r0] = a0;
+            if (v1) lg[r1] = a1;
           }
-        } else if (posv < p.cap) {
-          T* vc = static_cast<T*>(p.v_cache);
-          const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
-          A::store(vc, base + i, y0);
-          A::store(vc, base + i + half, y1);
+        }
+        if (argmax_better(a0, r0, best_v, best_i)) { best_v = a0; best_i = r0; }
+        if (v1 && argmax_better(a1, r1, best_v, best_i)) { best_v = a1; best_i = r1; }
+      } else if (lane == pp) {
+        T* out = static_cast<T*>(p.out);
+        if constexpr (EPI == kEpiStore) {
+          if (p.out_f32) {
+            float* of = static_cast<float*>(p.out);
+            of[r0] = a0;
+            if (v1) of[r1] = a1;
+          } else {
+            A::store(out, r0, a0);
+            if (v1) A::store(out, r1, a1);
+          }
+        } else if constexpr (EPI == kEpiResidual) {
+          const T* res = static_cast<const T*>(p.residual);
+          A::store(out, r0, A::load(res, r0) + A::round(a0));
+          if (v1) A::store(out, r1, A::load(res, r1) + A::round(a1));
+        } else if constexpr (EPI == kEpiGateUp) {
+          const float g = A::round(a0), up = A::round(a1);
+          A::store(out, u, silu_ref(g) * up);
+        } else if constexpr (EPI == kEpiQkv) {
+          const int64_t half = p.d / 2;
+          const int64_t head = u / half, i = u % half;
+          const float y0 = A::round(a0), y1 = A::round(a1);
+          if (head < p.hq + p.hkv) {
+            const float c = p.cos_tab[posv * half + i], s = p.sin_tab[posv * half + i];
+            const float o0 = y0 * c - y1 * s;
+            const float o1 = y1 * c + y0 * s;
+            if (head < p.hq) {
+              T* q = static_cast<T*>(p.q_out);
+              A::store(q, head * p.d + i, o0);
+              A::store(q, head * p.d + i + half, o1);
+            } else if (posv < p.cap) {
+              T* kc = static_cast<T*>(p.k_cache);
+              const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
+              A::store(kc, base + i, o0);
+              A::store(kc, base + i + half, o1);
+            }
+          } else if (posv < p.cap) {
+            T* vc = static_cast<T*>(p.v_cache);
+            const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
+            A::store(vc, base + i, y0);
+            A::store(vc, base + i + half, y1);
+          }
         }
       }
+    }
+  };
+
+  if constexpr (PIPE) {
+    // two register buffers: the next iteration's loads are in flight while the
+    // current one is reduced and stored
+    while (it < niter) {
+      float acc[P][2] = {};
+      int64_t nx = it + TW;
+      if (nx < niter) issue(fb, nx, 0);
+      accum(fa, 0, acc);
+      finish(acc, it);
+      it = nx;
+      if (it >= niter) break;
+      float acc2[P][2] = {};
+      nx = it + TW;
+      if (nx < niter) issue(fa, nx, 0);
+      accum(fb, 0, acc2);
+      finish(acc2, it);
+      it = nx;
+    }
+  } else {
+    while (it < niter) {
+      float acc[P][2] = {};
+#pragma unroll
+      for (int jb = 0; jb < NB; ++jb) {
+        if (jb > 0) issue(fa, it, jb);
+        accum(fa, jb, acc);
+      }
+      finish(acc, it);
+      it += TW;
+      if (it < niter) issue(fa, it, 0);
     }
   }
 
   if constexpr (EPI == kEpiLmHead) {
-    // block-level best -> partials; the last block reduces and publishes the token.
+    // block best -> partials; the last block (atomic ticket) reduces them, publishes
+    // the token / advances the decode state, and resets the ticket for the next call.
     __shared__ float bv_s[4];
     __shared__ int64_t bi_s[4];
     __shared__ bool last;
@@ -404,21 +508,42 @@ am_status_code ValidateWeight(const am_gfx950_weight& w) {
   return AM_STATUS_OK;
 }
 
-template <class A, int WF, bool NORM, int EPI>
-am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
+template <class A, int WF, bool NORM, int EPI, int JM, int P>
+am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (g.row_bytes / 16) * 4;
   if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
-  // Balanced persistent-style grid: at most ~8 resident blocks per CU.
-  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * 8 * 4;
-  const int64_t upw = CeilDiv(g.units, max_waves);
-  int64_t waves = CeilDiv(g.units, upw);
+  // Balanced grid of persistent waves: at most 8 waves per CU, iterations spread evenly.
+  const int64_t niter = CeilDiv(g.units, P);
+  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * 8;
+  const int64_t ipw = CeilDiv(niter, max_waves);
+  const int64_t waves = CeilDiv(niter, ipw);
   int64_t blocks = CeilDiv(waves, 4);
-  if (EPI == kEpiLmHead && blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P>), dim3(static_cast<unsigned>(blocks)), dim3(256),
                      static_cast<size_t>(lds), s, g);
   AM_RETURN_IF_LAUNCH_FAILED("gemv");
   return AM_STATUS_OK;
+}
+
+// Chunk-steps per row decide the register tiling: x stays in registers for up to
+// 16 chunk-steps (bounded by 128 dwords of x per lane).
+template <class A, int WF, bool NORM, int EPI>
+am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
+  using XS = XStore<A, WF>;
+  const int64_t J = CeilDiv(g.row_bytes / 16, 64);
+  if (J <= 2) return LaunchJ<A, WF, NORM, EPI, 2, 2>(g, s);
+  if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, 2>(g, s);
+  if constexpr (8 * XS::kDW <= 128) {
+    if (J <= 8) return LaunchJ<A, WF, NORM, EPI, 8, 1>(g, s);
+  }
+  if constexpr (16 * XS::kDW <= 128) {
+    if (J <= 16) return LaunchJ<A, WF, NORM, EPI, 16, 1>(g, s);
+  }
+  if constexpr (32 * XS::kDW <= 128) {
+    if (J <= 32) return LaunchJ<A, WF, NORM, EPI, 32, 1>(g, s);
+  }
+  return SetLastError(AM_STATUS_UNIMPLEMENTED, "gemv: in_features too large for register tiling of this format");
 }
 
 template <bool NORM, int EPI>
@@ -453,7 +578,7 @@ GemvArgs BaseArgs(const am_gfx950_weight& w) {
 
 }  // namespace
 
-// Used by linear.cpp-equivalent entry (am_gfx950_linear) for m = 1 rows.
+// Linear rows for am_gfx950_linear (decode GEMV; also the row loop of small m).
 am_status_code GemvLinearRow(const void* x, int32_t act, const am_gfx950_weight& w, void* out, int32_t out_dtype,
                              const void* residual, hipStream_t s) {
   if (auto st = ValidateWeight(w); st != AM_STATUS_OK) return st;
@@ -517,7 +642,7 @@ extern "C" am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_
   AM_CHECK_ARG(a != nullptr, "fused_gate_up: null args");
   if (auto st = ValidateWeight(a->w_gate_up); st != AM_STATUS_OK) return st;
   AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_gate_up: dtype");
-  AM_CHECK_ARG(a->w_gate_up.n % 2 == 0, "fused_gate_up: interleaved weight needs an even row count");
+  AM_CHECK_ARG(a->w_gate_up.n % 2 == 0, "fused_gate_up: gate/up weight needs an even row count");
   AM_CHECK_ARG(a->h && a->norm_w && a->act_out && a->eps > 0.0f, "fused_gate_up: bad pointer/eps");
   GemvArgs g = BaseArgs(a->w_gate_up);
   g.x = a->h;

@@ -351,3 +351,23 @@ def test_argmax_exact_ties_nan():
     for _ in range(2):
         L.call("am_gfx950_argmax", N.ArgmaxArgs(p(xd), 0, rows, n, p(out), p(ws), wsb), stream())
         assert list(host(out)) == [O.argmax(x[r]) for r in range(rows)] == [5000, 77, 0]
+
+
+def test_attention_split_count_follows_context():
+    """The kernel picks its split count from the live context (device start position):
+    alternate long and short contexts through one workspace and check every call."""
+    hq, hkv, d, cap = 32, 8, 128, 4096
+    q = O.round_bf16(O.synth_f32(12, 1, hq * d, std=1.0).reshape(1, hq * d))
+    kc = O.round_bf16(O.synth_f32(12, 2, hkv * cap * d, std=1.0).reshape(hkv, cap, d))
+    vc = O.round_bf16(O.synth_f32(12, 3, hkv * cap * d, std=1.0).reshape(hkv, cap, d))
+    qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+    out = empty((1, hq * d), torch.int16)
+    wsb = L.am_gfx950_attention_workspace_bytes(1, 1, hq, hkv, d, cap, 0)
+    ws = zeros((wsb,), torch.uint8)
+    posd = zeros((1,), torch.int64)
+    for start in (3000, 40, 0, 700, 4095, 31, 32, 3000):
+        posd.fill_(start)
+        a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), 1, hq, hkv, d, cap, 0, p(posd), 1, 0, 1, 0, p(ws), wsb)
+        L.call("am_gfx950_attention", a, stream())
+        close(O.bf16_to_f32(bits_host(out)), O.attention(q, kc, vc, 1, hq, hkv, d, cap, start), TOL["bf16"],
+              f"attention start={start}")
