@@ -173,8 +173,13 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 template <int JB, int P, bool SC>
 struct Frag {
   uint4 w[P][2][JB];
-  float s[P][2][SC ? JB : 1];
+  uint32_t s[P][2][SC ? JB : 1];  // raw fp16 group-scale bits, converted at use
+  float s8[P][2];                 // INT8 row scales
 };
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
 
 // Streaming 16-byte weight load (read once per token: non-temporal hint).
 __device__ __forceinline__ uint4 ld_stream(const uint8_t* row, int64_t c) {
@@ -191,14 +196,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   constexpr bool SC = WF == AM_WF_INT4;
   constexpr int JB = JM < 8 ? JM : 8;  // chunk-steps per load block
   constexpr int NB = JM / JB;          // load blocks per row
-  constexpr bool PIPE = NB == 1 && JM <= 4;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
   const int64_t K = p.k;
   const int64_t C = p.row_bytes / 16;  // chunks per row
   const int J = static_cast<int>((C + 63) / 64);
+  // LDS: x | per-chunk corrections | residual (Residual epilogue) | cos,sin (Qkv epilogue)
   uint8_t* xl = smem;
-  float* corr_lds = reinterpret_cast<float*>(smem + ((K * XS::kBytes + 15) / 16) * 16);
+  const int64_t off_corr = ((K * XS::kBytes + 15) / 16) * 16;
+  const int64_t off_res = off_corr + ((C * 4 + 15) / 16) * 16;
+  const int64_t off_cs = off_res + (EPI == kEpiResidual ? ((p.n * static_cast<int64_t>(sizeof(T)) + 15) / 16) * 16 : 0);
+  float* corr_lds = reinterpret_cast<float*>(smem + off_corr);
+  T* res_lds = reinterpret_cast<T*>(smem + off_res);
+  float* cs_lds = reinterpret_cast<float*>(smem + off_cs);
   const int lane = threadIdx.x & 63;
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
@@ -207,28 +217,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   const int chunks_per_group = (WF == AM_WF_INT4) ? p.group / kc : 1;
   const uint16_t* sc16 = static_cast<const uint16_t*>(p.scales);
 
-  // Loads chunk-steps [jb*JB, jb*JB + JB) of iteration `it` into f.
+  // Loads chunk-steps [jb*JB, jb*JB + JB) of iteration `it` into f.  Every load is
+  // unconditional (straight-line code, one wait at first use): out-of-range chunks
+  // and rows read a clamped in-bounds address instead, and contribute nothing because
+  // the lane's x registers for those chunks are zero and invalid rows are never
+  // stored.
   auto issue = [&](Frag<JB, P, SC>& f, int64_t it, int jb) {
 #pragma unroll
     for (int pp = 0; pp < P; ++pp) {
-      const int64_t u = it * P + pp;
+      int64_t u = it * P + pp;
+      if (u >= p.units) u = p.units - 1;
       int64_t r0, r1;
       pair_rows<EPI>(p, u, r0, r1);
-      const bool v0 = u < p.units;
-      const bool v1 = v0 && r1 < p.n;
+      if (r1 >= p.n) r1 = r0;
       const uint8_t* row0 = p.w + r0 * p.row_bytes;
-      const uint8_t* row1 = p.w + (v1 ? r1 : r0) * p.row_bytes;
+      const uint8_t* row1 = p.w + r1 * p.row_bytes;
 #pragma unroll
       for (int jj = 0; jj < JB; ++jj) {
         const int j = jb * JB + jj;
-        const int64_t c = lane + 64 * j;
-        const bool ok = j < J && c < C;
-        f.w[pp][0][jj] = (ok && v0) ? ld_stream(row0, c) : make_uint4(0, 0, 0, 0);
-        f.w[pp][1][jj] = (ok && v1) ? ld_stream(row1, c) : make_uint4(0, 0, 0, 0);
+        int64_t c = lane + 64 * j;
+        if (!(j < J && c < C)) c = 0;
+        f.w[pp][0][jj] = ld_stream(row0, c);
+        f.w[pp][1][jj] = ld_stream(row1, c);
         if constexpr (SC) {
           const int64_t g = c / chunks_per_group;
-          f.s[pp][0][jj] = (ok && v0) ? static_cast<float>(__builtin_bit_cast(_Float16, sc16[r0 * ng + g])) : 0.0f;
-          f.s[pp][1][jj] = (ok && v1) ? static_cast<float>(__builtin_bit_cast(_Float16, sc16[r1 * ng + g])) : 0.0f;
+          f.s[pp][0][jj] = sc16[r0 * ng + g];
+          f.s[pp][1][jj] = sc16[r1 * ng + g];
+        }
+      }
+      if constexpr (WF == AM_WF_INT8) {
+        if (jb == 0) {
+          f.s8[pp][0] = static_cast<const float*>(p.scales)[r0];
+          f.s8[pp][1] = static_cast<const float*>(p.scales)[r1];
         }
       }
     }
@@ -236,7 +256,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
 
   // Issue the first iteration's first load block before the prologue so HBM latency
   // overlaps the activation staging.
-  Frag<JB, P, SC> fa, fb;
+  Frag<JB, P, SC> fa;
   int64_t it = gw;
   if (it < niter) issue(fa, it, 0);
 
@@ -260,6 +280,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       reinterpret_cast<uint16_t*>(xl)[j] = f32_to_bf16_bits(v);
     else
       reinterpret_cast<float*>(xl)[j] = v;
+  }
+  // Epilogue operands come from LDS, so no global load is issued behind a prefetch
+  // (the memory counter is in order: a later load would wait for the prefetch).
+  // Each output row belongs to one wave, so staging the whole residual vector here
+  // reads every row before its only writer updates it.
+  int64_t posv = 0;
+  if constexpr (EPI == kEpiResidual) {
+    const T* res = static_cast<const T*>(p.residual);
+    for (int64_t r = threadIdx.x; r < p.n; r += 256) res_lds[r] = res[r];
+  }
+  if constexpr (EPI == kEpiQkv) {
+    posv = *p.pos;
+    const int64_t half = p.d / 2;
+    const int64_t pr = posv < p.cap ? posv : 0;
+    for (int64_t i = threadIdx.x; i < half; i += 256) {
+      cs_lds[i] = p.cos_tab[pr * half + i];
+      cs_lds[half + i] = p.sin_tab[pr * half + i];
+    }
   }
   __syncthreads();
   if constexpr (XS::kOff != 0.0f) {
@@ -289,8 +327,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
 
   float best_v = 0.0f;
   int64_t best_i = -1;
-  int64_t posv = 0;
-  if constexpr (EPI == kEpiQkv) posv = *p.pos;
 
   // Accumulates load block jb of f into acc.
   auto accum = [&](const Frag<JB, P, SC>& f, int jb, float (&acc)[P][2]) {
@@ -304,9 +340,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
           float dv = chunk_dot<A, WF>(f.w[pp][rr][jj], xr[j]);
           if constexpr (XS::kOff != 0.0f) dv -= corr[j];
           if constexpr (SC)
-            acc[pp][rr] = fmaf(f.s[pp][rr][jj], dv, acc[pp][rr]);
+            acc[pp][rr] = fmaf(f16_bits_to_f32(f.s[pp][rr][jj]), dv, acc[pp][rr]);
           else
             acc[pp][rr] += dv;
+        }
+      }
+      if constexpr (WF == AM_WF_INT8) {
+        if (jb == NB - 1) {  // per-row scale after the last block of the row
+          acc[pp][0] *= f.s8[pp][0];
+          acc[pp][1] *= f.s8[pp][1];
         }
       }
     }
@@ -326,12 +368,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       int64_t r0, r1;
       pair_rows<EPI>(p, u, r0, r1);
       const bool v1 = r1 < p.n;
-      float a0 = acc[pp][0], a1 = acc[pp][1];
-      if constexpr (WF == AM_WF_INT8) {
-        const float* s8 = static_cast<const float*>(p.scales);
-        a0 *= s8[r0];
-        a1 *= v1 ? s8[r1] : 0.0f;
-      }
+      const float a0 = acc[pp][0], a1 = acc[pp][1];
       if constexpr (EPI == kEpiLmHead) {
         if (lane == 0) {
           float* lg = static_cast<float*>(p.out);
@@ -354,9 +391,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
             if (v1) A::store(out, r1, a1);
           }
         } else if constexpr (EPI == kEpiResidual) {
-          const T* res = static_cast<const T*>(p.residual);
-          A::store(out, r0, A::load(res, r0) + A::round(a0));
-          if (v1) A::store(out, r1, A::load(res, r1) + A::round(a1));
+          A::store(out, r0, A::load(res_lds, r0) + A::round(a0));
+          if (v1) A::store(out, r1, A::load(res_lds, r1) + A::round(a1));
         } else if constexpr (EPI == kEpiGateUp) {
           const float g = A::round(a0), up = A::round(a1);
           A::store(out, u, silu_ref(g) * up);
@@ -365,7 +401,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
           const int64_t head = u / half, i = u % half;
           const float y0 = A::round(a0), y1 = A::round(a1);
           if (head < p.hq + p.hkv) {
-            const float c = p.cos_tab[posv * half + i], s = p.sin_tab[posv * half + i];
+            const float c = cs_lds[i], s = cs_lds[half + i];
             const float o0 = y0 * c - y1 * s;
             const float o1 = y1 * c + y0 * s;
             if (head < p.hq) {
@@ -389,36 +425,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     }
   };
 
-  if constexpr (PIPE) {
-    // two register buffers: the next iteration's loads are in flight while the
-    // current one is reduced and stored
-    while (it < niter) {
-      float acc[P][2] = {};
-      int64_t nx = it + TW;
-      if (nx < niter) issue(fb, nx, 0);
-      accum(fa, 0, acc);
-      finish(acc, it);
-      it = nx;
-      if (it >= niter) break;
-      float acc2[P][2] = {};
-      nx = it + TW;
-      if (nx < niter) issue(fa, nx, 0);
-      accum(fb, 0, acc2);
-      finish(acc2, it);
-      it = nx;
-    }
-  } else {
-    while (it < niter) {
-      float acc[P][2] = {};
+  // Each iteration's loads are all issued before any of them is used; the next
+  // iteration's first block is issued as soon as the registers are consumed, so its
+  // latency overlaps the cross-lane reduction and the epilogue stores.
+  while (it < niter) {
+    float acc[P][2] = {};
 #pragma unroll
-      for (int jb = 0; jb < NB; ++jb) {
-        if (jb > 0) issue(fa, it, jb);
-        accum(fa, jb, acc);
-      }
-      finish(acc, it);
-      it += TW;
-      if (it < niter) issue(fa, it, 0);
+    for (int jb = 0; jb < NB; ++jb) {
+      if (jb > 0) issue(fa, it, jb);
+      accum(fa, jb, acc);
     }
+    const int64_t nx = it + TW;
+    if (nx < niter) issue(fa, nx, 0);
+    finish(acc, it);
+    it = nx;
   }
 
   if constexpr (EPI == kEpiLmHead) {
@@ -511,11 +531,26 @@ am_status_code ValidateWeight(const am_gfx950_weight& w) {
 template <class A, int WF, bool NORM, int EPI, int JM, int P>
 am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
-  const int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (g.row_bytes / 16) * 4;
+  const int64_t tb = A::kDtype == AM_DT_BF16 ? 2 : 4;
+  int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (((g.row_bytes / 16) * 4 + 15) / 16) * 16;
+  if (EPI == kEpiResidual) lds += ((g.n * tb + 15) / 16) * 16;
+  if (EPI == kEpiQkv) lds += g.d * 4;
   if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
-  // Balanced grid of persistent waves: at most 8 waves per CU, iterations spread evenly.
+  // Balanced grid of persistent waves: as many resident waves as the kernel's register
+  // and LDS footprint allows (HBM latency is hidden by waves in flight), iterations
+  // spread evenly over them.
+  static thread_local int64_t cached_lds = -1;
+  static thread_local int cached_blocks = 2;
+  if (cached_lds != lds) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<A, WF, NORM, EPI, JM, P>, 256,
+                                                     static_cast<size_t>(lds)) != hipSuccess || nb < 1)
+      nb = 2;
+    cached_blocks = nb;
+    cached_lds = lds;
+  }
   const int64_t niter = CeilDiv(g.units, P);
-  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * 8;
+  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * cached_blocks * 4;
   const int64_t ipw = CeilDiv(niter, max_waves);
   const int64_t waves = CeilDiv(niter, ipw);
   int64_t blocks = CeilDiv(waves, 4);
