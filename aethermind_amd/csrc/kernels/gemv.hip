@@ -59,6 +59,7 @@ struct GemvArgs {
   float* pv;
   int64_t* pi;
   int32_t out_f32;
+  int32_t vec;  // x, norm_w, residual 16-byte aligned and whole 16-byte pieces
 };
 
 // k values per 16-byte chunk of a weight row
@@ -80,19 +81,29 @@ template <class A, int WF> struct XStore {
 
 __device__ __forceinline__ bf16x2_t as_bf2(uint32_t u) { return __builtin_bit_cast(bf16x2_t, u); }
 
-// Dot of one 16-byte weight chunk with its x values (kDW dwords at xd).
+// Unpack constants held in VGPRs: gfx9 VOP3 encodings take no literal operands, so
+// with both constants in registers each nibble pair costs one v_and_or_b32 (plus one
+// shift) instead of separate and/or instructions.
+struct Unpack {
+  uint32_t mask, magic;
+  __device__ __forceinline__ Unpack() : mask(0x000F000Fu), magic(0x43004300u) {
+    asm volatile("" : "+v"(mask), "+v"(magic));
+  }
+};
+
+// init + dot of one 16-byte weight chunk with its x values (kDW dwords at xd).
 template <class A, int WF>
-__device__ __forceinline__ float chunk_dot(const uint4 w, const uint32_t* xd) {
+__device__ __forceinline__ float chunk_dot(const uint4 w, const uint32_t* xd, float init, const Unpack& up) {
   using XS = XStore<A, WF>;
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-  float acc = 0.0f;
+  float acc = init;
   if constexpr (XS::kBF16) {
     if constexpr (WF == AM_WF_INT4) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t pair = ((ws[t] >> (4 * pp)) & 0x000F000Fu) | 0x43004300u;
+          const uint32_t pair = ((ws[t] >> (4 * pp)) & up.mask) | up.magic;
           acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(xd[4 * t + pp]), as_bf2(pair), acc, false);
         }
     } else {  // BF16 weights
@@ -187,42 +198,168 @@ __device__ __forceinline__ uint4 ld_stream(const uint8_t* row, int64_t c) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Activation vector in LDS: chunk c (the kc values that meet 16-byte weight chunk c)
+// occupies kc*kBytes contiguous bytes as NPC 16-byte pieces; piece i is stored in
+// slot (i + (c >> 1)) % NPC so that lanes reading consecutive chunks start in
+// different LDS banks.
+template <class A, int WF>
+struct XLds {
+  using XS = XStore<A, WF>;
+  static constexpr int kc = Fmt<WF>::kc;
+  static constexpr int NPC = XS::kDW / 4;          // 16-byte pieces per chunk (1..8)
+  static constexpr int CB = kc * XS::kBytes;       // bytes per chunk
+  __device__ static __forceinline__ int64_t addr(int64_t j) {  // byte address of value j
+    const int64_t c = j / kc;
+    const int b = static_cast<int>(j % kc) * XS::kBytes;
+    const int slot = ((b >> 4) + static_cast<int>(c >> 1)) % NPC;
+    return c * CB + slot * 16 + (b & 15);
+  }
+  __device__ static __forceinline__ void store(uint8_t* xl, int64_t j, float v) {
+    if constexpr (XS::kBF16)
+      *reinterpret_cast<uint16_t*>(xl + addr(j)) = f32_to_bf16_bits(v);
+    else
+      *reinterpret_cast<float*>(xl + addr(j)) = v;
+  }
+  // the XS::kDW dwords of chunk c, in value order
+  __device__ static __forceinline__ void load_chunk(const uint8_t* xl, int64_t c, uint32_t* xd) {
+#pragma unroll
+    for (int i = 0; i < NPC; ++i) {
+      const int slot = (i + static_cast<int>(c >> 1)) % NPC;
+      const uint4 v = *reinterpret_cast<const uint4*>(xl + c * CB + slot * 16);
+      xd[4 * i] = v.x;
+      xd[4 * i + 1] = v.y;
+      xd[4 * i + 2] = v.z;
+      xd[4 * i + 3] = v.w;
+    }
+  }
+  // sum of the kc values of a chunk held in xd
+  __device__ static __forceinline__ float chunk_sum(const uint32_t* xd) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XS::kDW; ++i) {
+      if constexpr (XS::kBF16) {
+        s += __uint_as_float(xd[i] << 16);
+        s += __uint_as_float(xd[i] & 0xFFFF0000u);
+      } else {
+        s += __uint_as_float(xd[i]);
+      }
+    }
+    return s;
+  }
+};
+
+// element e of a 16-byte piece of activations of type T, as float
+template <class A>
+__device__ __forceinline__ float piece_elem(const uint4& v, int e) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (A::kDtype == AM_DT_BF16)
+    return __uint_as_float((e & 1) ? (w[e >> 1] & 0xFFFF0000u) : (w[e >> 1] << 16));
+  else
+    return __uint_as_float(w[e]);
+}
+
 template <class A, int WF, bool NORM, int EPI, int JM, int P>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   using XS = XStore<A, WF>;
+  using XL_ = XLds<A, WF>;
   using T = typename A::T;
   constexpr int kc = Fmt<WF>::kc;
   constexpr int XDW = XS::kDW;
   constexpr bool SC = WF == AM_WF_INT4;
-  constexpr int JB = JM < 8 ? JM : 8;  // chunk-steps per load block
-  constexpr int NB = JM / JB;          // load blocks per row
+  // x chunks live in registers when they fit in 32 dwords per lane, else they are
+  // read from LDS per chunk-step inside the loop
+  constexpr bool XL = JM * XDW > 32;
+  constexpr int JB = XL ? (JM < 4 ? JM : 4) : JM;  // chunk-steps per load block
+  constexpr int NB = JM / JB;                      // load blocks per iteration
+  constexpr int EPP = 16 / static_cast<int>(sizeof(T));               // activations per 16-byte piece
+  constexpr int XP = (JM * 64 * kc + 256 * EPP - 1) / (256 * EPP);  // x pieces per thread
+  constexpr int RP = 4;                                               // residual pieces per thread (first pass)
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
+  const int tid = threadIdx.x;
   const int64_t K = p.k;
   const int64_t C = p.row_bytes / 16;  // chunks per row
   const int J = static_cast<int>((C + 63) / 64);
-  // LDS: x | per-chunk corrections | residual (Residual epilogue) | cos,sin (Qkv epilogue)
+  // LDS: x | per-chunk corrections (x-in-LDS variant) | residual | cos,sin
   uint8_t* xl = smem;
   const int64_t off_corr = ((K * XS::kBytes + 15) / 16) * 16;
-  const int64_t off_res = off_corr + ((C * 4 + 15) / 16) * 16;
+  const int64_t off_res = off_corr + (XL ? ((C * 4 + 15) / 16) * 16 : 0);
   const int64_t off_cs = off_res + (EPI == kEpiResidual ? ((p.n * static_cast<int64_t>(sizeof(T)) + 15) / 16) * 16 : 0);
   float* corr_lds = reinterpret_cast<float*>(smem + off_corr);
   T* res_lds = reinterpret_cast<T*>(smem + off_res);
   float* cs_lds = reinterpret_cast<float*>(smem + off_cs);
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = tid & 63;
+  // wave index made provably wave-uniform, so the loop below runs on scalar branches
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
   const int64_t niter = (p.units + P - 1) / P;
-  const int ng = (WF == AM_WF_INT4) ? static_cast<int>(K / p.group) : 1;
-  const int chunks_per_group = (WF == AM_WF_INT4) ? p.group / kc : 1;
+  const int ng = SC ? static_cast<int>(K / p.group) : 1;
+  const int chunks_per_group = SC ? p.group / kc : 1;
   const uint16_t* sc16 = static_cast<const uint16_t*>(p.scales);
+  // this wave's iterations are gw, gw + TW, ...; each is NB load blocks
+  const int64_t nit_w = gw < niter ? (niter - 1 - gw) / TW + 1 : 0;
+  const int64_t nblk = nit_w * NB;
 
-  // Loads chunk-steps [jb*JB, jb*JB + JB) of iteration `it` into f.  Every load is
-  // unconditional (straight-line code, one wait at first use): out-of-range chunks
-  // and rows read a clamped in-bounds address instead, and contribute nothing because
-  // the lane's x registers for those chunks are zero and invalid rows are never
-  // stored.
-  auto issue = [&](Frag<JB, P, SC>& f, int64_t it, int jb) {
+  // ---- 1. prologue operands: all loads issued at once, before any weight load ----
+  const T* xin = static_cast<const T*>(p.x);
+  const T* nw = static_cast<const T*>(p.norm_w);
+  const int64_t xpieces = K / EPP;
+  uint4 xv[XP];
+  uint4 nv[NORM ? XP : 1];
+  uint4 rv[RP];
+  const int64_t rpieces = p.n / EPP;
+  {
+    // Straight-line loads on every path (the arrays stay in registers); without the
+    // vector layout they read the (aligned) weight base instead and go unused.
+    const uint4* xs = reinterpret_cast<const uint4*>(p.vec ? static_cast<const void*>(xin) : p.w);
+    const uint4* ns = reinterpret_cast<const uint4*>(p.vec && NORM ? static_cast<const void*>(nw) : p.w);
+    const int64_t xlast = p.vec ? xpieces - 1 : 0;
+#pragma unroll
+    for (int v = 0; v < XP; ++v) {
+      int64_t pi = tid + 256 * v;
+      if (pi > xlast) pi = xlast;
+      xv[v] = xs[pi];
+      if constexpr (NORM) nv[v] = ns[pi];
+    }
+    if constexpr (EPI == kEpiResidual) {
+      const uint4* rs = reinterpret_cast<const uint4*>(p.vec ? p.residual : static_cast<const void*>(p.w));
+      const int64_t rlast = p.vec ? rpieces - 1 : 0;
+#pragma unroll
+      for (int v = 0; v < RP; ++v) {
+        int64_t pi = tid + 256 * v;
+        if (pi > rlast) pi = rlast;
+        rv[v] = rs[pi];
+      }
+    }
+  }
+  int64_t posv = 0;
+  float cs_c = 0.0f, cs_s = 0.0f;
+  if constexpr (EPI == kEpiQkv) {
+    posv = *p.pos;
+    const int64_t half = p.d / 2;
+    const int64_t pr = posv < p.cap ? posv : 0;
+    const int64_t i = tid < half ? tid : 0;
+    cs_c = p.cos_tab[pr * half + i];
+    cs_s = p.sin_tab[pr * half + i];
+  }
+
+  // ---- 2. first weight block ----
+  // Loads chunk-steps [jb*JB, jb*JB + JB) of this wave's block b into f.  Every load
+  // is unconditional (straight-line code, one wait at first use): out-of-range chunks
+  // and rows read a clamped in-bounds address instead and contribute nothing, because
+  // the lane's x values for those chunks are zero and invalid rows are never stored.
+  // A block past the wave's last one re-reads that last block (a wave without work
+  // reads the grid's last iteration).
+  auto issue = [&](Frag<JB, P, SC>& f, int64_t b) {
+    int64_t it;
+    int jb = 0;
+    if (nblk == 0) {
+      it = niter - 1;
+    } else {
+      if (b >= nblk) b = nblk - 1;
+      it = gw + (NB == 1 ? b : b / NB) * TW;
+      if constexpr (NB > 1) jb = static_cast<int>(b % NB);
+    }
 #pragma unroll
     for (int pp = 0; pp < P; ++pp) {
       int64_t u = it * P + pp;
@@ -246,107 +383,171 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
         }
       }
       if constexpr (WF == AM_WF_INT8) {
-        if (jb == 0) {
-          f.s8[pp][0] = static_cast<const float*>(p.scales)[r0];
-          f.s8[pp][1] = static_cast<const float*>(p.scales)[r1];
-        }
+        f.s8[pp][0] = static_cast<const float*>(p.scales)[r0];
+        f.s8[pp][1] = static_cast<const float*>(p.scales)[r1];
       }
     }
   };
+  Frag<JB, P, SC> fa, fb;
+  issue(fa, 0);
 
-  // Issue the first iteration's first load block before the prologue so HBM latency
-  // overlaps the activation staging.
-  Frag<JB, P, SC> fa;
-  int64_t it = gw;
-  if (it < niter) issue(fa, it, 0);
-
-  // ---- prologue: x (optionally RMSNorm'd) -> LDS, per-chunk offset corrections ----
-  const T* xin = static_cast<const T*>(p.x);
-  float inv = 1.0f;
-  if constexpr (NORM) {
-    float ss = 0.0f;
-    for (int64_t j = threadIdx.x; j < K; j += 256) {
-      const float v = A::load(xin, j);
-      ss = fmaf(v, v, ss);
+  // ---- 3. prologue: x (optionally RMSNorm'd) -> LDS, epilogue operands -> LDS ----
+  // The vector pass runs on every path with clamped indices, so the register arrays
+  // are consumed in straight-line code (nothing moves the loads behind the weights);
+  // without the vector layout it only writes placeholders that the element pass
+  // below overwrites.
+  {
+    const bool vec = p.vec != 0;
+    float inv = 1.0f;
+    if constexpr (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int v = 0; v < XP; ++v) {
+        const bool ok = vec && tid + 256 * v < xpieces;
+#pragma unroll
+        for (int e = 0; e < EPP; ++e) {
+          const float x = ok ? piece_elem<A>(xv[v], e) : 0.0f;
+          ss = fmaf(x, x, ss);
+        }
+      }
+      ss = block_sum_256(ss, red);
+      inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
     }
-    ss = block_sum_256(ss, red);
-    inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
+    const int64_t xlast = vec ? xpieces - 1 : 0;
+#pragma unroll
+    for (int v = 0; v < XP; ++v) {
+      int64_t pi = tid + 256 * v;
+      if (pi > xlast) pi = xlast;
+      if constexpr (!NORM && XS::kBytes == sizeof(T) && XL_::CB >= 16) {
+        // a piece of the input is exactly one 16-byte LDS piece
+        *reinterpret_cast<uint4*>(xl + XL_::addr(pi * EPP)) = xv[v];
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPP; ++e) {
+          float x = piece_elem<A>(xv[v], e);
+          if constexpr (NORM) x = A::round((x * inv) * piece_elem<A>(nv[v], e));
+          int64_t j = pi * EPP + e;
+          if (j >= K) j = K - 1;
+          XL_::store(xl, j, x);
+        }
+      }
+    }
+    if constexpr (EPI == kEpiResidual) {
+      const int64_t rlast = vec ? rpieces - 1 : 0;
+#pragma unroll
+      for (int v = 0; v < RP; ++v) {
+        int64_t pi = tid + 256 * v;
+        if (pi > rlast) pi = rlast;
+        reinterpret_cast<uint4*>(res_lds)[pi] = rv[v];
+      }
+      if (vec) {
+        const uint4* res = static_cast<const uint4*>(p.residual);
+        for (int64_t pi = tid + 256 * RP; pi < rpieces; pi += 256) reinterpret_cast<uint4*>(res_lds)[pi] = res[pi];
+      }
+    }
   }
-  const T* nw = static_cast<const T*>(p.norm_w);
-  for (int64_t j = threadIdx.x; j < K; j += 256) {
-    float v = A::load(xin, j);
-    if constexpr (NORM) v = A::round((v * inv) * A::load(nw, j));
-    if constexpr (XS::kBF16)
-      reinterpret_cast<uint16_t*>(xl)[j] = f32_to_bf16_bits(v);
-    else
-      reinterpret_cast<float*>(xl)[j] = v;
-  }
-  // Epilogue operands come from LDS, so no global load is issued behind a prefetch
-  // (the memory counter is in order: a later load would wait for the prefetch).
-  // Each output row belongs to one wave, so staging the whole residual vector here
-  // reads every row before its only writer updates it.
-  int64_t posv = 0;
-  if constexpr (EPI == kEpiResidual) {
-    const T* res = static_cast<const T*>(p.residual);
-    for (int64_t r = threadIdx.x; r < p.n; r += 256) res_lds[r] = res[r];
+  if (!p.vec) {
+    // unaligned or ragged activations: element loops overwrite the placeholders
+    __syncthreads();
+    float inv = 1.0f;
+    if constexpr (NORM) {
+      float ss = 0.0f;
+      for (int64_t j = tid; j < K; j += 256) {
+        const float v = A::load(xin, j);
+        ss = fmaf(v, v, ss);
+      }
+      ss = block_sum_256(ss, red);
+      inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
+    }
+    for (int64_t j = tid; j < K; j += 256) {
+      float v = A::load(xin, j);
+      if constexpr (NORM) v = A::round((v * inv) * A::load(nw, j));
+      XL_::store(xl, j, v);
+    }
+    if constexpr (EPI == kEpiResidual) {
+      const T* res = static_cast<const T*>(p.residual);
+      for (int64_t r = tid; r < p.n; r += 256) res_lds[r] = res[r];
+    }
   }
   if constexpr (EPI == kEpiQkv) {
-    posv = *p.pos;
     const int64_t half = p.d / 2;
-    const int64_t pr = posv < p.cap ? posv : 0;
-    for (int64_t i = threadIdx.x; i < half; i += 256) {
-      cs_lds[i] = p.cos_tab[pr * half + i];
-      cs_lds[half + i] = p.sin_tab[pr * half + i];
+    if (tid < half) {
+      cs_lds[tid] = cs_c;
+      cs_lds[half + tid] = cs_s;
     }
   }
   __syncthreads();
-  if constexpr (XS::kOff != 0.0f) {
-    for (int64_t c = threadIdx.x; c < C; c += 256) {
-      float s = 0.0f;
-      for (int i = 0; i < kc; ++i) {
-        const int64_t j = c * kc + i;
-        s += XS::kBF16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xl)[j])
-                       : reinterpret_cast<const float*>(xl)[j];
-      }
-      corr_lds[c] = XS::kOff * s;
+  if constexpr (XL && XS::kOff != 0.0f) {
+    for (int64_t c = tid; c < C; c += 256) {
+      uint32_t xd[XDW];
+      XL_::load_chunk(xl, c, xd);
+      corr_lds[c] = XS::kOff * XL_::chunk_sum(xd);
     }
     __syncthreads();
   }
-  // this lane's x chunks into registers
-  uint32_t xr[JM][XDW];
-  float corr[JM];
+
+  // ---- 4. second weight block, then this lane's x chunks ----
+  issue(fb, 1);
+  uint32_t xr[XL ? 1 : JM][XDW];
+  float corr[XL ? 1 : JM];
+  if constexpr (!XL) {
 #pragma unroll
-  for (int j = 0; j < JM; ++j) {
-    const int64_t c = lane + 64 * j;
-    const bool ok = j < J && c < C;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(xl) + c * XDW;
+    for (int j = 0; j < JM; ++j) {
+      const int64_t c = lane + 64 * j;
+      if (j < J && c < C) {
+        XL_::load_chunk(xl, c, xr[j]);
+        corr[j] = XS::kOff != 0.0f ? XS::kOff * XL_::chunk_sum(xr[j]) : 0.0f;
+      } else {
 #pragma unroll
-    for (int t = 0; t < XDW; ++t) xr[j][t] = ok ? src[t] : 0u;
-    corr[j] = (XS::kOff != 0.0f && ok) ? corr_lds[c] : 0.0f;
+        for (int t = 0; t < XDW; ++t) xr[j][t] = 0u;
+        corr[j] = 0.0f;
+      }
+    }
   }
 
   float best_v = 0.0f;
   int64_t best_i = -1;
 
+  const Unpack up;
   // Accumulates load block jb of f into acc.
   auto accum = [&](const Frag<JB, P, SC>& f, int jb, float (&acc)[P][2]) {
 #pragma unroll
-    for (int pp = 0; pp < P; ++pp) {
+    for (int jj = 0; jj < JB; ++jj) {
+      const int j = jb * JB + jj;
+      uint32_t xc[XL ? XDW : 1];
+      const uint32_t* xd;
+      float cj;
+      if constexpr (XL) {
+        const int64_t c = lane + 64 * j;
+        const bool ok = j < J && c < C;
+        XL_::load_chunk(xl, ok ? c : 0, xc);
+        if (!ok) {
 #pragma unroll
-      for (int jj = 0; jj < JB; ++jj) {
-        const int j = jb * JB + jj;
+          for (int t = 0; t < XDW; ++t) xc[t] = 0u;
+        }
+        xd = xc;
+        cj = (XS::kOff != 0.0f && ok) ? corr_lds[c] : 0.0f;
+      } else {
+        xd = xr[jj];
+        cj = corr[jj];
+      }
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) {
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
-          float dv = chunk_dot<A, WF>(f.w[pp][rr][jj], xr[j]);
-          if constexpr (XS::kOff != 0.0f) dv -= corr[j];
+          // the offset correction seeds the accumulator: dv = dot - kOff * sum(x)
+          const float dv = chunk_dot<A, WF>(f.w[pp][rr][jj], xd, XS::kOff != 0.0f ? -cj : 0.0f, up);
           if constexpr (SC)
             acc[pp][rr] = fmaf(f16_bits_to_f32(f.s[pp][rr][jj]), dv, acc[pp][rr]);
           else
             acc[pp][rr] += dv;
         }
       }
-      if constexpr (WF == AM_WF_INT8) {
-        if (jb == NB - 1) {  // per-row scale after the last block of the row
+    }
+    if constexpr (WF == AM_WF_INT8) {
+      if (jb == NB - 1) {  // per-row scale after the last block of the row
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
           acc[pp][0] *= f.s8[pp][0];
           acc[pp][1] *= f.s8[pp][1];
         }
@@ -354,7 +555,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     }
   };
 
-  // Reduces acc across the wave and applies the epilogue of iteration itc.
+  // Reduces acc across the wave, applies the epilogue of iteration itc, zeroes acc.
   auto finish = [&](float (&acc)[P][2], int64_t itc) {
 #pragma unroll
     for (int pp = 0; pp < P; ++pp) {
@@ -423,22 +624,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
         }
       }
     }
-  };
-
-  // Each iteration's loads are all issued before any of them is used; the next
-  // iteration's first block is issued as soon as the registers are consumed, so its
-  // latency overlaps the cross-lane reduction and the epilogue stores.
-  while (it < niter) {
-    float acc[P][2] = {};
 #pragma unroll
-    for (int jb = 0; jb < NB; ++jb) {
-      if (jb > 0) issue(fa, it, jb);
-      accum(fa, jb, acc);
+    for (int pp = 0; pp < P; ++pp) acc[pp][0] = acc[pp][1] = 0.0f;
+  };
+  auto blk_jb = [&](int64_t b) { return NB == 1 ? 0 : static_cast<int>(b % NB); };
+  auto blk_it = [&](int64_t b) { return gw + (NB == 1 ? b : b / NB) * TW; };
+
+  // ---- 5. main loop: blocks alternate between fa and fb; the block after next is
+  // issued as soon as a buffer has been consumed, so one block is always in flight
+  // while the other is reduced.  The exits sit before the issues, so on the path
+  // that stays in the loop both buffers are always pending in the same order. ----
+  float acc[P][2] = {};
+  int64_t b = 0;
+  while (b < nblk) {
+    accum(fa, blk_jb(b), acc);
+    if (blk_jb(b) == NB - 1) finish(acc, blk_it(b));
+    if (b + 2 >= nblk) {
+      if (b + 1 < nblk) {
+        accum(fb, blk_jb(b + 1), acc);
+        if (blk_jb(b + 1) == NB - 1) finish(acc, blk_it(b + 1));
+      }
+      break;
     }
-    const int64_t nx = it + TW;
-    if (nx < niter) issue(fa, nx, 0);
-    finish(acc, it);
-    it = nx;
+    issue(fa, b + 2);
+    accum(fb, blk_jb(b + 1), acc);
+    if (blk_jb(b + 1) == NB - 1) finish(acc, blk_it(b + 1));
+    if (b + 3 >= nblk) {
+      accum(fa, blk_jb(b + 2), acc);
+      if (blk_jb(b + 2) == NB - 1) finish(acc, blk_it(b + 2));
+      break;
+    }
+    issue(fb, b + 3);
+    b += 2;
   }
 
   if constexpr (EPI == kEpiLmHead) {
@@ -532,7 +749,8 @@ template <class A, int WF, bool NORM, int EPI, int JM, int P>
 am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t tb = A::kDtype == AM_DT_BF16 ? 2 : 4;
-  int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (((g.row_bytes / 16) * 4 + 15) / 16) * 16;
+  constexpr bool XL = JM * XS::kDW > 32;
+  int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (XL ? (((g.row_bytes / 16) * 4 + 15) / 16) * 16 : 0);
   if (EPI == kEpiResidual) lds += ((g.n * tb + 15) / 16) * 16;
   if (EPI == kEpiQkv) lds += g.d * 4;
   if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
@@ -555,20 +773,25 @@ am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   const int64_t waves = CeilDiv(niter, ipw);
   int64_t blocks = CeilDiv(waves, 4);
   if (blocks > 65536) blocks = 65536;
+  GemvArgs ga = g;
+  auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  ga.vec = al16(g.x) && (g.k * tb) % 16 == 0 && (!NORM || al16(g.norm_w)) &&
+           (EPI != kEpiResidual || (al16(g.residual) && (g.n * tb) % 16 == 0));
   hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                     static_cast<size_t>(lds), s, g);
+                     static_cast<size_t>(lds), s, ga);
   AM_RETURN_IF_LAUNCH_FAILED("gemv");
   return AM_STATUS_OK;
 }
 
-// Chunk-steps per row decide the register tiling: x stays in registers for up to
-// 16 chunk-steps (bounded by 128 dwords of x per lane).
+// Chunk-steps per row (J) pick the instantiation: JM >= J chunk-steps per lane,
+// bounded so the prologue's x pieces per thread stay within 32 registers.
 template <class A, int WF, bool NORM, int EPI>
 am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t J = CeilDiv(g.row_bytes / 16, 64);
   if (J <= 2) return LaunchJ<A, WF, NORM, EPI, 2, 2>(g, s);
-  if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, 2>(g, s);
+  // x in registers: two row pairs per iteration; x read from LDS: one
+  if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, (4 * XS::kDW > 32 ? 1 : 2)>(g, s);
   if constexpr (8 * XS::kDW <= 128) {
     if (J <= 8) return LaunchJ<A, WF, NORM, EPI, 8, 1>(g, s);
   }
@@ -639,6 +862,7 @@ extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a,
   AM_CHECK_ARG(a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0 && a->head_dim > 0 && a->head_dim % 2 == 0,
                "fused_qkv: bad head configuration");
   AM_CHECK_ARG(a->w_qkv.n == (a->hq + 2 * a->hkv) * a->head_dim, "fused_qkv: weight rows != (hq+2hkv)*d");
+  AM_CHECK_ARG(a->head_dim <= 512, "fused_qkv: head_dim above 512");
   AM_CHECK_ARG(a->h && a->norm_w && a->cos_tab && a->sin_tab && a->pos && a->q_out && a->k_cache && a->v_cache,
                "fused_qkv: null pointer");
   AM_CHECK_ARG(a->eps > 0.0f, "fused_qkv: eps must be positive");
