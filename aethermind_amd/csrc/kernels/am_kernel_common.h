@@ -33,10 +33,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as
 
 // float -> bf16 round-to-nearest-even, NaN -> 0x7FC0 (the reference's conversion,
 // bfloat16.cpp:20-32).
+// The conversion is v_cvt_pk_bf16_f32 (RNE); only NaN needs the canonical pattern.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
-  const uint32_t x = __float_as_uint(v);
-  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-  return static_cast<uint16_t>((x + (((x >> 16) & 1u) + 0x7FFFu)) >> 16);
+  const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  return v != v ? static_cast<uint16_t>(0x7FC0u) : h;
 }
 
 struct ActF32 {

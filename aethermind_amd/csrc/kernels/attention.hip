@@ -5,13 +5,16 @@
 // contiguous slice of positions.  Inside the block:
 //   * D/8 lanes cover one cache row (8 elements = 16 bytes of bf16 each), so a wave
 //     reads 64/(D/8) consecutive rows per load instruction: for D = 128 that is four
-//     256-byte rows = 1 KiB contiguous per instruction.
-//   * Each lane group keeps an fp32 online softmax (running max, sum, output slice);
-//     groups are merged with xor shuffles, waves through LDS.
-//   * splits > 1: partial (m, l, o) go to the workspace and the last block of the
-//     (row, kv head) pair, picked with an atomic ticket, merges them in order and
-//     resets the ticket, so the kernel needs no separate combine launch and no
-//     memset between calls (safe to capture in a HIP graph).
+//     256-byte rows = 1 KiB contiguous per instruction.  Each lane group loads U rows
+//     before using any of them, so U KiB per wave are in flight at once.
+//   * Each lane group keeps an fp32 online softmax (running max, sum, output slice)
+//     in base 2: q is pre-scaled by log2(e)/sqrt(d), so every exponential is one
+//     v_exp_f32.  Row dot products are summed over the lane group with DPP.
+//     Groups are merged with xor shuffles, waves through LDS.
+//   * The split count follows the live context (at least kMinPerSplit positions per
+//     split); with one split the block writes the output, otherwise it writes a
+//     partial record (m, l, o) and attention_combine_kernel, launched right after on
+//     the same stream, merges the records.  No atomics, fences or zeroed scratch.
 
 #include <cmath>
 
@@ -29,13 +32,13 @@ struct AttnArgs {
   const int64_t* start_dev;
   int64_t cbs;  // cache batch stride (elements)
   int32_t splits;
-  float scale;
+  float scale;  // log2(e) / sqrt(d)
   float* part;
-  unsigned* tickets;
 };
 
 // Fewest cache positions one split block handles (short contexts use fewer splits).
-constexpr int64_t kMinPerSplit = 32;
+constexpr int64_t kMinPerSplit = 64;
+constexpr float kLog2e = 1.4426950408889634f;
 
 template <class A>
 __device__ __forceinline__ void load8(const typename A::T* p, float* out) {
@@ -55,25 +58,84 @@ __device__ __forceinline__ void load8(const typename A::T* p, float* out) {
   }
 }
 
-// merge (m2, l2, o2) into (m, l, o)
+// Raw 16 bytes of one lane's slice of a cache row (bf16: 8 values; f32: 4 + 4).
+template <class A>
+struct RowSlice {
+  uint4 a, b;
+};
+template <class A>
+__device__ __forceinline__ RowSlice<A> load_slice(const typename A::T* p) {
+  RowSlice<A> r;
+  r.a = *reinterpret_cast<const uint4*>(p);
+  if constexpr (A::kDtype != AM_DT_BF16) r.b = *reinterpret_cast<const uint4*>(p + 4);
+  return r;
+}
+template <class A>
+__device__ __forceinline__ void unpack_slice(const RowSlice<A>& r, float* out) {
+  const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+  if constexpr (A::kDtype == AM_DT_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(w[i] << 16);
+      out[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  } else {
+    const uint32_t v[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = __uint_as_float(w[i]);
+      out[4 + i] = __uint_as_float(v[i]);
+    }
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of LP lanes (LP = 8 or 16); every lane receives its sum.
+template <int LP>
+__device__ __forceinline__ float group_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of the 8-lane half
+  if constexpr (LP == 16) v = dpp_add<0x140>(v);  // row_mirror: the other half of the row
+  return v;
+}
+
+// merge (m2, l2, o2) into (m, l, o); base-2 exponentials
 __device__ __forceinline__ void merge_state(float& m, float& l, float* o, float m2, float l2, const float* o2) {
   const float mn = fmaxf(m, m2);
   if (mn == -INFINITY) return;
-  const float c1 = expf(m - mn), c2 = expf(m2 - mn);
+  const float c1 = exp2f(m - mn), c2 = exp2f(m2 - mn);
   l = l * c1 + l2 * c2;
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = o[i] * c1 + o2[i] * c2;
   m = mn;
 }
 
+// live split count of a (row, kv head): every block and the combine agree on it
+__device__ __forceinline__ int64_t live_splits(int64_t n_keys, int32_t splits) {
+  int64_t ns = (n_keys + kMinPerSplit - 1) / kMinPerSplit;
+  if (ns > splits) ns = splits;
+  if (ns < 1) ns = 1;
+  return ns;
+}
+
+__device__ __forceinline__ int64_t row_keys(const AttnArgs& p, int64_t b, int64_t s) {
+  const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
+  return start + s + 1 <= p.cap ? start + s + 1 : p.cap;
+}
+
 template <class A, int D, int G>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   constexpr int LP = D / 8;      // lanes per cache row
   constexpr int PPW = 64 / LP;   // rows per wave step
+  constexpr int U = 4;           // rows per lane group loaded before use
+  constexpr int STEP = 4 * PPW;  // rows per block step
   using T = typename A::T;
   __shared__ float sm_m[4][G], sm_l[4][G];
   __shared__ float sm_o[4][G][D];
-  __shared__ bool last;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % LP, ps = lane / LP;
@@ -81,15 +143,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const int64_t b = qr / p.seq, s = qr % p.seq;
   const int64_t g = blockIdx.y;
   const int split = blockIdx.x;
-  const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
-  const int64_t n_keys = start + s + 1 <= p.cap ? start + s + 1 : p.cap;
-  // Splits actually used for this row: at least kMinPerSplit positions each, so
-  // short contexts do not pay for merging many near-empty partials.  Every block of
-  // the (row, kv head) group computes the same count; surplus blocks leave at once.
-  int64_t nsplit = (n_keys + kMinPerSplit - 1) / kMinPerSplit;
-  if (nsplit > p.splits) nsplit = p.splits;
-  if (nsplit < 1) nsplit = 1;
-  if (split >= nsplit) return;
+  const int64_t n_keys = row_keys(p, b, s);
+  const int64_t nsplit = live_splits(n_keys, p.splits);
+  if (split >= nsplit) return;  // surplus block for this context
   const int64_t per = (n_keys + nsplit - 1) / nsplit;
   const int64_t lo = split * per;
   const int64_t hi = lo + per < n_keys ? lo + per : n_keys;
@@ -114,24 +170,37 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     for (int i = 0; i < 8; ++i) o[hh][i] = 0.0f;
   }
 
-  for (int64_t pos = lo + wave * PPW + ps; pos < hi; pos += 4 * PPW) {
-    float kv[8], vv[8];
-    load8<A>(kbase + pos * D, kv);
-    load8<A>(vbase + pos * D, vv);
+  for (int64_t base = lo + wave * PPW + ps; base < hi; base += U * STEP) {
+    RowSlice<A> kr[U], vr[U];
+    bool ok[U];
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      float d = 0.0f;
+    for (int u = 0; u < U; ++u) {
+      int64_t pos = base + u * STEP;
+      ok[u] = pos < hi;
+      if (!ok[u]) pos = lo;  // in-bounds address, result discarded
+      kr[u] = load_slice<A>(kbase + pos * D);
+      vr[u] = load_slice<A>(vbase + pos * D);
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d = fmaf(qv[hh][i], kv[i], d);
+    for (int u = 0; u < U; ++u) {
+      float kv[8], vv[8];
+      unpack_slice<A>(kr[u], kv);
+      unpack_slice<A>(vr[u], vv);
 #pragma unroll
-      for (int off = LP / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
-      const float mn = fmaxf(m[hh], d);
-      const float c = expf(m[hh] - mn);
-      const float e = expf(d - mn);
-      l[hh] = l[hh] * c + e;
+      for (int hh = 0; hh < G; ++hh) {
+        float d = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[hh][i] = fmaf(o[hh][i], c, e * vv[i]);
-      m[hh] = mn;
+        for (int i = 0; i < 8; ++i) d = fmaf(qv[hh][i], kv[i], d);
+        d = group_sum<LP>(d);
+        if (!ok[u]) d = -INFINITY;
+        const float mn = fmaxf(m[hh], d);
+        const float c = mn == -INFINITY ? 1.0f : exp2f(m[hh] - mn);
+        const float e = ok[u] ? exp2f(d - mn) : 0.0f;
+        l[hh] = fmaf(l[hh], c, e);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[hh][i] = fmaf(o[hh][i], c, e * vv[i]);
+        m[hh] = mn;
+      }
     }
   }
   // merge the PPW row streams of the wave (lanes sub, sub+LP, ...)
@@ -184,54 +253,45 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) rec[hh * (D + 2) + 2 + sub * 8 + i] = o[hh][i];
       }
-      __threadfence();
     }
   }
+}
+
+// Merges the split records of one (query row, q head): grid = (hq, batch*seq), D
+// threads, one output dimension each.  Rows that used a single split were written by
+// attention_kernel and are left alone.
+template <class A, int D>
+__global__ __launch_bounds__(D) void attention_combine_kernel(AttnArgs p) {
+  using T = typename A::T;
+  const int64_t h = blockIdx.x, qr = blockIdx.y;
+  const int64_t b = qr / p.seq, s = qr % p.seq;
+  const int64_t n_keys = row_keys(p, b, s);
+  const int64_t nsplit = live_splits(n_keys, p.splits);
   if (nsplit == 1) return;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned t = atomicAdd(&p.tickets[qr * p.hkv + g], 1u);
-    last = (t == static_cast<unsigned>(nsplit - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // acquire: the other blocks' partial records are visible now
-  // Parallel merge: thread t owns head t / (D / DPT) and DPT consecutive dims; every
-  // split's record is read with plain (pipelined) loads.
-  constexpr int DPT = (D * G) / 256 > 0 ? (D * G) / 256 : 1;
-  constexpr int TPH = D / DPT;  // threads per head
-  const int hh = threadIdx.x / TPH;
-  const int d0 = (threadIdx.x % TPH) * DPT;
-  if (hh < G) {
-    const float* base = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2) + hh * (D + 2);
-    float mx = -INFINITY;
-    for (int64_t sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, base[sp * G * (D + 2)]);
-    float den = 0.0f;
-    float acc[DPT];
-#pragma unroll
-    for (int i = 0; i < DPT; ++i) acc[i] = 0.0f;
-    if (mx != -INFINITY) {
-      for (int64_t sp = 0; sp < nsplit; ++sp) {
-        const float* rec = base + sp * G * (D + 2);
-        const float c = expf(rec[0] - mx);
-        den = fmaf(rec[1], c, den);
-#pragma unroll
-        for (int i = 0; i < DPT; ++i) acc[i] = fmaf(rec[2 + d0 + i], c, acc[i]);
-      }
+  const int64_t G = p.hq / p.hkv;
+  const int64_t g = h / G, hh = h % G;
+  const float* base = p.part + ((qr * p.hkv + g) * p.splits * G + hh) * (D + 2);
+  const int64_t rs = G * (D + 2);  // record stride between splits
+  float mx = -INFINITY;
+  for (int64_t sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, base[sp * rs]);
+  float den = 0.0f, acc = 0.0f;
+  if (mx != -INFINITY) {
+    for (int64_t sp = 0; sp < nsplit; ++sp) {
+      const float* rec = base + sp * rs;
+      const float c = exp2f(rec[0] - mx);
+      den = fmaf(rec[1], c, den);
+      acc = fmaf(rec[2 + threadIdx.x], c, acc);
     }
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D + d0;
-#pragma unroll
-    for (int i = 0; i < DPT; ++i) A::store(out, i, acc[i] * inv);
   }
-  if (threadIdx.x == 0) p.tickets[qr * p.hkv + g] = 0u;
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  T* out = static_cast<T*>(p.out) + (qr * p.hq + h) * D;
+  A::store(out, threadIdx.x, acc * inv);
 }
 
 int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
   if (requested > 0) return requested;
   if (seq > 1) return 1;
-  int64_t s = cap / 128;
+  int64_t s = cap / kMinPerSplit;
   if (s < 1) s = 1;
   if (s > 64) s = 64;
   return static_cast<int>(s);
@@ -247,6 +307,10 @@ am_status_code LaunchD(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
     default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
   }
   AM_RETURN_IF_LAUNCH_FAILED("attention");
+  if (a.splits > 1) {
+    hipLaunchKernelGGL((attention_combine_kernel<A, D>), dim3(static_cast<unsigned>(a.hq), grid.z), dim3(D), 0, s, a);
+    AM_RETURN_IF_LAUNCH_FAILED("attention combine");
+  }
   return AM_STATUS_OK;
 }
 
@@ -257,10 +321,10 @@ using namespace am;
 
 extern "C" int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
                                                        int64_t head_dim, int64_t capacity, int32_t num_splits) {
+  (void)hkv;
   const int splits = ChooseSplits(seq, capacity, num_splits);
-  const int64_t tickets = 256 * CeilDiv(batch * seq * hkv * 4, 256);
-  if (splits == 1) return tickets;
-  return tickets + batch * seq * hq * splits * (head_dim + 2) * 4;
+  if (splits == 1) return 0;
+  return batch * seq * hq * splits * (head_dim + 2) * 4;
 }
 
 extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a, void* stream) {
@@ -292,12 +356,8 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
   p.start_dev = a->start_pos_dev;
   p.cbs = batch > 1 ? a->cache_batch_stride : 0;
   p.splits = splits;
-  p.scale = 1.0f / sqrtf(static_cast<float>(a->head_dim));
-  if (splits > 1) {
-    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
-    p.tickets = reinterpret_cast<unsigned*>(ws);
-    p.part = reinterpret_cast<float*>(ws + 256 * CeilDiv(batch * a->seq * a->hkv * 4, 256));
-  }
+  p.scale = kLog2e / sqrtf(static_cast<float>(a->head_dim));
+  if (splits > 1) p.part = static_cast<float*>(a->workspace);
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   const int64_t G = a->hq / a->hkv;
   hipStream_t s = AsStream(stream);

@@ -140,19 +140,74 @@ __device__ __forceinline__ float chunk_dot(const uint4 w, const uint32_t* xd, fl
   return acc;
 }
 
-// Sum over the 64 lanes: DPP inside each 16-lane row (quad swaps, then row
-// rotations by 4 and 8), then the four row sums through readlane.  The result is
-// wave-uniform.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
-  const int b = __builtin_bit_cast(int, v);
-  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
-         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+// ---- cross-lane reduction of one iteration's row sums ----
+// Every lane holds partial sums of the 2P rows of an iteration (P pairs).  A butterfly
+// of gfx950 permlane swaps (32-lane halves, then 16-lane rows), one DPP row rotation
+// and DPP adds folds all rows at once; a final swap leaves both rows of pair pp in
+// one lane, so the epilogue of every pair runs in the same instruction stream.
+//   v_permlane32_swap(a, b) -> {[a.lo, b.lo], [a.hi, b.hi]}
+//   v_permlane16_swap(a, b) -> {[a.r0, b.r0, a.r2, b.r2], [a.r1, b.r1, a.r3, b.r3]}
+__device__ __forceinline__ float swap32_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_add(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// sum over each aligned 8-lane group (every lane receives it)
+__device__ __forceinline__ float sum8(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  return dpp_add<0x141>(v);  // row_half_mirror
+}
+__device__ __forceinline__ float sum16(float v) { return dpp_add<0x140>(sum8(v)); }  // + row_mirror
+
+// acc[pp][rr] partial sums -> (a0, a1) = full sums of pair pp in the lane that owns it;
+// returns pp for that lane, -1 elsewhere.
+template <int P>
+__device__ __forceinline__ int reduce_pairs(const float (&acc)[P][2], int lane, float& a0, float& a1) {
+  if constexpr (P == 1) {
+    float x = swap32_add(acc[0][0], acc[0][1]);  // [v0 | v1] halves
+    x = swap16_add(x, x);                        // each 16-lane row: its half folded to 16 lanes
+    x = sum16(x);                                // lanes 0-31: v0, 32-63: v1
+    const auto w = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a0 = __uint_as_float(w[0]);
+    a1 = __uint_as_float(w[1]);
+    return lane == 0 ? 0 : -1;
+  } else if constexpr (P == 2) {
+    const float x0 = swap32_add(acc[0][0], acc[1][0]);  // [v0 | v2]
+    const float x1 = swap32_add(acc[0][1], acc[1][1]);  // [v1 | v3]
+    float y = swap16_add(x0, x1);                       // rows [v0, v1, v2, v3]
+    y = sum16(y);
+    const auto w = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    a0 = __uint_as_float(w[0]);  // lane 0: pair 0, lane 32: pair 1
+    a1 = __uint_as_float(w[1]);
+    return (lane & 31) == 0 ? (lane >> 5) : -1;
+  } else {
+    static_assert(P == 4, "pairs per iteration: 1, 2 or 4");
+    // v_k = acc[k / 2][k % 2]
+    const float x0 = swap32_add(acc[0][0], acc[2][0]);  // [v0 | v4]
+    const float x1 = swap32_add(acc[0][1], acc[2][1]);  // [v1 | v5]
+    const float x2 = swap32_add(acc[1][0], acc[3][0]);  // [v2 | v6]
+    const float x3 = swap32_add(acc[1][1], acc[3][1]);  // [v3 | v7]
+    const float y0 = swap16_add(x0, x1);                // rows [v0, v1, v4, v5]
+    const float y1 = swap16_add(x2, x3);                // rows [v2, v3, v6, v7]
+    // fold each row to 8 lanes: low 8 lanes keep y0's row, high 8 lanes y1's
+    const bool hi8 = (lane & 8) != 0;
+    const float keep = hi8 ? y1 : y0, send = hi8 ? y0 : y1;
+    float z = keep + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0x128, 0xF,
+                                                                         0xF, false));  // row_ror:8
+    z = sum8(z);  // 8-lane groups: row0 [v0|v2], row1 [v1|v3], row2 [v4|v6], row3 [v5|v7]
+    const auto w = __builtin_amdgcn_permlane16_swap(__float_as_uint(z), __float_as_uint(z), false, false);
+    a0 = __uint_as_float(w[0]);  // lanes 0, 8, 32, 40: pairs 0, 1, 2, 3
+    a1 = __uint_as_float(w[1]);
+    return ((lane & 23) == 0) ? (((lane >> 5) << 1) | ((lane >> 3) & 1)) : -1;
+  }
 }
 
 __device__ __forceinline__ float silu_ref(float g) {
@@ -280,10 +335,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   const int64_t K = p.k;
   const int64_t C = p.row_bytes / 16;  // chunks per row
   const int J = static_cast<int>((C + 63) / 64);
-  // LDS: x | per-chunk corrections (x-in-LDS variant) | residual | cos,sin
+  // LDS: x | per-chunk offset corrections (INT formats) | residual | cos,sin
   uint8_t* xl = smem;
   const int64_t off_corr = ((K * XS::kBytes + 15) / 16) * 16;
-  const int64_t off_res = off_corr + (XL ? ((C * 4 + 15) / 16) * 16 : 0);
+  const int64_t off_res = off_corr + (XS::kOff != 0.0f ? ((C * 4 + 15) / 16) * 16 : 0);
   const int64_t off_cs = off_res + (EPI == kEpiResidual ? ((p.n * static_cast<int64_t>(sizeof(T)) + 15) / 16) * 16 : 0);
   float* corr_lds = reinterpret_cast<float*>(smem + off_corr);
   T* res_lds = reinterpret_cast<T*>(smem + off_res);
@@ -395,7 +450,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   // The vector pass runs on every path with clamped indices, so the register arrays
   // are consumed in straight-line code (nothing moves the loads behind the weights);
   // without the vector layout it only writes placeholders that the element pass
-  // below overwrites.
+  // below overwrites.  Each 16-byte input piece is staged with one or two 16-byte LDS
+  // stores; the per-chunk offset corrections are summed over the aligned lane group
+  // that holds the chunk's pieces (consecutive threads hold consecutive pieces).
   {
     const bool vec = p.vec != 0;
     float inv = 1.0f;
@@ -416,20 +473,51 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     const int64_t xlast = vec ? xpieces - 1 : 0;
 #pragma unroll
     for (int v = 0; v < XP; ++v) {
-      int64_t pi = tid + 256 * v;
-      if (pi > xlast) pi = xlast;
-      if constexpr (!NORM && XS::kBytes == sizeof(T) && XL_::CB >= 16) {
-        // a piece of the input is exactly one 16-byte LDS piece
-        *reinterpret_cast<uint4*>(xl + XL_::addr(pi * EPP)) = xv[v];
+      const int64_t pi0 = tid + 256 * v;
+      const bool ok = vec && pi0 < xpieces;
+      const int64_t pi = pi0 > xlast ? xlast : pi0;
+      float xs[EPP];  // staged values (bf16-exact when LDS holds bf16)
+      if constexpr (XS::kBF16) {
+        uint32_t packed[4];
+        if constexpr (NORM) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float x0 = (piece_elem<A>(xv[v], 2 * t) * inv) * piece_elem<A>(nv[v], 2 * t);
+            const float x1 = (piece_elem<A>(xv[v], 2 * t + 1) * inv) * piece_elem<A>(nv[v], 2 * t + 1);
+            const bf16x2_t h = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};  // RNE
+            packed[t] = __builtin_bit_cast(uint32_t, h);
+          }
+        } else {
+          packed[0] = xv[v].x; packed[1] = xv[v].y; packed[2] = xv[v].z; packed[3] = xv[v].w;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          xs[2 * t] = __uint_as_float(packed[t] << 16);
+          xs[2 * t + 1] = __uint_as_float(packed[t] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<uint4*>(xl + XL_::addr(pi * EPP)) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
       } else {
 #pragma unroll
         for (int e = 0; e < EPP; ++e) {
           float x = piece_elem<A>(xv[v], e);
           if constexpr (NORM) x = A::round((x * inv) * piece_elem<A>(nv[v], e));
-          int64_t j = pi * EPP + e;
-          if (j >= K) j = K - 1;
-          XL_::store(xl, j, x);
+          xs[e] = x;
         }
+#pragma unroll
+        for (int h = 0; h < EPP / 4; ++h)
+          *reinterpret_cast<float4*>(xl + XL_::addr(pi * EPP + 4 * h)) =
+              make_float4(xs[4 * h], xs[4 * h + 1], xs[4 * h + 2], xs[4 * h + 3]);
+      }
+      if constexpr (XS::kOff != 0.0f) {
+        constexpr int PPC = kc / EPP;  // input pieces per weight chunk: 2, 4 or 8
+        float ps = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPP; ++e) ps += xs[e];
+        if (!ok) ps = 0.0f;
+        ps = dpp_add<0xB1>(ps);
+        if constexpr (PPC >= 4) ps = dpp_add<0x4E>(ps);
+        if constexpr (PPC >= 8) ps = dpp_add<0x141>(ps);
+        if (ok && (tid % PPC) == 0) corr_lds[pi / PPC] = XS::kOff * ps;
       }
     }
     if constexpr (EPI == kEpiResidual) {
@@ -468,6 +556,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       const T* res = static_cast<const T*>(p.residual);
       for (int64_t r = tid; r < p.n; r += 256) res_lds[r] = res[r];
     }
+    if constexpr (XS::kOff != 0.0f) {
+      __syncthreads();
+      for (int64_t c = tid; c < C; c += 256) {
+        uint32_t xd[XDW];
+        XL_::load_chunk(xl, c, xd);
+        corr_lds[c] = XS::kOff * XL_::chunk_sum(xd);
+      }
+    }
   }
   if constexpr (EPI == kEpiQkv) {
     const int64_t half = p.d / 2;
@@ -477,14 +573,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     }
   }
   __syncthreads();
-  if constexpr (XL && XS::kOff != 0.0f) {
-    for (int64_t c = tid; c < C; c += 256) {
-      uint32_t xd[XDW];
-      XL_::load_chunk(xl, c, xd);
-      corr_lds[c] = XS::kOff * XL_::chunk_sum(xd);
-    }
-    __syncthreads();
-  }
 
   // ---- 4. second weight block, then this lane's x chunks ----
   issue(fb, 1);
@@ -496,7 +584,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       const int64_t c = lane + 64 * j;
       if (j < J && c < C) {
         XL_::load_chunk(xl, c, xr[j]);
-        corr[j] = XS::kOff != 0.0f ? XS::kOff * XL_::chunk_sum(xr[j]) : 0.0f;
+        corr[j] = XS::kOff != 0.0f ? corr_lds[c] : 0.0f;
       } else {
 #pragma unroll
         for (int t = 0; t < XDW; ++t) xr[j][t] = 0u;
@@ -555,77 +643,68 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     }
   };
 
-  // Reduces acc across the wave, applies the epilogue of iteration itc, zeroes acc.
+  // Reduces acc across the wave, applies the epilogue of iteration itc in the lane
+  // that owns each pair, zeroes acc.
   auto finish = [&](float (&acc)[P][2], int64_t itc) {
+    float a0, a1;
+    const int pp = reduce_pairs<P>(acc, lane, a0, a1);
 #pragma unroll
-    for (int pp = 0; pp < P; ++pp) {
-      acc[pp][0] = wave_sum_dpp(acc[pp][0]);
-      acc[pp][1] = wave_sum_dpp(acc[pp][1]);
-    }
-#pragma unroll
-    for (int pp = 0; pp < P; ++pp) {
-      const int64_t u = itc * P + pp;
-      if (u >= p.units) break;
-      int64_t r0, r1;
-      pair_rows<EPI>(p, u, r0, r1);
-      const bool v1 = r1 < p.n;
-      const float a0 = acc[pp][0], a1 = acc[pp][1];
-      if constexpr (EPI == kEpiLmHead) {
-        if (lane == 0) {
-          float* lg = static_cast<float*>(p.out);
-          if (lg != nullptr) {
-            lg[r0] = a0;
-            if (v1) lg[r1] = a1;
-          }
+    for (int q = 0; q < P; ++q) acc[q][0] = acc[q][1] = 0.0f;
+    if (pp < 0) return;
+    const int64_t u = itc * P + pp;
+    if (u >= p.units) return;
+    int64_t r0, r1;
+    pair_rows<EPI>(p, u, r0, r1);
+    const bool v1 = r1 < p.n;
+    T* out = static_cast<T*>(p.out);
+    if constexpr (EPI == kEpiLmHead) {
+      float* lg = static_cast<float*>(p.out);
+      if (lg != nullptr) {
+        lg[r0] = a0;
+        if (v1) lg[r1] = a1;
+      }
+      if (argmax_better(a0, r0, best_v, best_i)) { best_v = a0; best_i = r0; }
+      if (v1 && argmax_better(a1, r1, best_v, best_i)) { best_v = a1; best_i = r1; }
+    } else if constexpr (EPI == kEpiStore) {
+      if (p.out_f32) {
+        float* of = static_cast<float*>(p.out);
+        of[r0] = a0;
+        if (v1) of[r1] = a1;
+      } else {
+        A::store(out, r0, a0);
+        if (v1) A::store(out, r1, a1);
+      }
+    } else if constexpr (EPI == kEpiResidual) {
+      A::store(out, r0, A::load(res_lds, r0) + A::round(a0));
+      if (v1) A::store(out, r1, A::load(res_lds, r1) + A::round(a1));
+    } else if constexpr (EPI == kEpiGateUp) {
+      const float g = A::round(a0), up = A::round(a1);
+      A::store(out, u, silu_ref(g) * up);
+    } else if constexpr (EPI == kEpiQkv) {
+      const int64_t half = p.d / 2;
+      const int64_t head = u / half, i = u % half;
+      const float y0 = A::round(a0), y1 = A::round(a1);
+      if (head < p.hq + p.hkv) {
+        const float c = cs_lds[i], s = cs_lds[half + i];
+        const float o0 = y0 * c - y1 * s;
+        const float o1 = y1 * c + y0 * s;
+        if (head < p.hq) {
+          T* q = static_cast<T*>(p.q_out);
+          A::store(q, head * p.d + i, o0);
+          A::store(q, head * p.d + i + half, o1);
+        } else if (posv < p.cap) {
+          T* kc = static_cast<T*>(p.k_cache);
+          const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
+          A::store(kc, base + i, o0);
+          A::store(kc, base + i + half, o1);
         }
-        if (argmax_better(a0, r0, best_v, best_i)) { best_v = a0; best_i = r0; }
-        if (v1 && argmax_better(a1, r1, best_v, best_i)) { best_v = a1; best_i = r1; }
-      } else if (lane == pp) {
-        T* out = static_cast<T*>(p.out);
-        if constexpr (EPI == kEpiStore) {
-          if (p.out_f32) {
-            float* of = static_cast<float*>(p.out);
-            of[r0] = a0;
-            if (v1) of[r1] = a1;
-          } else {
-            A::store(out, r0, a0);
-            if (v1) A::store(out, r1, a1);
-          }
-        } else if constexpr (EPI == kEpiResidual) {
-          A::store(out, r0, A::load(res_lds, r0) + A::round(a0));
-          if (v1) A::store(out, r1, A::load(res_lds, r1) + A::round(a1));
-        } else if constexpr (EPI == kEpiGateUp) {
-          const float g = A::round(a0), up = A::round(a1);
-          A::store(out, u, silu_ref(g) * up);
-        } else if constexpr (EPI == kEpiQkv) {
-          const int64_t half = p.d / 2;
-          const int64_t head = u / half, i = u % half;
-          const float y0 = A::round(a0), y1 = A::round(a1);
-          if (head < p.hq + p.hkv) {
-            const float c = cs_lds[i], s = cs_lds[half + i];
-            const float o0 = y0 * c - y1 * s;
-            const float o1 = y1 * c + y0 * s;
-            if (head < p.hq) {
-              T* q = static_cast<T*>(p.q_out);
-              A::store(q, head * p.d + i, o0);
-              A::store(q, head * p.d + i + half, o1);
-            } else if (posv < p.cap) {
-              T* kc = static_cast<T*>(p.k_cache);
-              const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
-              A::store(kc, base + i, o0);
-              A::store(kc, base + i + half, o1);
-            }
-          } else if (posv < p.cap) {
-            T* vc = static_cast<T*>(p.v_cache);
-            const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
-            A::store(vc, base + i, y0);
-            A::store(vc, base + i + half, y1);
-          }
-        }
+      } else if (posv < p.cap) {
+        T* vc = static_cast<T*>(p.v_cache);
+        const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
+        A::store(vc, base + i, y0);
+        A::store(vc, base + i + half, y1);
       }
     }
-#pragma unroll
-    for (int pp = 0; pp < P; ++pp) acc[pp][0] = acc[pp][1] = 0.0f;
   };
   auto blk_jb = [&](int64_t b) { return NB == 1 ? 0 : static_cast<int>(b % NB); };
   auto blk_it = [&](int64_t b) { return gw + (NB == 1 ? b : b / NB) * TW; };
@@ -665,6 +744,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     __shared__ int64_t bi_s[4];
     __shared__ bool last;
     const int wave = threadIdx.x >> 6;
+    // each pair lane holds the best of its rows: reduce over the wave first
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best_v, o, 64);
+      const int64_t oi = __shfl_xor(best_i, o, 64);
+      if (oi >= 0 && argmax_better(ov, oi, best_v, best_i)) { best_v = ov; best_i = oi; }
+    }
     if (lane == 0) {
       bv_s[wave] = best_v;
       bi_s[wave] = best_i;
@@ -749,8 +835,7 @@ template <class A, int WF, bool NORM, int EPI, int JM, int P>
 am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t tb = A::kDtype == AM_DT_BF16 ? 2 : 4;
-  constexpr bool XL = JM * XS::kDW > 32;
-  int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (XL ? (((g.row_bytes / 16) * 4 + 15) / 16) * 16 : 0);
+  int64_t lds = ((g.k * XS::kBytes + 15) / 16) * 16 + (XS::kOff != 0.0f ? (((g.row_bytes / 16) * 4 + 15) / 16) * 16 : 0);
   if (EPI == kEpiResidual) lds += ((g.n * tb + 15) / 16) * 16;
   if (EPI == kEpiQkv) lds += g.d * 4;
   if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
