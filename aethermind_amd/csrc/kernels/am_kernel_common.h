@@ -68,6 +68,20 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Sum over a 256-thread block; every thread gets the result.  `red` holds >= 4 floats.
+// Sum over a block of NW waves (every thread receives it); red holds NW floats.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += red[w];
+  return t;
+}
+
 __device__ __forceinline__ float block_sum_256(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

@@ -20,6 +20,7 @@
 //   * Row sums are reduced with DPP row rotations plus four readlanes; the epilogue
 //     applies the reference op-boundary roundings of the nodes that were fused.
 
+#include <algorithm>
 #include <cmath>
 
 #include "am_kernel_common.h"
@@ -313,8 +314,9 @@ __device__ __forceinline__ float piece_elem(const uint4& v, int e) {
     return __uint_as_float(w[e]);
 }
 
-template <class A, int WF, bool NORM, int EPI, int JM, int P>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
+template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
+  constexpr int NT = NW * 64;  // threads per block
   using XS = XStore<A, WF>;
   using XL_ = XLds<A, WF>;
   using T = typename A::T;
@@ -324,13 +326,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   // x chunks live in registers when they fit in 32 dwords per lane, else they are
   // read from LDS per chunk-step inside the loop
   constexpr bool XL = JM * XDW > 32;
-  constexpr int JB = XL ? (JM < 4 ? JM : 4) : JM;  // chunk-steps per load block
+  // chunk-steps per load block (x-in-LDS: at most 4, and at most 64 dwords of x per step group)
+  constexpr int JBX = (64 / XDW) < 4 ? (64 / XDW) : 4;
+  constexpr int JB = XL ? (JM < JBX ? JM : JBX) : JM;
   constexpr int NB = JM / JB;                      // load blocks per iteration
   constexpr int EPP = 16 / static_cast<int>(sizeof(T));               // activations per 16-byte piece
-  constexpr int XP = (JM * 64 * kc + 256 * EPP - 1) / (256 * EPP);  // x pieces per thread
-  constexpr int RP = 4;                                               // residual pieces per thread (first pass)
+  constexpr int XP = (JM * 64 * kc + NT * EPP - 1) / (NT * EPP);  // x pieces per thread
+  constexpr int RP = 1024 / NT > 0 ? 1024 / NT : 1;                // residual pieces per thread (first pass)
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float red[4];
+  __shared__ float red[NW];
   const int tid = threadIdx.x;
   const int64_t K = p.k;
   const int64_t C = p.row_bytes / 16;  // chunks per row
@@ -345,8 +349,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   float* cs_lds = reinterpret_cast<float*>(smem + off_cs);
   const int lane = tid & 63;
   // wave index made provably wave-uniform, so the loop below runs on scalar branches
-  const int64_t gw = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t TW = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t gw = static_cast<int64_t>(blockIdx.x) * NW + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t TW = static_cast<int64_t>(gridDim.x) * NW;
   const int64_t niter = (p.units + P - 1) / P;
   const int ng = SC ? static_cast<int>(K / p.group) : 1;
   const int chunks_per_group = SC ? p.group / kc : 1;
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     const int64_t xlast = p.vec ? xpieces - 1 : 0;
 #pragma unroll
     for (int v = 0; v < XP; ++v) {
-      int64_t pi = tid + 256 * v;
+      int64_t pi = tid + NT * v;
       if (pi > xlast) pi = xlast;
       xv[v] = xs[pi];
       if constexpr (NORM) nv[v] = ns[pi];
@@ -381,7 +385,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       const int64_t rlast = p.vec ? rpieces - 1 : 0;
 #pragma unroll
       for (int v = 0; v < RP; ++v) {
-        int64_t pi = tid + 256 * v;
+        int64_t pi = tid + NT * v;
         if (pi > rlast) pi = rlast;
         rv[v] = rs[pi];
       }
@@ -460,20 +464,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       float ss = 0.0f;
 #pragma unroll
       for (int v = 0; v < XP; ++v) {
-        const bool ok = vec && tid + 256 * v < xpieces;
+        const bool ok = vec && tid + NT * v < xpieces;
 #pragma unroll
         for (int e = 0; e < EPP; ++e) {
           const float x = ok ? piece_elem<A>(xv[v], e) : 0.0f;
           ss = fmaf(x, x, ss);
         }
       }
-      ss = block_sum_256(ss, red);
+      ss = block_sum<NW>(ss, red);
       inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
     }
     const int64_t xlast = vec ? xpieces - 1 : 0;
 #pragma unroll
     for (int v = 0; v < XP; ++v) {
-      const int64_t pi0 = tid + 256 * v;
+      const int64_t pi0 = tid + NT * v;
       const bool ok = vec && pi0 < xpieces;
       const int64_t pi = pi0 > xlast ? xlast : pi0;
       float xs[EPP];  // staged values (bf16-exact when LDS holds bf16)
@@ -524,13 +528,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       const int64_t rlast = vec ? rpieces - 1 : 0;
 #pragma unroll
       for (int v = 0; v < RP; ++v) {
-        int64_t pi = tid + 256 * v;
+        int64_t pi = tid + NT * v;
         if (pi > rlast) pi = rlast;
         reinterpret_cast<uint4*>(res_lds)[pi] = rv[v];
       }
       if (vec) {
         const uint4* res = static_cast<const uint4*>(p.residual);
-        for (int64_t pi = tid + 256 * RP; pi < rpieces; pi += 256) reinterpret_cast<uint4*>(res_lds)[pi] = res[pi];
+        for (int64_t pi = tid + NT * RP; pi < rpieces; pi += NT) reinterpret_cast<uint4*>(res_lds)[pi] = res[pi];
       }
     }
   }
@@ -540,25 +544,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     float inv = 1.0f;
     if constexpr (NORM) {
       float ss = 0.0f;
-      for (int64_t j = tid; j < K; j += 256) {
+      for (int64_t j = tid; j < K; j += NT) {
         const float v = A::load(xin, j);
         ss = fmaf(v, v, ss);
       }
-      ss = block_sum_256(ss, red);
+      ss = block_sum<NW>(ss, red);
       inv = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
     }
-    for (int64_t j = tid; j < K; j += 256) {
+    for (int64_t j = tid; j < K; j += NT) {
       float v = A::load(xin, j);
       if constexpr (NORM) v = A::round((v * inv) * A::load(nw, j));
       XL_::store(xl, j, v);
     }
     if constexpr (EPI == kEpiResidual) {
       const T* res = static_cast<const T*>(p.residual);
-      for (int64_t r = tid; r < p.n; r += 256) res_lds[r] = res[r];
+      for (int64_t r = tid; r < p.n; r += NT) res_lds[r] = res[r];
     }
     if constexpr (XS::kOff != 0.0f) {
       __syncthreads();
-      for (int64_t c = tid; c < C; c += 256) {
+      for (int64_t c = tid; c < C; c += NT) {
         uint32_t xd[XDW];
         XL_::load_chunk(xl, c, xd);
         corr_lds[c] = XS::kOff * XL_::chunk_sum(xd);
@@ -740,8 +744,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
   if constexpr (EPI == kEpiLmHead) {
     // block best -> partials; the last block (atomic ticket) reduces them, publishes
     // the token / advances the decode state, and resets the ticket for the next call.
-    __shared__ float bv_s[4];
-    __shared__ int64_t bi_s[4];
+    __shared__ float bv_s[NW];
+    __shared__ int64_t bi_s[NW];
     __shared__ bool last;
     const int wave = threadIdx.x >> 6;
     // each pair lane holds the best of its rows: reduce over the wave first
@@ -759,7 +763,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
     if (threadIdx.x == 0) {
       float bv = 0.0f;
       int64_t bi = -1;
-      for (int w = 0; w < 4; ++w)
+      for (int w = 0; w < NW; ++w)
         if (bi_s[w] >= 0 && argmax_better(bv_s[w], bi_s[w], bv, bi)) { bv = bv_s[w]; bi = bi_s[w]; }
       p.pv[blockIdx.x] = bv;
       p.pi[blockIdx.x] = bi;
@@ -772,7 +776,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       __threadfence();
       float bv = 0.0f;
       int64_t bi = -1;
-      for (int64_t b = threadIdx.x; b < gridDim.x; b += 256) {
+      for (int64_t b = threadIdx.x; b < gridDim.x; b += NT) {
         const float v = __hip_atomic_load(&p.pv[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int64_t i = __hip_atomic_load(&p.pi[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (i >= 0 && argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
@@ -791,7 +795,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs p) {
       if (threadIdx.x == 0) {
         float fv = 0.0f;
         int64_t fi = -1;
-        for (int w = 0; w < 4; ++w)
+        for (int w = 0; w < NW; ++w)
           if (bi_s[w] >= 0 && argmax_better(bv_s[w], bi_s[w], fv, fi)) { fv = bv_s[w]; fi = bi_s[w]; }
         const int64_t tok = fi < 0 ? 0 : fi;
         p.token_out[0] = tok;
@@ -831,6 +835,29 @@ am_status_code ValidateWeight(const am_gfx950_weight& w) {
   return AM_STATUS_OK;
 }
 
+template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW>
+am_status_code LaunchNW(const GemvArgs& g, int64_t lds, hipStream_t s) {
+  // Persistent grid: at most the resident blocks per CU (one, for the large blocks),
+  // iterations strided over the waves.
+  static thread_local int64_t cached_lds = -1;
+  static thread_local int cached_blocks = 1;
+  if (cached_lds != lds) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<A, WF, NORM, EPI, JM, P, NW>, NW * 64,
+                                                     static_cast<size_t>(lds)) != hipSuccess || nb < 1)
+      nb = 1;
+    cached_blocks = nb;
+    cached_lds = lds;
+  }
+  const int64_t niter = CeilDiv(g.units, P);
+  int64_t blocks = std::min<int64_t>(static_cast<int64_t>(DeviceCUs()) * cached_blocks, CeilDiv(niter, NW));
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64),
+                     static_cast<size_t>(lds), s, g);
+  AM_RETURN_IF_LAUNCH_FAILED("gemv");
+  return AM_STATUS_OK;
+}
+
 template <class A, int WF, bool NORM, int EPI, int JM, int P>
 am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
@@ -839,33 +866,18 @@ am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   if (EPI == kEpiResidual) lds += ((g.n * tb + 15) / 16) * 16;
   if (EPI == kEpiQkv) lds += g.d * 4;
   if (lds > 150 * 1024) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemv: in_features too large for LDS staging");
-  // Balanced grid of persistent waves: as many resident waves as the kernel's register
-  // and LDS footprint allows (HBM latency is hidden by waves in flight), iterations
-  // spread evenly over them.
-  static thread_local int64_t cached_lds = -1;
-  static thread_local int cached_blocks = 2;
-  if (cached_lds != lds) {
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, gemv_kernel<A, WF, NORM, EPI, JM, P>, 256,
-                                                     static_cast<size_t>(lds)) != hipSuccess || nb < 1)
-      nb = 2;
-    cached_blocks = nb;
-    cached_lds = lds;
-  }
-  const int64_t niter = CeilDiv(g.units, P);
-  const int64_t max_waves = static_cast<int64_t>(DeviceCUs()) * cached_blocks * 4;
-  const int64_t ipw = CeilDiv(niter, max_waves);
-  const int64_t waves = CeilDiv(niter, ipw);
-  int64_t blocks = CeilDiv(waves, 4);
-  if (blocks > 65536) blocks = 65536;
   GemvArgs ga = g;
   auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
   ga.vec = al16(g.x) && (g.k * tb) % 16 == 0 && (!NORM || al16(g.norm_w)) &&
            (EPI != kEpiResidual || (al16(g.residual) && (g.n * tb) % 16 == 0));
-  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                     static_cast<size_t>(lds), s, ga);
-  AM_RETURN_IF_LAUNCH_FAILED("gemv");
-  return AM_STATUS_OK;
+  // Large problems: one block per CU of as many waves as fit (3 per SIMD for INT4
+  // with x in registers, else 2), so x is staged once per CU.  Small ones: 4-wave
+  // blocks spread over every CU.
+  constexpr bool XL = JM * XS::kDW > 32;
+  constexpr int NWB = (!XL && WF == AM_WF_INT4) ? 12 : 8;
+  if (CeilDiv(g.units, P) >= static_cast<int64_t>(DeviceCUs()) * NWB)
+    return LaunchNW<A, WF, NORM, EPI, JM, P, NWB>(ga, lds, s);
+  return LaunchNW<A, WF, NORM, EPI, JM, P, 4>(ga, lds, s);
 }
 
 // Chunk-steps per row (J) pick the instantiation: JM >= J chunk-steps per lane,
