@@ -29,6 +29,7 @@
 #include "am_core.h"
 #include "am_runtime.h"
 #include "gfx950_backend.h"
+#include "am_launch_timing.h"
 
 namespace am {
 am_status_code SetLastError(am_status_code code, const char* msg);
@@ -661,24 +662,47 @@ class LlamaSession {
     return Status::Ok();
   }
 
+  // Per-step device time of the decode plan, eager replay of the same steps on the
+  // session stream.  Weight-GEMV steps are timed with events bound to their single
+  // dispatch (hipExtLaunchKernelGGL start/stop), other steps with events around the step.
   Status Profile(int64_t n, double* ms_by_op, int64_t* count_by_op) {
     if (host_step == 0) return Status::FailedPrecondition("decode requires a prefilled session");
     if (host_pos + n > m->cfg.max_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
     const auto& steps = decode_plan->steps();
-    std::vector<hipEvent_t> ev(steps.size() + 1);
-    for (auto& e : ev) AM_HIP_OK(hipEventCreate(&e));
+    std::vector<hipEvent_t> e0(steps.size(), nullptr), e1(steps.size(), nullptr);
     Status st;
+    for (size_t i = 0; i < steps.size() && st.ok(); ++i)
+      if (hipEventCreate(&e0[i]) != hipSuccess || hipEventCreate(&e1[i]) != hipSuccess)
+        st = Status::Internal("profile: event creation failed");
+    am::LaunchTiming& lt = am::ThreadLaunchTiming();
     for (int64_t it = 0; it < n && st.ok(); ++it) {
-      AM_HIP_OK(hipEventRecord(ev[0], stream));
       for (size_t i = 0; i < steps.size() && st.ok(); ++i) {
-        st = LayerRunner::RunStep(i, steps[i], decode_bind);
-        (void)hipEventRecord(ev[i + 1], stream);
+        const OpType t = steps[i].op->Type();
+        const bool gemv = t == OpType::kFusedRmsNormQkvRoPEKVUpdate || t == OpType::kFusedLinearAdd ||
+                          t == OpType::kFusedRmsNormGateUpSiluMul || t == OpType::kFusedRmsNormLmHeadArgmax;
+        if (gemv) {
+          lt = {e0[i], e1[i], false};
+          st = LayerRunner::RunStep(i, steps[i], decode_bind);
+          const bool used = lt.used;
+          lt = {};
+          if (st.ok() && !used) st = Status::Internal("profile: GEMV step did not take the timed launch");
+        } else {
+          (void)hipEventRecord(e0[i], stream);
+          st = LayerRunner::RunStep(i, steps[i], decode_bind);
+          (void)hipEventRecord(e1[i], stream);
+        }
       }
       if (!st.ok()) break;
-      AM_HIP_OK(hipEventSynchronize(ev[steps.size()]));
+      if (hipStreamSynchronize(stream) != hipSuccess) {
+        st = Status::Internal("profile: stream synchronize failed");
+        break;
+      }
       for (size_t i = 0; i < steps.size(); ++i) {
         float ms = 0.f;
-        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+        if (hipEventElapsedTime(&ms, e0[i], e1[i]) != hipSuccess) {
+          st = Status::Internal("profile: event timing failed");
+          break;
+        }
         const int op = static_cast<int>(steps[i].op->Type());
         if (op < 64) {
           ms_by_op[op] += ms;
@@ -686,7 +710,11 @@ class LlamaSession {
         }
       }
     }
-    for (auto& e : ev) (void)hipEventDestroy(e);
+    lt = {};
+    for (size_t i = 0; i < steps.size(); ++i) {
+      if (e0[i]) (void)hipEventDestroy(e0[i]);
+      if (e1[i]) (void)hipEventDestroy(e1[i]);
+    }
     if (st.ok()) {
       host_pos += n;
       host_step += n;

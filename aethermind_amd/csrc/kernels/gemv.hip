@@ -24,6 +24,8 @@
 #include <cmath>
 
 #include "am_kernel_common.h"
+#include "am_launch_timing.h"
+#include <hip/hip_ext.h>
 
 namespace am {
 namespace {
@@ -852,8 +854,15 @@ am_status_code LaunchNW(const GemvArgs& g, int64_t lds, hipStream_t s) {
   const int64_t niter = CeilDiv(g.units, P);
   int64_t blocks = std::min<int64_t>(static_cast<int64_t>(DeviceCUs()) * cached_blocks, CeilDiv(niter, NW));
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64),
-                     static_cast<size_t>(lds), s, g);
+  LaunchTiming& lt = ThreadLaunchTiming();
+  if (lt.start != nullptr) {
+    hipExtLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)),
+                          dim3(NW * 64), static_cast<size_t>(lds), s, lt.start, lt.stop, 0, g);
+    lt.used = true;
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64),
+                       static_cast<size_t>(lds), s, g);
+  }
   AM_RETURN_IF_LAUNCH_FAILED("gemv");
   return AM_STATUS_OK;
 }
@@ -932,6 +941,11 @@ GemvArgs BaseArgs(const am_gfx950_weight& w) {
 }
 
 }  // namespace
+
+LaunchTiming& ThreadLaunchTiming() noexcept {
+  static thread_local LaunchTiming t;
+  return t;
+}
 
 // Linear rows for am_gfx950_linear (decode GEMV; also the row loop of small m).
 am_status_code GemvLinearRow(const void* x, int32_t act, const am_gfx950_weight& w, void* out, int32_t out_dtype,

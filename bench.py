@@ -98,6 +98,37 @@ def cpu_baseline(weight_format: int, seconds_budget: float = 20.0):
     }
 
 
+def calibrate_copy(mib: int) -> None:
+    """Device-to-device copy of a known size (the HIP runtime's copy kernel), three
+    times: the reference dispatch for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipFree.argtypes = [C.c_void_p]
+    n = mib << 20
+    a, b = C.c_void_p(), C.c_void_p()
+    if hip.hipMalloc(C.byref(a), n) != 0 or hip.hipMalloc(C.byref(b), n) != 0:
+        raise SystemExit("hipMalloc failed")
+    for _ in range(3):
+        if hip.hipMemcpy(b, a, n, 3) != 0:  # hipMemcpyDeviceToDevice
+            raise SystemExit("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"calibrate_copy_bytes": n}), flush=True)
+
+
+def measured_traffic(config: str):
+    """HBM bytes per decode token of the GEMV launches, from the committed rocprofv3 PMC
+    summary of this workload (None when there is none)."""
+    path = os.path.join(ROOT, "profiles", f"gemv_{config}_decode_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_token")
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,7 +138,12 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (PMC counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the decode path on one GPU only; --gpus must be 1 "
@@ -167,8 +203,9 @@ def main():
     log(f"decode: {steps} tokens in {dt*1e3:.1f} ms -> {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/token), "
         f"{L.am_session_decode_plan_size(s)} kernels/token")
 
-    # Per-kernel durations: HIP events around every step of the same decode plan on the
-    # session stream (eager replay of the plan, adjacent to the timed region).
+    # Per-kernel durations of the same decode plan right after the timed region: each
+    # weight GEMV launch carries start/stop HIP events bound to its dispatch on the
+    # session stream (hipExtLaunchKernelGGL); other steps are bracketed by events.
     ms_by_op = (C.c_double * 64)()
     cnt_by_op = (C.c_int64 * 64)()
     L.call("am_session_profile_decode", s, args.profile_steps, ms_by_op, cnt_by_op)
@@ -178,6 +215,8 @@ def main():
     gemv_ms = sum(ms_by_op[i] for i in GEMV_OPS) / args.profile_steps
     gemv_launches = sum(cnt_by_op[i] for i in GEMV_OPS) // args.profile_steps
     weight_bytes = L.am_model_weight_bytes_total(m)
+    if gemv_ms <= 0.0:
+        raise SystemExit("profile pass returned no GEMV time")
     achieved = weight_bytes / (gemv_ms * 1e-3) / 1e9
     log(f"weight GEMVs: {gemv_ms:.3f} ms/token over {gemv_launches} launches -> {achieved:.0f} GB/s "
         f"({achieved / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f})")
@@ -216,7 +255,8 @@ def main():
                    "model": cfgd["name"], "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
                    "prefill_ms": round(prefill_s * 1e3, 2), "kernels_per_token": plan_size},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
+                     "traffic_unit": "HBM bytes per token over the GEMV launches (rocprofv3 PMC, copy-scaled)",
                      "kernel": "gemv_kernel (weight-only INT4 dequant GEMV, all 4 fused epilogues)",
                      "bytes_per_token": weight_bytes, "gemv_ms_per_token": round(gemv_ms, 4),
                      "launches_per_token": gemv_launches},
