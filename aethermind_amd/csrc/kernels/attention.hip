@@ -1,20 +1,29 @@
 // GQA causal attention over the static KV cache (gfx950), split-K over positions.
 //
-// grid = (splits, kv_heads, batch*seq).  One 256-thread block owns one query row,
-// one kv head (so all hq/hkv query heads of the group share every K/V load) and one
-// contiguous slice of positions.  Inside the block:
+// grid = (splits, kv_heads, batch*seq).  One 512-thread block (8 waves) owns one
+// query row, one kv head (so all hq/hkv query heads of the group share every K/V
+// load) and one contiguous slice of positions.  Inside the block:
 //   * D/8 lanes cover one cache row (8 elements = 16 bytes of bf16 each), so a wave
 //     reads 64/(D/8) consecutive rows per load instruction: for D = 128 that is four
-//     256-byte rows = 1 KiB contiguous per instruction.  Each lane group loads U rows
-//     before using any of them, so U KiB per wave are in flight at once.
+//     256-byte rows = 1 KiB contiguous per instruction.
+//   * Positions go in batches of 8 waves x 64/(D/8) rows x U rows per lane group
+//     (U shrinks as the query group grows, so two batches fit in registers).
+//     q is loaded first, then two batches of K/V; the batch after next is issued as
+//     soon as a buffer has been consumed, so the cache streams while the current
+//     batch is reduced.  The loop exits sit before the issues, so the pending loads
+//     always retire in order.
 //   * Each lane group keeps an fp32 online softmax (running max, sum, output slice)
 //     in base 2: q is pre-scaled by log2(e)/sqrt(d), so every exponential is one
-//     v_exp_f32.  Row dot products are summed over the lane group with DPP.
-//     Groups are merged with xor shuffles, waves through LDS.
+//     v_exp_f32; a batch updates the running state once per head.  Row dot products
+//     are summed over the lane group with DPP; lane groups are merged with permlane
+//     swaps / DPP; the 8 waves through LDS, one (head, dim) per thread.
 //   * The split count follows the live context (at least kMinPerSplit positions per
-//     split); with one split the block writes the output, otherwise it writes a
-//     partial record (m, l, o) and attention_combine_kernel, launched right after on
-//     the same stream, merges the records.  No atomics, fences or zeroed scratch.
+//     split); with one split the block writes the output.  Otherwise every block
+//     writes a partial record (m, l, o) with device-scope stores, waits for them to
+//     complete and takes a ticket; the last block of the (row, kv head) reads the
+//     records back with device-scope loads, merges them and resets the ticket.  Only
+//     the records and the ticket are device-coherent accesses: no cache-wide
+//     writeback or invalidate, and no second launch.
 
 #include <cmath>
 
@@ -34,10 +43,16 @@ struct AttnArgs {
   int32_t splits;
   float scale;  // log2(e) / sqrt(d)
   float* part;
+  unsigned* tickets;  // [rows][hkv], zero between calls
 };
 
-// Fewest cache positions one split block handles (short contexts use fewer splits).
-constexpr int64_t kMinPerSplit = 64;
+constexpr int kWaves = 8;
+// Fewest cache positions one split block handles (contexts up to this length use a
+// single block per (row, kv head) and need no cross-block merge), and the most
+// splits: measured on MI355X, 128 positions per block and at most 16 blocks per
+// (row, kv head) minimise decode time from 128 to 4096 positions.
+constexpr int64_t kMinPerSplit = 128;
+constexpr int kMaxSplits = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <class A>
@@ -58,10 +73,11 @@ __device__ __forceinline__ void load8(const typename A::T* p, float* out) {
   }
 }
 
-// Raw 16 bytes of one lane's slice of a cache row (bf16: 8 values; f32: 4 + 4).
+// Raw bytes of one lane's 8-element slice of a cache row (bf16: 16 B; f32: 32 B).
 template <class A>
 struct RowSlice {
-  uint4 a, b;
+  uint4 a;
+  uint4 b;  // f32 only
 };
 template <class A>
 __device__ __forceinline__ RowSlice<A> load_slice(const typename A::T* p) {
@@ -103,6 +119,20 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Value held by lane (lane ^ OFF), OFF in {8, 16, 32}.
+template <int OFF>
+__device__ __forceinline__ float xor_partner(float v, int lane) {
+  if constexpr (OFF == 8) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(((lane >> 4) & 1) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(lane < 32 ? r[1] : r[0]);
+  }
+}
+
 // merge (m2, l2, o2) into (m, l, o); base-2 exponentials
 __device__ __forceinline__ void merge_state(float& m, float& l, float* o, float m2, float l2, const float* o2) {
   const float mn = fmaxf(m, m2);
@@ -114,7 +144,7 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* o, float 
   m = mn;
 }
 
-// live split count of a (row, kv head): every block and the combine agree on it
+// live split count of a (row, kv head): every block agrees on it
 __device__ __forceinline__ int64_t live_splits(int64_t n_keys, int32_t splits) {
   int64_t ns = (n_keys + kMinPerSplit - 1) / kMinPerSplit;
   if (ns > splits) ns = splits;
@@ -128,16 +158,22 @@ __device__ __forceinline__ int64_t row_keys(const AttnArgs& p, int64_t b, int64_
 }
 
 template <class A, int D, int G>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
-  constexpr int LP = D / 8;      // lanes per cache row
-  constexpr int PPW = 64 / LP;   // rows per wave step
-  constexpr int U = 4;           // rows per lane group loaded before use
-  constexpr int STEP = 4 * PPW;  // rows per block step
+__global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
+  constexpr int NT = kWaves * 64;
+  constexpr int LP = D / 8;                                 // lanes per cache row
+  constexpr int PPW = 64 / LP;                              // rows per wave step
+  // rows per lane group per batch: two batches of raw K/V rows stay in registers
+  constexpr int UB = A::kDtype == AM_DT_BF16 ? 8 : 4;
+  constexpr int U = G <= 2 ? UB : (G == 4 ? UB / 2 : UB / 4);
+  constexpr int STEP = kWaves * PPW;                        // rows per block step
+  constexpr int64_t BATCH = static_cast<int64_t>(STEP) * U;  // rows per batch
   using T = typename A::T;
-  __shared__ float sm_m[4][G], sm_l[4][G];
-  __shared__ float sm_o[4][G][D];
+  __shared__ float sm_m[kWaves][G], sm_l[kWaves][G];
+  __shared__ float sm_o[kWaves][G][D];
+  __shared__ bool last;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane % LP, ps = lane / LP;
   const int64_t qr = blockIdx.z;
   const int64_t b = qr / p.seq, s = qr % p.seq;
@@ -149,18 +185,40 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   const int64_t per = (n_keys + nsplit - 1) / nsplit;
   const int64_t lo = split * per;
   const int64_t hi = lo + per < n_keys ? lo + per : n_keys;
+  const int64_t nb = (hi - lo + BATCH - 1) / BATCH;  // batches (>= 1)
 
+  // q first: the memory counter retires in order, so the K/V batches behind it do not
+  // delay the first use of q.
   const T* qp = static_cast<const T*>(p.q) + (qr * p.hq + g * G) * D + sub * 8;
+  RowSlice<A> qraw[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) qraw[hh] = load_slice<A>(qp + hh * D);
+
+  const T* kbase = static_cast<const T*>(p.kc) + b * p.cbs + g * p.cap * D + sub * 8;
+  const T* vbase = static_cast<const T*>(p.vc) + b * p.cbs + g * p.cap * D + sub * 8;
+  const int64_t row0 = wave * PPW + ps;  // this lane group's first row in a block step
+  // Loads batch bi (clamped to the last batch; out-of-range rows read row lo).
+  auto issue = [&](RowSlice<A> (&kr)[U], RowSlice<A> (&vr)[U], int64_t bi) {
+    if (bi >= nb) bi = nb - 1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int64_t pos = lo + bi * BATCH + row0 + u * STEP;
+      if (pos >= hi) pos = lo;
+      kr[u] = load_slice<A>(kbase + pos * D);
+      vr[u] = load_slice<A>(vbase + pos * D);
+    }
+  };
+  RowSlice<A> ka[U], va[U], kb[U], vb[U];
+  issue(ka, va, 0);
+  issue(kb, vb, 1);
+
   float qv[G][8];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    load8<A>(qp + hh * D, qv[hh]);
+    unpack_slice<A>(qraw[hh], qv[hh]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) qv[hh][i] *= p.scale;
   }
-  const T* kbase = static_cast<const T*>(p.kc) + b * p.cbs + g * p.cap * D + sub * 8;
-  const T* vbase = static_cast<const T*>(p.vc) + b * p.cbs + g * p.cap * D + sub * 8;
-
   float m[G], l[G], o[G][8];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
@@ -170,49 +228,89 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     for (int i = 0; i < 8; ++i) o[hh][i] = 0.0f;
   }
 
-  for (int64_t base = lo + wave * PPW + ps; base < hi; base += U * STEP) {
-    RowSlice<A> kr[U], vr[U];
-    bool ok[U];
+  // One batch: all U dots per head first, then one running-state update per head.
+  auto process = [&](const RowSlice<A> (&kr)[U], const RowSlice<A> (&vr)[U], int64_t bi) {
+    float e[G][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      int64_t pos = base + u * STEP;
-      ok[u] = pos < hi;
-      if (!ok[u]) pos = lo;  // in-bounds address, result discarded
-      kr[u] = load_slice<A>(kbase + pos * D);
-      vr[u] = load_slice<A>(vbase + pos * D);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kv[8], vv[8];
+      float kv[8];
       unpack_slice<A>(kr[u], kv);
-      unpack_slice<A>(vr[u], vv);
+      const bool ok = lo + bi * BATCH + row0 + u * STEP < hi;
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) {
         float d = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) d = fmaf(qv[hh][i], kv[i], d);
         d = group_sum<LP>(d);
-        if (!ok[u]) d = -INFINITY;
-        const float mn = fmaxf(m[hh], d);
-        const float c = mn == -INFINITY ? 1.0f : exp2f(m[hh] - mn);
-        const float e = ok[u] ? exp2f(d - mn) : 0.0f;
-        l[hh] = fmaf(l[hh], c, e);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[hh][i] = fmaf(o[hh][i], c, e * vv[i]);
-        m[hh] = mn;
+        e[hh][u] = ok ? d : -INFINITY;
       }
     }
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      float mn = m[hh];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mn = fmaxf(mn, e[hh][u]);
+      const float c = mn == -INFINITY ? 1.0f : exp2f(m[hh] - mn);
+      float sum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        e[hh][u] = e[hh][u] == -INFINITY ? 0.0f : exp2f(e[hh][u] - mn);
+        sum += e[hh][u];
+      }
+      l[hh] = fmaf(l[hh], c, sum);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[hh][i] *= c;
+      m[hh] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vv[8];
+      unpack_slice<A>(vr[u], vv);
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[hh][i] = fmaf(e[hh][u], vv[i], o[hh][i]);
+    }
+  };
+
+  for (int64_t bi = 0;;) {
+    process(ka, va, bi);
+    if (bi + 2 >= nb) {
+      if (bi + 1 < nb) process(kb, vb, bi + 1);
+      break;
+    }
+    issue(ka, va, bi + 2);
+    process(kb, vb, bi + 1);
+    if (bi + 3 >= nb) {
+      process(ka, va, bi + 2);
+      break;
+    }
+    issue(kb, vb, bi + 3);
+    bi += 2;
   }
-  // merge the PPW row streams of the wave (lanes sub, sub+LP, ...)
+
+  // merge the PPW row streams of the wave (lane groups sub, sub+LP, ...)
 #pragma unroll
   for (int off = LP; off < 64; off <<= 1) {
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
-      const float m2 = __shfl_xor(m[hh], off, 64);
-      const float l2 = __shfl_xor(l[hh], off, 64);
-      float o2[8];
+      float m2, l2, o2[8];
+      if (off == 8) {
+        m2 = xor_partner<8>(m[hh], lane);
+        l2 = xor_partner<8>(l[hh], lane);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o2[i] = __shfl_xor(o[hh][i], off, 64);
+        for (int i = 0; i < 8; ++i) o2[i] = xor_partner<8>(o[hh][i], lane);
+      } else if (off == 16) {
+        m2 = xor_partner<16>(m[hh], lane);
+        l2 = xor_partner<16>(l[hh], lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o2[i] = xor_partner<16>(o[hh][i], lane);
+      } else {
+        m2 = xor_partner<32>(m[hh], lane);
+        l2 = xor_partner<32>(l[hh], lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o2[i] = xor_partner<32>(o[hh][i], lane);
+      }
       merge_state(m[hh], l[hh], o[hh], m2, l2, o2);
     }
   }
@@ -228,64 +326,69 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     }
   }
   __syncthreads();
-  if (wave == 0 && ps == 0) {
-#pragma unroll
-    for (int w = 1; w < 4; ++w)
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) merge_state(m[hh], l[hh], o[hh], sm_m[w][hh], sm_l[w][hh], &sm_o[w][hh][sub * 8]);
-    if (nsplit == 1) {
-      T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G) * D + sub * 8;
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) A::store(out + hh * D, i, o[hh][i] * inv);
-      }
-    } else {
-      // partial record per head: [m, l, o[D]]
-      float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * (D + 2);
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        if (sub == 0) {
-          rec[hh * (D + 2)] = m[hh];
-          rec[hh * (D + 2) + 1] = l[hh];
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) rec[hh * (D + 2) + 2 + sub * 8 + i] = o[hh][i];
-      }
-    }
-  }
-}
 
-// Merges the split records of one (query row, q head): grid = (hq, batch*seq), D
-// threads, one output dimension each.  Rows that used a single split were written by
-// attention_kernel and are left alone.
-template <class A, int D>
-__global__ __launch_bounds__(D) void attention_combine_kernel(AttnArgs p) {
-  using T = typename A::T;
-  const int64_t h = blockIdx.x, qr = blockIdx.y;
-  const int64_t b = qr / p.seq, s = qr % p.seq;
-  const int64_t n_keys = row_keys(p, b, s);
-  const int64_t nsplit = live_splits(n_keys, p.splits);
-  if (nsplit == 1) return;
-  const int64_t G = p.hq / p.hkv;
-  const int64_t g = h / G, hh = h % G;
-  const float* base = p.part + ((qr * p.hkv + g) * p.splits * G + hh) * (D + 2);
-  const int64_t rs = G * (D + 2);  // record stride between splits
-  float mx = -INFINITY;
-  for (int64_t sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, base[sp * rs]);
-  float den = 0.0f, acc = 0.0f;
-  if (mx != -INFINITY) {
-    for (int64_t sp = 0; sp < nsplit; ++sp) {
-      const float* rec = base + sp * rs;
-      const float c = exp2f(rec[0] - mx);
-      den = fmaf(rec[1], c, den);
-      acc = fmaf(rec[2 + threadIdx.x], c, acc);
+  // Merge the waves: thread t owns (head, dim) pairs t, t + NT, ...; with one split it
+  // writes the output, otherwise the block's partial record (device-scope stores).
+  float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * (D + 2);
+  for (int t = threadIdx.x; t < G * D; t += NT) {
+    const int hh = t / D, dd = t % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w][hh]);
+    float den = 0.0f, acc = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float c = exp2f(sm_m[w][hh] - mx);
+        den = fmaf(sm_l[w][hh], c, den);
+        acc = fmaf(sm_o[w][hh][dd], c, acc);
+      }
+    }
+    if (nsplit == 1) {
+      T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
+      A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
+    } else {
+      if (dd == 0) {
+        __hip_atomic_store(&rec[hh * (D + 2)], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&rec[hh * (D + 2) + 1], den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(&rec[hh * (D + 2) + 2 + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  T* out = static_cast<T*>(p.out) + (qr * p.hq + h) * D;
-  A::store(out, threadIdx.x, acc * inv);
+  if (nsplit == 1) return;
+  // every thread's record stores have completed before the block takes its ticket
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(&p.tickets[qr * p.hkv + g], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    last = t == static_cast<unsigned>(nsplit - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Merge the splits: thread t owns (head, dim) pairs t, t + NT, ...; the records are
+  // read with device-scope loads.
+  const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
+  const int64_t rs = G * (D + 2);  // record stride between splits
+  for (int t = threadIdx.x; t < G * D; t += NT) {
+    const int hh = t / D, dd = t % D;
+    const float* base = base0 + hh * (D + 2);
+    float mx = -INFINITY;
+    for (int64_t sp = 0; sp < nsplit; ++sp)
+      mx = fmaxf(mx, __hip_atomic_load(&base[sp * rs], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float den = 0.0f, acc = 0.0f;
+    if (mx != -INFINITY) {
+      for (int64_t sp = 0; sp < nsplit; ++sp) {
+        const float* r = base + sp * rs;
+        const float c = exp2f(__hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
+        den = fmaf(__hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, den);
+        acc = fmaf(__hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, acc);
+      }
+    }
+    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
+    A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&p.tickets[qr * p.hkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
@@ -293,24 +396,20 @@ int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
   if (seq > 1) return 1;
   int64_t s = cap / kMinPerSplit;
   if (s < 1) s = 1;
-  if (s > 64) s = 64;
+  if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s);
 }
 
 template <class A, int D>
 am_status_code LaunchD(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
   switch (G) {
-    case 1: hipLaunchKernelGGL((attention_kernel<A, D, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attention_kernel<A, D, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attention_kernel<A, D, 4>), grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((attention_kernel<A, D, 8>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attention_kernel<A, D, 1>), grid, dim3(kWaves * 64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attention_kernel<A, D, 2>), grid, dim3(kWaves * 64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attention_kernel<A, D, 4>), grid, dim3(kWaves * 64), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attention_kernel<A, D, 8>), grid, dim3(kWaves * 64), 0, s, a); break;
     default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
   }
   AM_RETURN_IF_LAUNCH_FAILED("attention");
-  if (a.splits > 1) {
-    hipLaunchKernelGGL((attention_combine_kernel<A, D>), dim3(static_cast<unsigned>(a.hq), grid.z), dim3(D), 0, s, a);
-    AM_RETURN_IF_LAUNCH_FAILED("attention combine");
-  }
   return AM_STATUS_OK;
 }
 
@@ -321,10 +420,10 @@ using namespace am;
 
 extern "C" int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
                                                        int64_t head_dim, int64_t capacity, int32_t num_splits) {
-  (void)hkv;
   const int splits = ChooseSplits(seq, capacity, num_splits);
   if (splits == 1) return 0;
-  return batch * seq * hq * splits * (head_dim + 2) * 4;
+  const int64_t tickets = 256 * CeilDiv(batch * seq * hkv * 4, 256);
+  return tickets + batch * seq * hq * splits * (head_dim + 2) * 4;
 }
 
 extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a, void* stream) {
@@ -357,7 +456,11 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
   p.cbs = batch > 1 ? a->cache_batch_stride : 0;
   p.splits = splits;
   p.scale = kLog2e / sqrtf(static_cast<float>(a->head_dim));
-  if (splits > 1) p.part = static_cast<float*>(a->workspace);
+  if (splits > 1) {
+    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+    p.tickets = reinterpret_cast<unsigned*>(ws);
+    p.part = reinterpret_cast<float*>(ws + 256 * CeilDiv(batch * a->seq * a->hkv * 4, 256));
+  }
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   const int64_t G = a->hq / a->hkv;
   hipStream_t s = AsStream(stream);

@@ -157,11 +157,11 @@ am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* args, void* h
  * position start+s and attends to cache positions [0, start+s]; q head h reads kv
  * head h/(hq/hkv); scale 1/sqrt(d); fp32 online softmax.  The cache rows for the new
  * positions must already be written (KVCacheUpdate precedes Attention).
- * workspace: device scratch of am_gfx950_attention_workspace_bytes(...) bytes (split
- * partial records; no initialisation needed, 0 bytes when no split is possible).
- * Decode rows are split over positions when the context is long: the partials are
- * merged by a second kernel launched on the same stream, so the output is complete
- * when the stream reaches the next operation.
+ * workspace: device scratch of am_gfx950_attention_workspace_bytes(...) bytes (0 when
+ * no split is possible), whose first 4*hkv*batch*seq bytes (split tickets) must be
+ * zero before the first call; the kernel leaves them zero.  Decode rows are split
+ * over positions when the context is long; the last block of each (row, kv head)
+ * merges the partial records, so one launch produces the output.
  * batch > 1 stacks independent sequences: q [batch][seq][hq*d], caches
  * [batch] planes of cache_batch_stride elements, start positions start_pos_dev[b]. */
 typedef struct am_gfx950_attention_args {
