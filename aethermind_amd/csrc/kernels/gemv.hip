@@ -879,12 +879,13 @@ am_status_code LaunchJ(const GemvArgs& g, hipStream_t s) {
   auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
   ga.vec = al16(g.x) && (g.k * tb) % 16 == 0 && (!NORM || al16(g.norm_w)) &&
            (EPI != kEpiResidual || (al16(g.residual) && (g.n * tb) % 16 == 0));
-  // Large problems: one block per CU of as many waves as fit (3 per SIMD for INT4
-  // with x in registers, else 2), so x is staged once per CU.  Small ones: 4-wave
-  // blocks spread over every CU.
+  // Large problems: one 8-wave block per CU, so x is staged once per CU (x-in-LDS
+  // kernels as soon as every wave has an iteration, register-x kernels from two
+  // iterations per wave).  Small ones: 4-wave blocks spread over every CU.  (Block
+  // sizes and pairs per iteration were chosen by measurement on MI355X.)
   constexpr bool XL = JM * XS::kDW > 32;
-  constexpr int NWB = (!XL && WF == AM_WF_INT4) ? 12 : 8;
-  if (CeilDiv(g.units, P) >= static_cast<int64_t>(DeviceCUs()) * NWB)
+  constexpr int NWB = (P == 2 && !XL && WF == AM_WF_INT4) ? 12 : 8;
+  if (CeilDiv(g.units, P) >= static_cast<int64_t>(DeviceCUs()) * NWB * (XL ? 1 : 2))
     return LaunchNW<A, WF, NORM, EPI, JM, P, NWB>(ga, lds, s);
   return LaunchNW<A, WF, NORM, EPI, JM, P, 4>(ga, lds, s);
 }
@@ -895,9 +896,12 @@ template <class A, int WF, bool NORM, int EPI>
 am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t J = CeilDiv(g.row_bytes / 16, 64);
-  if (J <= 2) return LaunchJ<A, WF, NORM, EPI, 2, 2>(g, s);
-  // x in registers: two row pairs per iteration; x read from LDS: one
-  if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, (4 * XS::kDW > 32 ? 1 : 2)>(g, s);
+  // One row pair per iteration keeps two weight buffers within ~100 registers, so
+  // four to five waves fit per SIMD; the lm_head (argmax epilogue, 64k pairs) runs two
+  // pairs per iteration.
+  constexpr int PS = EPI == kEpiLmHead ? 2 : 1;
+  if (J <= 2) return LaunchJ<A, WF, NORM, EPI, 2, PS>(g, s);
+  if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, 1>(g, s);
   if constexpr (8 * XS::kDW <= 128) {
     if (J <= 8) return LaunchJ<A, WF, NORM, EPI, 8, 1>(g, s);
   }
