@@ -328,8 +328,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   // x chunks live in registers when they fit in 32 dwords per lane, else they are
   // read from LDS per chunk-step inside the loop
   constexpr bool XL = JM * XDW > 32;
-  // chunk-steps per load block (x-in-LDS: at most 4, and at most 64 dwords of x per step group)
-  constexpr int JBX = (64 / XDW) < 4 ? (64 / XDW) : 4;
+  // chunk-steps per load block with x in LDS: 2 (measured best for the 14336-long rows:
+  // small blocks keep ~85 registers and a finer double-buffered pipeline)
+  constexpr int JBX = 2;
   constexpr int JB = XL ? (JM < JBX ? JM : JBX) : JM;
   constexpr int NB = JM / JB;                      // load blocks per iteration
   constexpr int EPP = 16 / static_cast<int>(sizeof(T));               // activations per 16-byte piece
