@@ -162,19 +162,19 @@ def test_rmsnorm_random(act):
 
 
 # ---------------------------------------------------------------- linear
-def _weights(n, k, fmt, seed):
+def _weights(n, k, fmt, seed, group=128):
     bits = O.synth_bf16(seed, 0x55, n * k).reshape(n, k)
     if fmt == N.AM_WF_F32:
         w = O.synth_f32(seed, 0x55, n * k).reshape(n, k)
         dw, keep = pack_weight(w, fmt)
         return w, dw, keep
     w = O.bf16_to_f32(bits).copy()
-    dw, keep = pack_weight(w, fmt, 128, src_bf16_bits=bits)
+    dw, keep = pack_weight(w, fmt, group, src_bf16_bits=bits)
     if fmt == N.AM_WF_INT8:
         w = O.dequant_int8(*O.quant_int8(w))
     elif fmt == N.AM_WF_INT4:
-        pk, sc = O.quant_int4(w, 128)
-        w = O.dequant_int4(pk, sc, k, 128)
+        pk, sc = O.quant_int4(w, group)
+        w = O.dequant_int4(pk, sc, k, group)
     return w, dw, keep
 
 
@@ -208,6 +208,22 @@ def test_linear_gemm_mfma(fmt, mnk):
     ref = O.linear(x, wref)
     close(got, ref, TOL["bf16"], f"gemm fmt={fmt} {m}x{n}x{k}")
     # per-row check so a transposed/misplaced tile cannot hide behind the global max
+    for r in (0, m // 2, m - 1):
+        close(got[r], ref[r], 3e-2, f"row {r}")
+
+
+@pytest.mark.parametrize("group", [256, 512])
+def test_linear_gemm_int4_multi_step_groups(group):
+    """INT4 groups that span several 128-wide k steps of the MFMA GEMM"""
+    m, n, k = 130, 260, 2048
+    wref, dw, keep = _weights(n, k, N.AM_WF_INT4, seed=9, group=group)
+    x = O.round_bf16(O.synth_f32(8, 3, m * k, std=1.0).reshape(m, k))
+    out = empty((m, n), torch.int16)
+    xd = bf16_dev(O.bf16_bits(x))
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2), stream())
+    got = O.bf16_to_f32(bits_host(out))
+    ref = O.linear(x, wref)
+    close(got, ref, TOL["bf16"], f"gemm int4 g{group} {m}x{n}x{k}")
     for r in (0, m // 2, m - 1):
         close(got[r], ref[r], 3e-2, f"row {r}")
 
