@@ -41,6 +41,7 @@ struct AttnArgs {
   const int64_t* start_dev;
   int64_t cbs;  // cache batch stride (elements)
   int32_t splits;
+  int32_t min_per_split;  // fewest positions one split block handles
   float scale;  // log2(e) / sqrt(d)
   float* part;
   unsigned* tickets;  // [rows][hkv], zero between calls
@@ -145,8 +146,8 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* o, float 
 }
 
 // live split count of a (row, kv head): every block agrees on it
-__device__ __forceinline__ int64_t live_splits(int64_t n_keys, int32_t splits) {
-  int64_t ns = (n_keys + kMinPerSplit - 1) / kMinPerSplit;
+__device__ __forceinline__ int64_t live_splits(int64_t n_keys, int32_t splits, int32_t min_per_split) {
+  int64_t ns = (n_keys + min_per_split - 1) / min_per_split;
   if (ns > splits) ns = splits;
   if (ns < 1) ns = 1;
   return ns;
@@ -156,6 +157,80 @@ __device__ __forceinline__ int64_t row_keys(const AttnArgs& p, int64_t b, int64_
   const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
   return start + s + 1 <= p.cap ? start + s + 1 : p.cap;
 }
+
+// Merge the NW per-wave states (sm_m, sm_l, sm_o) of one block, then write the output
+// (one split) or the block's partial record, and let the last split block of the
+// (row, kv head) merge the records.
+template <class A, int D, int G, int NW>
+__device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_m)[G], const float (*sm_l)[G],
+                                            const float (*sm_o)[G][D], bool& last, int64_t qr, int64_t g, int split,
+                                            int64_t nsplit) {
+  constexpr int NT = NW * 64;
+  using T = typename A::T;
+  // Merge the waves: thread t owns (head, dim) pairs t, t + NT, ...; with one split it
+  // writes the output, otherwise the block's partial record (device-scope stores).
+  float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * (D + 2);
+  for (int t = threadIdx.x; t < G * D; t += NT) {
+    const int hh = t / D, dd = t % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm_m[w][hh]);
+    float den = 0.0f, acc = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float c = exp2f(sm_m[w][hh] - mx);
+        den = fmaf(sm_l[w][hh], c, den);
+        acc = fmaf(sm_o[w][hh][dd], c, acc);
+      }
+    }
+    if (nsplit == 1) {
+      T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
+      A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
+    } else {
+      if (dd == 0) {
+        __hip_atomic_store(&rec[hh * (D + 2)], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&rec[hh * (D + 2) + 1], den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(&rec[hh * (D + 2) + 2 + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (nsplit == 1) return;
+  // every thread's record stores have completed before the block takes its ticket
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(&p.tickets[qr * p.hkv + g], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    last = t == static_cast<unsigned>(nsplit - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Merge the splits: thread t owns (head, dim) pairs t, t + NT, ...; the records are
+  // read with device-scope loads.
+  const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
+  const int64_t rs = G * (D + 2);  // record stride between splits
+  for (int t = threadIdx.x; t < G * D; t += NT) {
+    const int hh = t / D, dd = t % D;
+    const float* base = base0 + hh * (D + 2);
+    float mx = -INFINITY;
+    for (int64_t sp = 0; sp < nsplit; ++sp)
+      mx = fmaxf(mx, __hip_atomic_load(&base[sp * rs], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float den = 0.0f, acc = 0.0f;
+    if (mx != -INFINITY) {
+      for (int64_t sp = 0; sp < nsplit; ++sp) {
+        const float* r = base + sp * rs;
+        const float c = exp2f(__hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
+        den = fmaf(__hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, den);
+        acc = fmaf(__hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, acc);
+      }
+    }
+    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
+    A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&p.tickets[qr * p.hkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 
 template <class A, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
@@ -180,7 +255,7 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
   const int64_t g = blockIdx.y;
   const int split = blockIdx.x;
   const int64_t n_keys = row_keys(p, b, s);
-  const int64_t nsplit = live_splits(n_keys, p.splits);
+  const int64_t nsplit = live_splits(n_keys, p.splits, p.min_per_split);
   if (split >= nsplit) return;  // surplus block for this context
   const int64_t per = (n_keys + nsplit - 1) / nsplit;
   const int64_t lo = split * per;
@@ -327,68 +402,230 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
   }
   __syncthreads();
 
-  // Merge the waves: thread t owns (head, dim) pairs t, t + NT, ...; with one split it
-  // writes the output, otherwise the block's partial record (device-scope stores).
-  float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * (D + 2);
-  for (int t = threadIdx.x; t < G * D; t += NT) {
-    const int hh = t / D, dd = t % D;
-    float mx = -INFINITY;
+  finish_rows<A, D, G, kWaves>(p, sm_m, sm_l, sm_o, last, qr, g, split, nsplit);
+}
+
+// ---- decode: one query position per row, bf16 q and cache, both products on MFMA ----
+//
+// grid = (splits, kv_heads, batch).  A block of kDecWaves waves owns one (row, kv head)
+// and a slice of positions; wave w takes the 32-position steps w, w + kDecWaves, ...
+// of the slice, with the next step's K and V loads in flight while a step computes.
+//   * Scores: S^T = K Q^T on v_mfma_f32_16x16x32_bf16, A = 16 cache rows (each lane
+//     loads 16 contiguous bytes of a K row), B = the G query heads of the group
+//     (columns >= G are zero).  Lane (j, h) receives the scores of head j for positions
+//     4h + r of a 16-position tile, so the softmax state of head j lives in the lanes
+//     with lane % 16 == j.  Products are exact and sums fp32; the log2(e)/sqrt(d)
+//     scale is applied to the fp32 scores.
+//   * O += P V on the same MFMA: the reduction index runs over positions, and the lane
+//     that holds a score is exactly the lane that supplies it as an A element (the k
+//     order of the product is free), so P never moves between lanes.  P is split into
+//     bf16 hi + lo parts (two MFMAs), which keeps it to about 16 significant bits.  V
+//     is the B operand with k = position; it is staged row-major in a per-wave LDS tile
+//     and gathered by column.
+//   * The per-wave states are merged in LDS, and split blocks merge through the same
+//     records and ticket as the general kernel.
+constexpr int kDecWaves = 8;
+// Split policy of the decode kernel, measured on MI355X with a cold cache (the layer's
+// K/V evicted by the weight stream, as in decode): at least 128 positions per split
+// block and at most 8 split blocks per (row, kv head) minimise the kernel time from
+// 128 to 4096 positions.  A split block costs a cross-block merge, so short contexts
+// keep a single block.
+constexpr int32_t kDecMinPerSplit = 128;
+constexpr int kDecMaxSplits = 8;
+
+template <int D, int G>
+__global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnArgs p) {
+  constexpr int NW = kDecWaves;
+  constexpr int KK = D / 32;                 // MFMA k steps of one score tile
+  constexpr int DT = D / 16;                 // 16-wide output tiles
+  constexpr int VR = D + 8;                  // padded LDS row of the staged V tile (bf16)
+  constexpr int VCH = 32 * (D / 8) / 64;     // 16-byte V pieces per lane per step
+  __shared__ __align__(16) uint16_t sv[NW][32 * VR];
+  __shared__ float sm_m[NW][G], sm_l[NW][G];
+  __shared__ float sm_o[NW][G][D];
+  __shared__ uint4 sq[D / 32][64];  // the score B operand, per lane
+  __shared__ bool last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, h = lane >> 4;
+  typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+  typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+  const int64_t qr = blockIdx.z;
+  const int64_t b = qr / p.seq, s = qr % p.seq;
+  const int64_t g = blockIdx.y;
+  const int split = blockIdx.x;
+  const int64_t n_keys = row_keys(p, b, s);
+  const int64_t nsplit = live_splits(n_keys, p.splits, p.min_per_split);
+  if (split >= nsplit) return;  // surplus block for this context
+  const int64_t per = (n_keys + nsplit - 1) / nsplit;
+  const int64_t lo = split * per;
+  const int64_t hi = lo + per < n_keys ? lo + per : n_keys;
+  const int64_t nsteps = (hi - lo + 31) / 32;
+  const int64_t my = nsteps > wave ? (nsteps - wave + NW - 1) / NW : 0;  // this wave's steps
+
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.kc) + b * p.cbs + g * p.cap * D;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.vc) + b * p.cbs + g * p.cap * D;
+
+  struct Buf {
+    uint4 k[2][KK];  // two 16-row score tiles
+    uint4 v[VCH];    // the step's 32 V rows, 16 bytes per lane per piece
+  };
+  // Loads step (clamped to this wave's last step; rows past the slice read row lo).
+  // Loads step i (clamped to this wave's last step; rows past the slice read row
+  // hi - 1).  Offsets are 32-bit element offsets from the (row, kv head) bases:
+  // one head's cache is cap * D elements.
+  constexpr int PR = D / 8;    // 16-byte pieces per cache row
+  constexpr int RPC = 64 / PR;  // V rows per load instruction
+  const uint32_t last_row = static_cast<uint32_t>(hi - 1);
+  auto issue = [&](Buf& bf, int64_t i) {
+    if (i >= my) i = my - 1;
+    const uint32_t base = static_cast<uint32_t>(lo + 32 * (wave + i * NW));
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w][hh]);
-    float den = 0.0f, acc = 0.0f;
-    if (mx != -INFINITY) {
+    for (int tt = 0; tt < 2; ++tt) {
+      const uint32_t pos = min(base + 16 * tt + j, last_row);
+      const uint16_t* kp = kbase + (pos * D + 8 * h);
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float c = exp2f(sm_m[w][hh] - mx);
-        den = fmaf(sm_l[w][hh], c, den);
-        acc = fmaf(sm_o[w][hh][dd], c, acc);
-      }
+      for (int kk = 0; kk < KK; ++kk) bf.k[tt][kk] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
     }
-    if (nsplit == 1) {
-      T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
-      A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
-    } else {
-      if (dd == 0) {
-        __hip_atomic_store(&rec[hh * (D + 2)], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&rec[hh * (D + 2) + 1], den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int c = 0; c < VCH; ++c) {
+      const uint32_t pos = min(base + lane / PR + RPC * c, last_row);
+      bf.v[c] = *reinterpret_cast<const uint4*>(vbase + (pos * D + 8 * (lane % PR)));
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.0f;  // head j's state over this lane's positions
+  f32x4_t o[DT];                          // O[4h + r][16 dt + j]
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint16_t* const tile = sv[wave];
+
+  auto compute = [&](const Buf& bf, int64_t i) {
+    const int64_t base = lo + 32 * (wave + i * NW);
+    // stage V row-major: piece c of the lane is row piece / (D/8), 8 columns
+#pragma unroll
+    for (int c = 0; c < VCH; ++c)
+      *reinterpret_cast<uint4*>(tile + (lane / PR + RPC * c) * VR + 8 * (lane % PR)) = bf.v[c];
+    // scores of positions base + 16 tt + 4 h + r for head j
+    float sc[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, bf.k[tt][kk]),
+                                                       __builtin_bit_cast(bf16x8_t, sq[kk][lane]), acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[tt][r] = base + 16 * tt + 4 * h + r < hi ? acc[r] * p.scale : -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    bm = fmaxf(bm, xor_partner<16>(bm, lane));
+    bm = fmaxf(bm, xor_partner<32>(bm, lane));
+    const float mn = fmaxf(m_run, bm);
+    const float c = mn == -INFINITY ? 1.0f : exp2f(m_run - mn);
+    float pr[2][4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[tt][r] = sc[tt][r] == -INFINITY ? 0.0f : exp2f(sc[tt][r] - mn);
+        sum += pr[tt][r];
       }
-      __hip_atomic_store(&rec[hh * (D + 2) + 2 + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    l_run = fmaf(l_run, c, sum);
+    m_run = mn;
+    // rescale O rows 4h + r by their head's factor (held by lane 16 h + 4 h + r)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float cr = __shfl(c, 16 * h + 4 * h + r);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt][r] *= cr;
+    }
+    // A operand: element e of lane (j, h) is position 16 (e >> 2) + 4 h + (e & 3)
+    bf16x8_t phi, plo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = pr[e >> 2][e & 3];
+      const __bf16 hb = static_cast<__bf16>(v);
+      phi[e] = hb;
+      plo[e] = static_cast<__bf16>(v - static_cast<float>(hb));
+    }
+    // B operand per output tile: V[that position][16 dt + j], gathered from the tile
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int e0 = 2 * e2, e1 = 2 * e2 + 1;
+        const int r0 = 16 * (e0 >> 2) + 4 * h + (e0 & 3), r1 = 16 * (e1 >> 2) + 4 * h + (e1 & 3);
+        w[e2] = static_cast<uint32_t>(tile[r0 * VR + 16 * dt + j]) |
+                (static_cast<uint32_t>(tile[r1 * VR + 16 * dt + j]) << 16);
+      }
+      const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop, o[dt], 0, 0, 0);
+    }
+  };
+
+  // Steps alternate between two buffers; the step after next is issued once a buffer
+  // is consumed.  Every path after an issue consumes that buffer (the exits finish
+  // the pending steps), so the loads stay where they are issued instead of being
+  // moved down to the one path that uses them.
+  Buf ba, bb;
+  if (my > 0) {
+    issue(ba, 0);
+    issue(bb, 1);
+  }
+  // B operand of the scores: lane (j, h) holds query head j of the group at
+  // d = 32 kk + 8 h .. +8 (zero for j >= G); staged once per block, behind the first
+  // cache loads.
+  if (wave == 0) {
+    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + (qr * p.hq + g * G + (j < G ? j : 0)) * D + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint4 v = *reinterpret_cast<const uint4*>(qp + 32 * kk);
+      if (j >= G) v = make_uint4(0, 0, 0, 0);
+      sq[kk][lane] = v;
     }
   }
-  if (nsplit == 1) return;
-  // every thread's record stores have completed before the block takes its ticket
-  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned t = __hip_atomic_fetch_add(&p.tickets[qr * p.hkv + g], 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    last = t == static_cast<unsigned>(nsplit - 1);
+  if (my > 0) {
+    for (int64_t i = 0;;) {
+      compute(ba, i);
+      if (i + 2 >= my) {
+        if (i + 1 < my) compute(bb, i + 1);
+        break;
+      }
+      issue(ba, i + 2);
+      compute(bb, i + 1);
+      if (i + 3 >= my) {
+        compute(ba, i + 2);
+        break;
+      }
+      issue(bb, i + 3);
+      i += 2;
+    }
+  }
+
+  // head j's sum over the four lane rows; all rows already share the running max
+  l_run += xor_partner<16>(l_run, lane);
+  l_run += xor_partner<32>(l_run, lane);
+  if (h == 0 && j < G) {
+    sm_m[wave][j] = m_run;
+    sm_l[wave][j] = l_run;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int q = 4 * h + r;
+    if (q < G) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) sm_o[wave][q][16 * dt + j] = o[dt][r];
+    }
   }
   __syncthreads();
-  if (!last) return;
-  // Merge the splits: thread t owns (head, dim) pairs t, t + NT, ...; the records are
-  // read with device-scope loads.
-  const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
-  const int64_t rs = G * (D + 2);  // record stride between splits
-  for (int t = threadIdx.x; t < G * D; t += NT) {
-    const int hh = t / D, dd = t % D;
-    const float* base = base0 + hh * (D + 2);
-    float mx = -INFINITY;
-    for (int64_t sp = 0; sp < nsplit; ++sp)
-      mx = fmaxf(mx, __hip_atomic_load(&base[sp * rs], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float den = 0.0f, acc = 0.0f;
-    if (mx != -INFINITY) {
-      for (int64_t sp = 0; sp < nsplit; ++sp) {
-        const float* r = base + sp * rs;
-        const float c = exp2f(__hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
-        den = fmaf(__hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, den);
-        acc = fmaf(__hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, acc);
-      }
-    }
-    T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
-    A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(&p.tickets[qr * p.hkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  finish_rows<ActBF16, D, G, NW>(p, sm_m, sm_l, sm_o, last, qr, g, split, nsplit);
 }
 
 int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
@@ -398,6 +635,19 @@ int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
   if (s < 1) s = 1;
   if (s > kMaxSplits) s = kMaxSplits;
   return static_cast<int>(s);
+}
+
+template <int D>
+am_status_code LaunchDecode(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((attention_decode_kernel<D, 1>), grid, dim3(kDecWaves * 64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attention_decode_kernel<D, 2>), grid, dim3(kDecWaves * 64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attention_decode_kernel<D, 4>), grid, dim3(kDecWaves * 64), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attention_decode_kernel<D, 8>), grid, dim3(kDecWaves * 64), 0, s, a); break;
+    default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
+  }
+  AM_RETURN_IF_LAUNCH_FAILED("attention");
+  return AM_STATUS_OK;
 }
 
 template <class A, int D>
@@ -461,9 +711,18 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
     p.tickets = reinterpret_cast<unsigned*>(ws);
     p.part = reinterpret_cast<float*>(ws + 256 * CeilDiv(batch * a->seq * a->hkv * 4, 256));
   }
-  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   const int64_t G = a->hq / a->hkv;
   hipStream_t s = AsStream(stream);
+  if (a->dtype == AM_DT_BF16 && a->seq == 1) {
+    AM_CHECK_ARG(a->capacity * a->head_dim < (int64_t{1} << 31), "attention: cache too large for 32-bit offsets");
+    // decode: MFMA kernel; an explicit split request is honoured down to 32 positions
+    p.min_per_split = a->num_splits > 0 ? 32 : kDecMinPerSplit;
+    if (a->num_splits <= 0 && p.splits > kDecMaxSplits) p.splits = kDecMaxSplits;
+    const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch));
+    return a->head_dim == 128 ? LaunchDecode<128>(G, grid, p, s) : LaunchDecode<64>(G, grid, p, s);
+  }
+  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
+  p.min_per_split = static_cast<int32_t>(kMinPerSplit);
   if (a->dtype == AM_DT_BF16)
     return a->head_dim == 128 ? LaunchD<ActBF16, 128>(G, grid, p, s) : LaunchD<ActBF16, 64>(G, grid, p, s);
   return a->head_dim == 128 ? LaunchD<ActF32, 128>(G, grid, p, s) : LaunchD<ActF32, 64>(G, grid, p, s);

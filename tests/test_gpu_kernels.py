@@ -318,6 +318,36 @@ def test_attention(act, d, case):
         close(got, O.attention(q, kc, vc, S, hq, hkv, d, cap, start), TOL[act], f"attention {name}")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 4), (8, 2), (16, 2)])
+@pytest.mark.parametrize("splits", [0, 7])
+def test_attention_decode_batched(d, heads, splits):
+    """bf16 decode (one query per row) for every query-group size, three batch rows with
+    their own device start positions and cache slices; forced and automatic splits.
+    Besides the 2e-2 bar, every element must be within one bf16 step of the oracle."""
+    hq, hkv = heads
+    cap, B = 1536, 3
+    starts = [4, 300, 1500]
+    q = O.round_bf16(O.synth_f32(13, 1, B * hq * d, std=1.0).reshape(B, hq * d))
+    kc = O.round_bf16(O.synth_f32(13, 2, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    vc = O.round_bf16(O.synth_f32(13, 3, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+    out = empty((B, hq * d), torch.int16)
+    posd = dev(np.array(starts, np.int64))
+    wsb = L.am_gfx950_attention_workspace_bytes(B, 1, hq, hkv, d, cap, splits)
+    ws = zeros((max(wsb, 1),), torch.uint8)
+    a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), 1, hq, hkv, d, cap, 0, p(posd), B, hkv * cap * d, 1, splits,
+                        p(ws), wsb)
+    for _ in range(2):  # second call checks the tickets were left at zero
+        L.call("am_gfx950_attention", a, stream())
+        got = O.bf16_to_f32(bits_host(out))
+        for r in range(B):
+            ref = O.attention(q[r:r + 1], kc[r], vc[r], 1, hq, hkv, d, cap, starts[r])[0]
+            close(got[r], ref, TOL["bf16"], f"decode row {r} start {starts[r]}")
+            bad = np.abs(got[r] - ref) > 2.0 ** -7 * np.abs(ref) + 1e-4 * np.abs(ref).max()
+            assert not bad.any(), (r, np.flatnonzero(bad)[:8], got[r][bad][:8], ref[bad][:8])
+
+
 def test_attention_special_cases():
     # one position -> out = V row; identical keys -> out = mean of V over the window
     hq, hkv, d, cap = 4, 1, 64, 64
