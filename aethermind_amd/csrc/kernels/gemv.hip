@@ -223,9 +223,11 @@ __device__ __forceinline__ float silu_ref(float g) {
 template <int EPI>
 __device__ __forceinline__ void pair_rows(const GemvArgs& p, int64_t u, int64_t& r0, int64_t& r1) {
   if constexpr (EPI == kEpiQkv) {
-    const int64_t half = p.d / 2;
-    const int64_t head = u / half, i = u % half;
-    r0 = head * p.d + i;
+    // 32-bit division: units and head_dim are far below 2^31 (checked on the host)
+    const uint32_t half = static_cast<uint32_t>(p.d / 2);
+    const uint32_t uu = static_cast<uint32_t>(u);
+    const uint32_t head = uu / half, i = uu - head * half;
+    r0 = static_cast<int64_t>(head) * p.d + i;
     r1 = r0 + half;
   } else if constexpr (EPI == kEpiGateUp) {
     r0 = u;  // gate row u, up row u: rows [0, F) are gate, [F, 2F) are up
@@ -316,7 +318,9 @@ __device__ __forceinline__ float piece_elem(const uint4& v, int e) {
     return __uint_as_float(w[e]);
 }
 
-template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW>
+// ONE: every wave has at most one load block (the launch covers all iterations with
+// one per wave and x stays in registers), so there is no second buffer to prefetch.
+template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW, bool ONE = false>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   constexpr int NT = NW * 64;  // threads per block
   using XS = XStore<A, WF>;
@@ -355,11 +359,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * NW + __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t TW = static_cast<int64_t>(gridDim.x) * NW;
   const int64_t niter = (p.units + P - 1) / P;
-  const int ng = SC ? static_cast<int>(K / p.group) : 1;
+  // 32-bit divisions (the host keeps K, units and the grid below 2^31): the 64-bit
+  // forms cost a long scalar sequence ahead of the first loads
+  const int ng = SC ? static_cast<int>(static_cast<uint32_t>(K) / static_cast<uint32_t>(p.group)) : 1;
   const int chunks_per_group = SC ? p.group / kc : 1;
   const uint16_t* sc16 = static_cast<const uint16_t*>(p.scales);
   // this wave's iterations are gw, gw + TW, ...; each is NB load blocks
-  const int64_t nit_w = gw < niter ? (niter - 1 - gw) / TW + 1 : 0;
+  const int64_t nit_w =
+      gw < niter ? static_cast<int64_t>(static_cast<uint32_t>(niter - 1 - gw) / static_cast<uint32_t>(TW)) + 1 : 0;
   const int64_t nblk = nit_w * NB;
 
   // ---- 1. prologue operands: all loads issued at once, before any weight load ----
@@ -439,7 +446,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
         f.w[pp][0][jj] = ld_stream(row0, c);
         f.w[pp][1][jj] = ld_stream(row1, c);
         if constexpr (SC) {
-          const int64_t g = c / chunks_per_group;
+          const int g = static_cast<int>(c) / chunks_per_group;
           f.s[pp][0][jj] = sc16[r0 * ng + g];
           f.s[pp][1][jj] = sc16[r1 * ng + g];
         }
@@ -582,7 +589,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   __syncthreads();
 
   // ---- 4. second weight block, then this lane's x chunks ----
-  issue(fb, 1);
+  if constexpr (!ONE) issue(fb, 1);
   uint32_t xr[XL ? 1 : JM][XDW];
   float corr[XL ? 1 : JM];
   if constexpr (!XL) {
@@ -722,7 +729,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   // that stays in the loop both buffers are always pending in the same order. ----
   float acc[P][2] = {};
   int64_t b = 0;
-  while (b < nblk) {
+  if constexpr (ONE) {
+    static_assert(NB == 1, "single-block launches keep x in registers");
+    if (nblk > 0) {
+      accum(fa, 0, acc);
+      finish(acc, blk_it(0));
+    }
+  }
+  while (!ONE && b < nblk) {
     accum(fa, blk_jb(b), acc);
     if (blk_jb(b) == NB - 1) finish(acc, blk_it(b));
     if (b + 2 >= nblk) {
@@ -826,6 +840,7 @@ int64_t RowBytes(int32_t fmt, int64_t k) {
 
 am_status_code ValidateWeight(const am_gfx950_weight& w) {
   AM_CHECK_ARG(w.data != nullptr && w.n > 0 && w.k > 0, "weight: null data or empty shape");
+  AM_CHECK_ARG(w.n < (int64_t{1} << 31) && w.k < (int64_t{1} << 31), "weight: dimensions must be below 2^31");
   AM_CHECK_ARG(w.format >= AM_WF_F32 && w.format <= AM_WF_INT4, "weight: unknown format");
   const int kc[4] = {4, 8, 16, 32};
   AM_CHECK_ARG(w.k % kc[w.format] == 0, "weight: in_features must fill whole 16-byte chunks");
@@ -835,6 +850,21 @@ am_status_code ValidateWeight(const am_gfx950_weight& w) {
   }
   if (w.format >= AM_WF_INT8) AM_CHECK_ARG(w.scales != nullptr, "weight: quantized weight needs scales");
   AM_CHECK_ARG((reinterpret_cast<uintptr_t>(w.data) & 15u) == 0, "weight: data must be 16-byte aligned");
+  return AM_STATUS_OK;
+}
+
+template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW, bool ONE>
+am_status_code LaunchGrid(const GemvArgs& g, int64_t blocks, int64_t lds, hipStream_t s) {
+  LaunchTiming& lt = ThreadLaunchTiming();
+  if (lt.start != nullptr) {
+    hipExtLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW, ONE>), dim3(static_cast<unsigned>(blocks)),
+                          dim3(NW * 64), static_cast<size_t>(lds), s, lt.start, lt.stop, 0, g);
+    lt.used = true;
+  } else {
+    hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW, ONE>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(NW * 64), static_cast<size_t>(lds), s, g);
+  }
+  AM_RETURN_IF_LAUNCH_FAILED("gemv");
   return AM_STATUS_OK;
 }
 
@@ -855,17 +885,13 @@ am_status_code LaunchNW(const GemvArgs& g, int64_t lds, hipStream_t s) {
   const int64_t niter = CeilDiv(g.units, P);
   int64_t blocks = std::min<int64_t>(static_cast<int64_t>(DeviceCUs()) * cached_blocks, CeilDiv(niter, NW));
   if (blocks > 65536) blocks = 65536;
-  LaunchTiming& lt = ThreadLaunchTiming();
-  if (lt.start != nullptr) {
-    hipExtLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)),
-                          dim3(NW * 64), static_cast<size_t>(lds), s, lt.start, lt.stop, 0, g);
-    lt.used = true;
-  } else {
-    hipLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64),
-                       static_cast<size_t>(lds), s, g);
+  // one load block per wave: x in registers (a single block per iteration) and no
+  // wave with a second iteration
+  constexpr bool XL = JM * XStore<A, WF>::kDW > 32;
+  if constexpr (!XL) {
+    if (blocks * NW >= niter) return LaunchGrid<A, WF, NORM, EPI, JM, P, NW, true>(g, blocks, lds, s);
   }
-  AM_RETURN_IF_LAUNCH_FAILED("gemv");
-  return AM_STATUS_OK;
+  return LaunchGrid<A, WF, NORM, EPI, JM, P, NW, false>(g, blocks, lds, s);
 }
 
 template <class A, int WF, bool NORM, int EPI, int JM, int P>
@@ -979,6 +1005,7 @@ extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a,
                "fused_qkv: bad head configuration");
   AM_CHECK_ARG(a->w_qkv.n == (a->hq + 2 * a->hkv) * a->head_dim, "fused_qkv: weight rows != (hq+2hkv)*d");
   AM_CHECK_ARG(a->head_dim <= 512, "fused_qkv: head_dim above 512");
+  AM_CHECK_ARG(a->w_qkv.n < (int64_t{1} << 31), "fused_qkv: too many weight rows");
   AM_CHECK_ARG(a->h && a->norm_w && a->cos_tab && a->sin_tab && a->pos && a->q_out && a->k_cache && a->v_cache,
                "fused_qkv: null pointer");
   AM_CHECK_ARG(a->eps > 0.0f, "fused_qkv: eps must be positive");
