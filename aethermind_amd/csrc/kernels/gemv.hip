@@ -853,6 +853,137 @@ am_status_code ValidateWeight(const am_gfx950_weight& w) {
   return AM_STATUS_OK;
 }
 
+// ---- split-K GEMV for long rows ----
+// When a lane's share of x no longer fits in registers (rows longer than 64 lanes x 2
+// chunks), a block owns kSkRows consecutive rows and its NW*64 lanes split every row
+// instead: lane slot t reads 16-byte chunk t of all kSkRows rows (each load
+// instruction still moves 1 KiB of one row), holds the kc x values of chunk t in
+// registers, and the block issues all of its rows' weight loads at once.  The row
+// sums are folded over the lanes (permlane swaps, then DPP) and over the waves in LDS.
+constexpr int kSkRows = 16;
+constexpr int kSkWaves = 8;
+
+template <class A, int WF, int EPI>
+__global__ __launch_bounds__(kSkWaves * 64) void gemv_ksplit_kernel(GemvArgs p) {
+  static_assert(EPI == kEpiStore || EPI == kEpiResidual, "split-K rows: plain or residual epilogue");
+  using XS = XStore<A, WF>;
+  using T = typename A::T;
+  constexpr int kc = Fmt<WF>::kc;
+  constexpr int XDW = XS::kDW;
+  constexpr bool SC = WF == AM_WF_INT4;
+  __shared__ float red[kSkWaves][kSkRows];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t C = p.row_bytes / 16;  // <= kSkWaves * 64 (host)
+  const int64_t r_base = static_cast<int64_t>(blockIdx.x) * kSkRows;
+  const bool active = tid < C;
+  const int64_t c = active ? tid : 0;
+
+  // Every load is unconditional and issued before any use: the epilogue operand (each
+  // thread reads row tid % kSkRows, in bounds), x, then the block's weight chunks and
+  // scales, each as a uniform row base plus a 32-bit lane offset.
+  const uint32_t cu = static_cast<uint32_t>(c);
+  float res = 0.0f;
+  if constexpr (EPI == kEpiResidual) {
+    const int64_t rr = r_base + (tid & (kSkRows - 1));
+    res = A::load(static_cast<const T*>(p.residual), rr < p.n ? rr : p.n - 1);
+  }
+  uint32_t xd[XDW];
+  {
+    const uint4* xs = reinterpret_cast<const uint4*>(p.x) + cu * (XDW / 4);
+#pragma unroll
+    for (int i = 0; i < XDW / 4; ++i) {
+      const uint4 v = xs[i];
+      xd[4 * i] = v.x; xd[4 * i + 1] = v.y; xd[4 * i + 2] = v.z; xd[4 * i + 3] = v.w;
+    }
+  }
+  uint4 w[kSkRows];
+  uint32_t sb[SC ? kSkRows : 1];
+  const int ng = SC ? static_cast<int>(static_cast<uint32_t>(p.k) / static_cast<uint32_t>(p.group)) : 1;
+  const uint32_t g = SC ? cu / static_cast<uint32_t>(p.group / kc) : 0u;
+  const uint16_t* sc16 = static_cast<const uint16_t*>(p.scales);
+#pragma unroll
+  for (int r = 0; r < kSkRows; ++r) {
+    const int64_t row = r_base + r < p.n ? r_base + r : p.n - 1;
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.w + row * p.row_bytes) + cu);
+    w[r] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+  if constexpr (SC) {
+#pragma unroll
+    for (int r = 0; r < kSkRows; ++r) {
+      const int64_t row = r_base + r < p.n ? r_base + r : p.n - 1;
+      sb[r] = (sc16 + row * ng)[g];
+    }
+  }
+
+  // offset correction of this lane's chunk: kOff * sum(x)
+  float corr = 0.0f;
+  if constexpr (XS::kOff != 0.0f) {
+    float sx = 0.0f;
+    if constexpr (XS::kBF16) {
+#pragma unroll
+      for (int t = 0; t < XDW; ++t) sx += __uint_as_float(xd[t] << 16) + __uint_as_float(xd[t] & 0xFFFF0000u);
+    } else {
+#pragma unroll
+      for (int t = 0; t < XDW; ++t) sx += __uint_as_float(xd[t]);
+    }
+    corr = XS::kOff * sx;
+  }
+  const Unpack up;
+  float acc[kSkRows];
+#pragma unroll
+  for (int r = 0; r < kSkRows; ++r) {
+    const float dv = chunk_dot<A, WF>(w[r], xd, -corr, up);
+    acc[r] = SC ? f16_bits_to_f32(sb[r]) * dv : dv;
+    if (!active) acc[r] = 0.0f;
+  }
+
+  // lanes: row 4 (lane / 16) + k of the block in every lane of that 16-lane row
+  float x8[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x8[k] = swap32_add(acc[k], acc[k + 8]);
+  float z[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) z[k] = sum16(swap16_add(x8[k], x8[k + 4]));
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) red[wave][4 * (lane >> 4) + k] = z[k];
+  }
+  __syncthreads();
+  if (tid < kSkRows) {  // res holds row r_base + tid here
+    const int64_t row = r_base + tid;
+    if (row < p.n) {
+      float a = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < kSkWaves; ++wv) a += red[wv][tid];
+      if constexpr (WF == AM_WF_INT8) a *= static_cast<const float*>(p.scales)[row];
+      if constexpr (EPI == kEpiResidual) {
+        A::store(static_cast<T*>(p.out), row, res + A::round(a));
+      } else if (p.out_f32) {
+        static_cast<float*>(p.out)[row] = a;
+      } else {
+        A::store(static_cast<T*>(p.out), row, a);
+      }
+    }
+  }
+}
+
+template <class A, int WF, int EPI>
+am_status_code LaunchKsplit(const GemvArgs& g, hipStream_t s) {
+  const int64_t blocks = CeilDiv(g.n, kSkRows);
+  LaunchTiming& lt = ThreadLaunchTiming();
+  if (lt.start != nullptr) {
+    hipExtLaunchKernelGGL((gemv_ksplit_kernel<A, WF, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kSkWaves * 64),
+                          0, s, lt.start, lt.stop, 0, g);
+    lt.used = true;
+  } else {
+    hipLaunchKernelGGL((gemv_ksplit_kernel<A, WF, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kSkWaves * 64), 0,
+                       s, g);
+  }
+  AM_RETURN_IF_LAUNCH_FAILED("gemv");
+  return AM_STATUS_OK;
+}
+
 template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW, bool ONE>
 am_status_code LaunchGrid(const GemvArgs& g, int64_t blocks, int64_t lds, hipStream_t s) {
   LaunchTiming& lt = ThreadLaunchTiming();
@@ -923,19 +1054,36 @@ template <class A, int WF, bool NORM, int EPI>
 am_status_code LaunchT(const GemvArgs& g, hipStream_t s) {
   using XS = XStore<A, WF>;
   const int64_t J = CeilDiv(g.row_bytes / 16, 64);
+  // Long rows (more than two chunk-steps per lane): split each row over a block's
+  // lanes, one chunk per lane.  That kernel reads x in its storage format (bf16
+  // exactly where the dot takes bf16 pairs, fp32 for fp32 activations).
+  constexpr bool kSkFormat = (A::kDtype == AM_DT_BF16) == XS::kBF16;
+  if constexpr (!NORM && kSkFormat && (EPI == kEpiStore || EPI == kEpiResidual)) {
+    const int64_t tb = A::kDtype == AM_DT_BF16 ? 2 : 4;
+    auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    const bool vec = al16(g.x) && (g.k * tb) % 16 == 0 && (EPI != kEpiResidual || al16(g.residual));
+    if (J * XS::kDW > 32 && vec && g.row_bytes / 16 <= kSkWaves * 64 && g.n < (int64_t{1} << 31) / kSkRows) {
+      GemvArgs ga = g;
+      ga.vec = 1;
+      return LaunchKsplit<A, WF, EPI>(ga, s);
+    }
+  }
   // One row pair per iteration keeps two weight buffers within ~100 registers, so
   // four to five waves fit per SIMD; the lm_head (argmax epilogue, 64k pairs) runs two
   // pairs per iteration.
   constexpr int PS = EPI == kEpiLmHead ? 2 : 1;
   if (J <= 2) return LaunchJ<A, WF, NORM, EPI, 2, PS>(g, s);
   if (J <= 4) return LaunchJ<A, WF, NORM, EPI, 4, 1>(g, s);
-  if constexpr (8 * XS::kDW <= 128) {
+  // The prologue holds a thread's x input pieces (JM*64*kc values over >= 256
+  // threads) in registers: at most 8 pieces, i.e. JM * kc <= 32 * (values per piece).
+  constexpr int kEpp = 16 / static_cast<int>(sizeof(typename A::T));
+  if constexpr (8 * Fmt<WF>::kc <= 32 * kEpp) {
     if (J <= 8) return LaunchJ<A, WF, NORM, EPI, 8, 1>(g, s);
   }
-  if constexpr (16 * XS::kDW <= 128) {
+  if constexpr (16 * Fmt<WF>::kc <= 32 * kEpp) {
     if (J <= 16) return LaunchJ<A, WF, NORM, EPI, 16, 1>(g, s);
   }
-  if constexpr (32 * XS::kDW <= 128) {
+  if constexpr (32 * Fmt<WF>::kc <= 32 * kEpp) {
     if (J <= 32) return LaunchJ<A, WF, NORM, EPI, 32, 1>(g, s);
   }
   return SetLastError(AM_STATUS_UNIMPLEMENTED, "gemv: in_features too large for register tiling of this format");

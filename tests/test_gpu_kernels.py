@@ -228,6 +228,65 @@ def test_linear_gemm_int4_multi_step_groups(group):
         close(got[r], ref[r], 3e-2, f"row {r}")
 
 
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [N.AM_WF_F32, N.AM_WF_BF16, N.AM_WF_INT8, N.AM_WF_INT4])
+@pytest.mark.parametrize("nk", [(1040, 14336), (100, 6144)])
+def test_linear_gemv_long_rows(act, fmt, nk):
+    """Rows longer than two chunks per lane: the split-K kernel (INT4) and the
+    x-in-LDS kernel (other formats), including a row count that is not a multiple
+    of the split-K block's 16 rows."""
+    n, k = nk
+    wref, dw, keep = _weights(n, k, fmt, seed=15)
+    x = O.synth_f32(16, 1, k, std=1.0).reshape(1, k)
+    # K > 8192 is served for INT4 with any activations and for bf16 activations with
+    # bf16 / INT8 weights; the other combinations (only the fp32 tiny model uses fp32
+    # activations, at K <= 1376) are refused cleanly
+    unsupported = k > 8192 and (fmt == N.AM_WF_F32 or (act == "f32" and fmt != N.AM_WF_INT4))
+    if unsupported:
+        xd = dev(x) if act == "f32" else bf16_dev(O.bf16_bits(O.round_bf16(x)))
+        out = empty((1, n), torch.float32)
+        dt = N.AM_DT_F32 if act == "f32" else N.AM_DT_BF16
+        with pytest.raises(N.NativeError) as e:
+            L.call("am_gfx950_linear", N.LinearArgs(p(xd), dt, 1, dw, p(out), N.AM_DT_F32, None, 1), stream())
+        assert e.value.status == "UNIMPLEMENTED"
+        return
+    res = O.synth_f32(16, 2, n, std=1.0).reshape(1, n)
+    if act == "bf16":
+        x, res = O.round_bf16(x), O.round_bf16(res)
+        xd, rd, dt = bf16_dev(O.bf16_bits(x)), bf16_dev(O.bf16_bits(res)), N.AM_DT_BF16
+        out = empty((1, n), torch.int16)
+        cv = lambda t: O.bf16_to_f32(bits_host(t))  # noqa: E731
+        rnd = O.round_bf16
+    else:
+        xd, rd, dt = dev(x), dev(res), N.AM_DT_F32
+        out = empty((1, n), torch.float32)
+        cv, rnd = host, (lambda v: v)  # noqa: E731
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), dt, 1, dw, p(out), dt, None, 1), stream())
+    ref = O.linear(x, wref)
+    close(cv(out), ref, TOL[act], f"gemv act={act} fmt={fmt} {n}x{k}")
+    for r in (0, n // 2, n - 1):
+        close(cv(out)[0, r:r + 1], ref[0, r:r + 1], 3e-2 if act == "bf16" else 2e-3, f"row {r}")
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), dt, 1, dw, p(out), dt, p(rd), 1), stream())
+    close(cv(out), rnd(res + rnd(ref)), TOL[act], f"gemv+residual act={act} fmt={fmt} {n}x{k}")
+
+
+def test_fused_linear_residual_down_shape():
+    """The decode down projection: h = round(h + round(W x)) in place, K = 14336."""
+    n, k = 4096, 14336
+    wref, dw, keep = _weights(n, k, N.AM_WF_INT4, seed=17)
+    x = O.round_bf16(O.synth_f32(18, 1, k, std=1.0).reshape(1, k))
+    h = O.round_bf16(O.synth_f32(18, 2, n, std=1.0).reshape(1, n))
+    xd, hd = bf16_dev(O.bf16_bits(x)), bf16_dev(O.bf16_bits(h))
+    L.call("am_gfx950_fused_linear_residual", N.FusedLinearResidualArgs(p(xd), dw, p(hd), N.AM_DT_BF16), stream())
+    wx = O.round_bf16(O.linear(x, wref))
+    ref = O.round_bf16(h + wx)
+    got = O.bf16_to_f32(bits_host(hd))
+    close(got, ref, TOL["bf16"], "fused down")
+    # every element within one bf16 step of each of the two roundings
+    bad = np.abs(got - ref) > 2.0 ** -7 * (np.abs(ref) + np.abs(wx)) + 1e-6
+    assert not bad.any(), np.flatnonzero(bad)[:8]
+
+
 def test_linear_residual_and_f32_logits():
     n, k = 640, 512
     wref, dw, keep = _weights(n, k, N.AM_WF_INT4, seed=9)
