@@ -234,7 +234,6 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
 
 template <class A, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
-  constexpr int NT = kWaves * 64;
   constexpr int LP = D / 8;                                 // lanes per cache row
   constexpr int PPW = 64 / LP;                              // rows per wave step
   // rows per lane group per batch: two batches of raw K/V rows stay in registers

@@ -30,9 +30,12 @@ def _short(name: str) -> str:
 
 
 def _gemv_epilogue(name: str):
-    """EPI template argument of a gemv_kernel instance (0 plain store, 1 residual, 2 qkv,
-    3 gate/up, 4 lm_head), None for other kernels"""
+    """EPI template argument of a gemv_kernel or gemv_ksplit_kernel instance (0 plain
+    store, 1 residual, 2 qkv, 3 gate/up, 4 lm_head), None for other kernels"""
     m = re.search(GEMV_PREFIX + r"<\w+, (\d+), (?:true|false), (\d+),", name)
+    if m:
+        return int(m.group(2))
+    m = re.search(r"gemv_ksplit_kernel<\w+, (\d+), (\d+)>", name)
     return int(m.group(2)) if m else None
 
 
