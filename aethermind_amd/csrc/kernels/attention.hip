@@ -627,6 +627,195 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
   finish_rows<ActBF16, D, G, NW>(p, sm_m, sm_l, sm_o, last, qr, g, split, nsplit);
 }
 
+// ---- prefill / chunked prefill: many query rows, bf16, both products on MFMA ----
+//
+// grid = (ceil(seq / QB), kv_heads, batch) with kPreWaves-wave blocks.  Each wave owns
+// 16 query columns: 16/G consecutive query positions x the G heads of the kv group
+// (column j = position j / G, head j % G).  The block walks the key positions up to its
+// last query's position in tiles of 32, each K and V tile loaded once into LDS
+// (double-buffered: tile t+1 is fetched into registers while tile t is consumed) and
+// shared by the block's waves.  Per tile a wave computes S^T = K Q^T (A = 16 K rows
+// from LDS, B = its 16 query columns held in registers), masks keys after each query's
+// position, updates the base-2 online softmax of its columns exactly as the decode
+// kernel does, and adds P V on MFMA (P as bf16 hi + lo, V gathered by column from the
+// padded LDS tile).  Waves own distinct queries, so there is no merge: each wave
+// normalises its columns and writes them.
+constexpr int kPreWaves = 4;
+
+template <int D, int G>
+__global__ __launch_bounds__(kPreWaves * 64) void attention_prefill_kernel(AttnArgs p) {
+  constexpr int NW = kPreWaves, NT = NW * 64;
+  constexpr int QT = 16 / G;               // query positions per wave
+  constexpr int QB = NW * QT;              // query positions per block
+  constexpr int KK = D / 32;               // MFMA k steps of one score tile
+  constexpr int DT = D / 16;               // 16-wide output tiles
+  constexpr int KR = D + 8;                // padded LDS row (bf16) of the K and V tiles
+  constexpr int TP = 32;                   // key positions per tile
+  constexpr int PR = D / 8;                // 16-byte pieces per cache row
+  constexpr int PCH = TP * PR / NT;        // pieces per thread per tile (K and V each)
+  static_assert(PCH >= 1 && TP * PR % NT == 0, "tile pieces must divide over the block");
+  typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+  typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+  __shared__ __align__(16) uint16_t sk[2][TP * KR];
+  __shared__ __align__(16) uint16_t sv[2][TP * KR];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, h = lane >> 4;
+  const int64_t b = blockIdx.z, g = blockIdx.y;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * QB;
+  const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
+  // this lane's query column j: position s, absolute position qpos (-1: no query)
+  const int64_t s = s0 + wave * QT + j / G;
+  const int64_t qpos = s < p.seq ? start + s : -1;
+  const int64_t s_last = s0 + QB - 1 < p.seq - 1 ? s0 + QB - 1 : p.seq - 1;
+  int64_t kend = start + s_last + 1;  // keys the block needs: [0, kend)
+  if (kend > p.cap) kend = p.cap;
+  const int64_t ntiles = (kend + TP - 1) / TP;
+
+  // B operand: query column j at d = 32 kk + 8 h .. +8 (zero for missing queries)
+  bf16x8_t qop[KK];
+  {
+    const int64_t sq = s < p.seq ? s : p.seq - 1;
+    const uint16_t* qp =
+        static_cast<const uint16_t*>(p.q) + ((b * p.seq + sq) * p.hq + g * G + j % G) * D + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint4 v = *reinterpret_cast<const uint4*>(qp + 32 * kk);
+      if (qpos < 0) v = make_uint4(0, 0, 0, 0);
+      qop[kk] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.kc) + b * p.cbs + g * p.cap * D;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.vc) + b * p.cbs + g * p.cap * D;
+  const uint32_t last_row = static_cast<uint32_t>(kend - 1);
+  uint4 kr[PCH], vr[PCH];
+  // piece c of the thread: tile row tid / PR + c * NT / PR, 8 columns at 8 * (tid % PR)
+  auto load_tile = [&](int64_t t) {
+#pragma unroll
+    for (int c = 0; c < PCH; ++c) {
+      const uint32_t pos = min(static_cast<uint32_t>(t * TP + tid / PR + c * (NT / PR)), last_row);
+      kr[c] = *reinterpret_cast<const uint4*>(kbase + (pos * D + 8 * (tid % PR)));
+      vr[c] = *reinterpret_cast<const uint4*>(vbase + (pos * D + 8 * (tid % PR)));
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < PCH; ++c) {
+      const int row = tid / PR + c * (NT / PR);
+      *reinterpret_cast<uint4*>(&sk[buf][row * KR + 8 * (tid % PR)]) = kr[c];
+      *reinterpret_cast<uint4*>(&sv[buf][row * KR + 8 * (tid % PR)]) = vr[c];
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4_t o[DT];  // O[column 4h + r][16 dt + j]
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int buf, int64_t t) {
+    const uint16_t* kt = sk[buf];
+    const uint16_t* vt = sv[buf];
+    float sc[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const uint4 a = *reinterpret_cast<const uint4*>(kt + (16 * tt + j) * KR + 32 * kk + 8 * h);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), qop[kk], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t key = t * TP + 16 * tt + 4 * h + r;
+        sc[tt][r] = key <= qpos && key < kend ? acc[r] * p.scale : -INFINITY;
+      }
+    }
+    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    bm = fmaxf(bm, xor_partner<16>(bm, lane));
+    bm = fmaxf(bm, xor_partner<32>(bm, lane));
+    const float mn = fmaxf(m_run, bm);
+    const float c = mn == -INFINITY ? 1.0f : exp2f(m_run - mn);
+    float pr[2][4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[tt][r] = sc[tt][r] == -INFINITY ? 0.0f : exp2f(sc[tt][r] - mn);
+        sum += pr[tt][r];
+      }
+    l_run = fmaf(l_run, c, sum);
+    m_run = mn;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float cr = __shfl(c, 16 * h + 4 * h + r);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt][r] *= cr;
+    }
+    bf16x8_t phi, plo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = pr[e >> 2][e & 3];
+      const __bf16 hb = static_cast<__bf16>(v);
+      phi[e] = hb;
+      plo[e] = static_cast<__bf16>(v - static_cast<float>(hb));
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int e0 = 2 * e2, e1 = 2 * e2 + 1;
+        const int r0 = 16 * (e0 >> 2) + 4 * h + (e0 & 3), r1 = 16 * (e1 >> 2) + 4 * h + (e1 & 3);
+        w[e2] = static_cast<uint32_t>(vt[r0 * KR + 16 * dt + j]) | (static_cast<uint32_t>(vt[r1 * KR + 16 * dt + j]) << 16);
+      }
+      const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop, o[dt], 0, 0, 0);
+    }
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int64_t t = 0; t < ntiles; ++t) {
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(t + 1);
+    compute(static_cast<int>(t & 1), t);
+    if (more) store_tile(static_cast<int>((t + 1) & 1));
+    __syncthreads();
+  }
+
+  // column j's sum over the four lane rows, then normalise and write
+  l_run += xor_partner<16>(l_run, lane);
+  l_run += xor_partner<32>(l_run, lane);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int q = 4 * h + r;  // this lane's output column
+    const float lq = __shfl(l_run, 16 * h + q);
+    const int64_t sq = s0 + wave * QT + q / G;
+    if (sq >= p.seq) continue;
+    uint16_t* out = static_cast<uint16_t*>(p.out) + ((b * p.seq + sq) * p.hq + g * G + q % G) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) out[16 * dt + j] = f32_to_bf16_bits(lq > 0.0f ? o[dt][r] / lq : 0.0f);
+  }
+}
+
+template <int D>
+am_status_code LaunchPrefill(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((attention_prefill_kernel<D, 1>), grid, dim3(kPreWaves * 64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attention_prefill_kernel<D, 2>), grid, dim3(kPreWaves * 64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attention_prefill_kernel<D, 4>), grid, dim3(kPreWaves * 64), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attention_prefill_kernel<D, 8>), grid, dim3(kPreWaves * 64), 0, s, a); break;
+    default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
+  }
+  AM_RETURN_IF_LAUNCH_FAILED("attention");
+  return AM_STATUS_OK;
+}
+
 int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
   if (requested > 0) return requested;
   if (seq > 1) return 1;
@@ -719,6 +908,14 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
     if (a->num_splits <= 0 && p.splits > kDecMaxSplits) p.splits = kDecMaxSplits;
     const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch));
     return a->head_dim == 128 ? LaunchDecode<128>(G, grid, p, s) : LaunchDecode<64>(G, grid, p, s);
+  }
+  if (a->dtype == AM_DT_BF16) {
+    // prefill: MFMA kernel, one block per (16 query columns per wave) x kv head x row
+    AM_CHECK_ARG(a->capacity * a->head_dim < (int64_t{1} << 31), "attention: cache too large for 32-bit offsets");
+    const int64_t qb = kPreWaves * (16 / G);
+    const dim3 grid(static_cast<unsigned>(CeilDiv(a->seq, qb)), static_cast<unsigned>(a->hkv),
+                    static_cast<unsigned>(batch));
+    return a->head_dim == 128 ? LaunchPrefill<128>(G, grid, p, s) : LaunchPrefill<64>(G, grid, p, s);
   }
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   p.min_per_split = static_cast<int32_t>(kMinPerSplit);

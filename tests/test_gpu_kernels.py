@@ -407,6 +407,33 @@ def test_attention_decode_batched(d, heads, splits):
             assert not bad.any(), (r, np.flatnonzero(bad)[:8], got[r][bad][:8], ref[bad][:8])
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 4), (8, 2), (16, 2)])
+@pytest.mark.parametrize("chunk", [(1, 77, 0), (2, 200, 700)])
+def test_attention_prefill_mfma(d, heads, chunk):
+    """bf16 prefill / chunked prefill (many query rows, causal, GQA) for every query-group
+    size, with batch rows at their own device start positions.  Besides the 2e-2 bar,
+    every element must be within one bf16 step of the oracle."""
+    hq, hkv = heads
+    B, S, start0 = chunk
+    cap = 1024
+    starts = [start0 + 13 * r for r in range(B)]
+    q = O.round_bf16(O.synth_f32(22, 1, B * S * hq * d, std=1.0).reshape(B, S, hq * d))
+    kc = O.round_bf16(O.synth_f32(22, 2, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    vc = O.round_bf16(O.synth_f32(22, 3, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+    out = empty((B, S, hq * d), torch.int16)
+    posd = dev(np.array(starts, np.int64))
+    a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), S, hq, hkv, d, cap, 0, p(posd), B, hkv * cap * d, 1, 0, None, 0)
+    L.call("am_gfx950_attention", a, stream())
+    got = O.bf16_to_f32(bits_host(out))
+    for r in range(B):
+        ref = O.attention(q[r], kc[r], vc[r], S, hq, hkv, d, cap, starts[r])
+        close(got[r], ref, TOL["bf16"], f"prefill row {r} start {starts[r]}")
+        bad = np.abs(got[r] - ref) > 2.0 ** -7 * np.abs(ref) + 1e-4 * np.abs(ref).max()
+        assert not bad.any(), (r, np.argwhere(bad)[:8])
+
+
 def test_attention_special_cases():
     # one position -> out = V row; identical keys -> out = mean of V over the window
     hq, hkv, d, cap = 4, 1, 64, 64
