@@ -161,6 +161,12 @@ Status AttentionKernel(const KernelContext& ctx) noexcept {
   a.head_dim = at.d;
   a.capacity = at.cap;
   a.batch = 1;
+  if (at.batch > 1) {
+    if (a.seq % at.batch != 0) return Status::InvalidArgument("AttentionKernel: rows are not a whole batch");
+    a.batch = at.batch;
+    a.seq /= at.batch;
+    a.cache_batch_stride = at.cbs;
+  }
   a.dtype = p->in[0].dt;
   a.num_splits = at.splits;
   a.workspace = ctx.workspace_binding.data;
@@ -227,6 +233,8 @@ Status FusedQkvKernel(const KernelContext& ctx) noexcept {
   a.head_dim = at.d;
   a.capacity = at.cap;
   a.dtype = p->in[0].dt;
+  a.rows = p->in[0].rank > 1 ? p->in[0].d[0] : 1;
+  a.cache_batch_stride = at.cbs;
   return FromC(am_gfx950_fused_qkv(&a, StreamOf(ctx)));
 }
 
@@ -235,7 +243,8 @@ Status FusedLinearAddKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
   AM_RETURN_IF_ERROR(NeedArgs(p, 1, 1, "FusedLinearAdd"));
   if (W(ctx) == nullptr) return Status::InvalidArgument("FusedLinearAdd requires packed weights");
-  am_gfx950_fused_linear_residual_args a{p->in[0].p, *W(ctx), p->out[0].p, p->out[0].dt};
+  am_gfx950_fused_linear_residual_args a{p->in[0].p, *W(ctx), p->out[0].p, p->out[0].dt,
+                                         p->in[0].rank > 1 ? p->in[0].d[0] : 1};
   return FromC(am_gfx950_fused_linear_residual(&a, StreamOf(ctx)));
 }
 
@@ -245,7 +254,8 @@ Status FusedGateUpKernel(const KernelContext& ctx) noexcept {
   AM_RETURN_IF_ERROR(NeedArgs(p, 2, 1, "FusedRmsNormGateUpSiluMul"));
   NormAttrs at{};
   if (!ReadAttrs(ctx, &at) || W(ctx) == nullptr) return Status::InvalidArgument("FusedGateUp: attrs/weights missing");
-  am_gfx950_fused_gate_up_args a{p->in[0].p, p->in[1].p, at.eps, *W(ctx), p->out[0].p, p->in[0].dt};
+  am_gfx950_fused_gate_up_args a{p->in[0].p, p->in[1].p, at.eps, *W(ctx), p->out[0].p, p->in[0].dt,
+                                 p->in[0].rank > 1 ? p->in[0].d[0] : 1};
   return FromC(am_gfx950_fused_gate_up(&a, StreamOf(ctx)));
 }
 
@@ -268,8 +278,10 @@ Status FusedLmHeadKernel(const KernelContext& ctx) noexcept {
     a.tokens_hist = static_cast<int64_t*>(p->out[2].p);
     a.pos = static_cast<int64_t*>(p->out[3].p);
     a.step = static_cast<int64_t*>(p->out[4].p);
+    a.hist_stride = p->out[2].rank > 1 ? p->out[2].d[1] : 0;
   }
   a.dtype = p->in[0].dt;
+  a.rows = p->in[0].rank > 1 ? p->in[0].d[0] : 1;
   return FromC(am_gfx950_fused_lm_head(&a, StreamOf(ctx)));
 }
 

@@ -33,8 +33,10 @@ Status BuildGfxParams(std::span<const TensorView> inputs, std::span<const Mutabl
 struct NormAttrs { float eps; };
 struct RopeAttrs { int64_t hq, hkv, d, max_pos; };
 struct KvAttrs { int64_t hkv, d, cap; };
-struct AttnAttrs { int64_t hq, hkv, d, cap; int32_t splits; };
-struct QkvAttrs { float eps; int64_t hq, hkv, d, cap; };
+// batch > 1: q holds batch sequences of seq/batch rows each; sequence r's cache planes
+// start cbs elements after sequence r-1's (cbs is the same batch stride for QkvAttrs).
+struct AttnAttrs { int64_t hq, hkv, d, cap; int32_t splits; int64_t batch, cbs; };
+struct QkvAttrs { float eps; int64_t hq, hkv, d, cap, cbs; };
 
 template <typename T>
 std::vector<std::byte> PackAttrs(const T& v) {

@@ -258,6 +258,24 @@ class LlamaModel {
 };
 
 // ------------------------------------------------------------------ session
+// KV planes of the session's sequences come from one allocation: the reference
+// KVCacheManager (one reservation each, kv_cache_manager.cpp:49-126) allocates its key
+// then value plane through this allocator, which hands sequence r the r-th slot of a
+// key region and of a value region, so every sequence's planes sit a fixed stride
+// apart (the batch stride of the batched decode kernels).
+struct KvSlotAllocator {
+  char* key = nullptr;
+  char* value = nullptr;
+  size_t slot_bytes = 0;
+  int next = 0;
+  static void* Alloc(size_t bytes, void* user) {
+    auto* a = static_cast<KvSlotAllocator*>(user);
+    if (bytes > a->slot_bytes || a->next > 1) return nullptr;
+    return a->next++ == 0 ? a->key : a->value;
+  }
+  static void Free(void*, void*) {}
+};
+
 class LlamaSession {
  public:
   LlamaModel* m = nullptr;
@@ -265,9 +283,15 @@ class LlamaSession {
   std::unique_ptr<HipStream> hs;
   BackendRegistry backends;
   Backend* backend = nullptr;
-  KVCacheManager kv;
-  KVCacheView view;
-  am_session_options opt{1, 1};
+  am_session_options opt{1, 1, 1};
+  int64_t B = 1;  // sequences decoded together
+
+  // KV: one reference KVCacheManager per sequence, planes in kv_slab
+  void* kv_slab = nullptr;
+  int64_t kv_row_elems = 0;  // elements between sequence r and r+1's planes
+  std::vector<std::unique_ptr<KvSlotAllocator>> kv_alloc;
+  std::vector<std::unique_ptr<KVCacheManager>> kvs;
+  std::vector<KVCacheView> views;
 
   // device buffers
   void* act_slab = nullptr;
@@ -275,9 +299,9 @@ class LlamaSession {
   int64_t* positions = nullptr;
   void *h = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *tmp = nullptr;
   void *gate = nullptr, *up = nullptr, *act = nullptr;
-  float* logits = nullptr;
-  int64_t* state = nullptr;  // [0] token, [1] pos, [2] step, [3..] unused
-  int64_t* hist = nullptr;   // [max_tokens]
+  float* logits = nullptr;   // [B][vocab]
+  int64_t* state = nullptr;  // token[B], pos[B], step
+  int64_t* hist = nullptr;   // [B][max_tokens + 1]
   int32_t* err = nullptr;
   void* attn_ws = nullptr;
   size_t attn_ws_bytes = 0;
@@ -290,41 +314,69 @@ class LlamaSession {
   RuntimeBindingContext decode_bind;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
-  int64_t host_pos = 0;   // mirrors state[1] after each host-visible sync point
-  int64_t host_step = 0;  // number of tokens generated in the current sequence
+  std::vector<int64_t> row_pos;     // host mirror of pos[r] after each host-visible sync point
+  std::vector<uint8_t> row_ready;   // sequence r has been prefilled
+  int64_t host_step = 0;            // decode steps since the last prefill (shared by all rows)
 
   ~LlamaSession() {
     if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
     if (graph) (void)hipGraphDestroy(graph);
+    views.clear();
+    kvs.clear();
+    if (kv_slab) (void)hipFree(kv_slab);
     if (act_slab) (void)hipFree(act_slab);
   }
 
-  int64_t* token_ptr() const { return state; }
-  int64_t* pos_ptr() const { return state + 1; }
-  int64_t* step_ptr() const { return state + 2; }
+  int64_t HistStride() const { return static_cast<int64_t>(m->cfg.max_tokens) + 1; }
+  int64_t* token_ptr(int64_t r = 0) const { return state + r; }
+  int64_t* pos_ptr(int64_t r = 0) const { return state + B + r; }
+  int64_t* step_ptr() const { return state + 2 * B; }
+  int64_t* hist_ptr(int64_t r = 0) const { return hist + r * HistStride(); }
+  int64_t host_pos() const { return row_pos.empty() ? 0 : row_pos[0]; }
 
   Status Init(LlamaModel* model, const am_session_options* o) {
     m = model;
     stream = model->stream;
     hs = std::make_unique<HipStream>(stream);
     if (o) opt = *o;
+    B = opt.batch > 1 ? opt.batch : 1;
+    const auto& c = m->cfg;
+    if (B > 16) return Status::InvalidArgument("session batch must be 1..16");
+    if (B > 1 && (!opt.fused_decode || c.act_dtype != AM_DT_BF16 || c.weight_format == AM_WF_F32))
+      return Status::Unimplemented("batched decode needs the fused plan, bf16 activations and bf16/int8/int4 weights");
     AM_RETURN_IF_ERROR(backends.RegisterFactory(std::make_unique<gfx950::Gfx950BackendFactory>()));
     auto b = backends.GetBackend(DeviceType::kHIP);
     if (!b.ok()) return b.status();
     backend = b.value();
     (void)am::DeviceCUs();
 
-    const auto& c = m->cfg;
-    AM_RETURN_IF_ERROR(kv.Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype)));
-    auto vw = kv.ReserveForSession(0, static_cast<size_t>(c.max_tokens));
-    if (!vw.ok()) return vw.status();
-    view = vw.value();
+    // KV: B reservations of max_tokens positions, planes a fixed stride apart
+    const size_t eb = ActBytes(c.act_dtype);
+    const size_t plane = static_cast<size_t>(c.num_layers) * c.num_kv_heads * c.max_tokens * c.head_dim * eb;
+    const size_t slot = (plane + 255) & ~size_t{255};
+    AM_HIP_OK(hipMalloc(&kv_slab, 2 * slot * static_cast<size_t>(B)));
+    kv_row_elems = static_cast<int64_t>(slot / eb);
+    for (int64_t r = 0; r < B; ++r) {
+      auto a = std::make_unique<KvSlotAllocator>();
+      a->key = static_cast<char*>(kv_slab) + static_cast<size_t>(r) * slot;
+      a->value = static_cast<char*>(kv_slab) + static_cast<size_t>(B + r) * slot;
+      a->slot_bytes = slot;
+      auto mgr = std::make_unique<KVCacheManager>(DeviceAllocator{&KvSlotAllocator::Alloc, &KvSlotAllocator::Free, a.get()});
+      AM_RETURN_IF_ERROR(mgr->Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype)));
+      auto vw = mgr->ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+      if (!vw.ok()) return vw.status();
+      views.push_back(vw.value());
+      kvs.push_back(std::move(mgr));
+      kv_alloc.push_back(std::move(a));
+    }
+    row_pos.assign(static_cast<size_t>(B), 0);
+    row_ready.assign(static_cast<size_t>(B), 0);
 
-    const int64_t S = c.max_prefill_chunk, H = c.hidden, F = c.ffn;
+    const int64_t S = std::max<int64_t>(c.max_prefill_chunk, B), H = c.hidden, F = c.ffn;
     const size_t ab = ActBytes(c.act_dtype);
     attn_ws_bytes = static_cast<size_t>(std::max(
         am_gfx950_attention_workspace_bytes(1, S, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0),
-        am_gfx950_attention_workspace_bytes(1, 1, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0)));
+        am_gfx950_attention_workspace_bytes(B, 1, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0)));
     am_ws_bytes = am_gfx950_argmax_workspace_bytes(1);
     const size_t sizes[] = {
         static_cast<size_t>(S) * 8,                   // ids
@@ -339,9 +391,9 @@ class LlamaSession {
         static_cast<size_t>(S * F) * ab,              // gate
         static_cast<size_t>(S * F) * ab,              // up
         static_cast<size_t>(S * F) * ab,              // act
-        static_cast<size_t>(c.vocab) * 4,             // logits
-        64,                                           // state
-        static_cast<size_t>(c.max_tokens + 1) * 8,    // hist
+        static_cast<size_t>(B * c.vocab) * 4,         // logits
+        static_cast<size_t>(2 * B + 1) * 8,           // state
+        static_cast<size_t>(B * HistStride()) * 8,    // hist
         64,                                           // err
         attn_ws_bytes,                                // attention workspace
         static_cast<size_t>(am_gfx950_lm_head_workspace_bytes()),
@@ -407,15 +459,15 @@ class LlamaSession {
     return HipSelector(a, a, WeightFormat::kPlain, ph);
   }
 
-  // Unfused per-layer body (reference node order) for `S` rows starting at device
-  // position *start (positions[] holds per-row positions).
+  // Unfused per-layer body (reference node order) for `S` rows of sequence `row`
+  // starting at device position *start (positions[] holds per-row positions).
   Status AddLayerUnfused(Builder& b, int64_t l, int64_t S, ExecPhase ph, const int64_t* pos_rows,
-                         const int64_t* start) {
+                         const int64_t* start, int64_t row) {
     const auto& c = m->cfg;
     const DataType A = ActType(c.act_dtype);
     const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, Q = m->QRows(), KV = m->KvRows();
-    auto kp = view.KeyPlane(static_cast<size_t>(l));
-    auto vp = view.ValuePlane(static_cast<size_t>(l));
+    auto kp = views[static_cast<size_t>(row)].KeyPlane(static_cast<size_t>(l));
+    auto vp = views[static_cast<size_t>(row)].ValuePlane(static_cast<size_t>(l));
     if (!kp.ok()) return kp.status();
     if (!vp.ok()) return vp.status();
     const gfx950::NormAttrs na{c.rms_eps};
@@ -440,7 +492,7 @@ class LlamaSession {
                              {TensorView(k, A, {S, KV}), TensorView(v, A, {S, KV}), kplane, vplane,
                               TensorView(start, DataType::Int(64), {1})},
                              {}));
-    const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0};
+    const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, 1, 0};
     AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
                              {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},
                              {MutableTensorView(attn, A, {S, Q})}, attn_ws_bytes));
@@ -463,27 +515,28 @@ class LlamaSession {
   }
 
   // RmsNorm(final) -> Linear lm_head (fp32 logits) -> Argmax (+ advance decode state)
-  // on the row `row` of h.
-  Status AddHeadUnfused(Builder& b, int64_t row, ExecPhase ph) {
+  // on the row `hrow` of h, for sequence `row`.
+  Status AddHeadUnfused(Builder& b, int64_t hrow, ExecPhase ph, int64_t row) {
     const auto& c = m->cfg;
     const DataType A = ActType(c.act_dtype);
     const int64_t H = c.hidden;
     const size_t ab = ActBytes(c.act_dtype);
-    void* hrow = static_cast<char*>(h) + static_cast<size_t>(row * H) * ab;
+    void* hr = static_cast<char*>(h) + static_cast<size_t>(hrow * H) * ab;
+    float* lg = logits + row * c.vocab;
     const gfx950::NormAttrs na{c.rms_eps};
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
-                             {TensorView(hrow, A, {1, H}), TensorView(m->final_norm, A, {H})},
+                             {TensorView(hr, A, {1, H}), TensorView(m->final_norm, A, {H})},
                              {MutableTensorView(xn, A, {1, H})}));
     // lm_head GEMV for one row (decode-phase kernel: GEMV) with fp32 logits out.
     AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ExecPhase::kDecode), &m->lm_head,
                              {TensorView(xn, A, {1, H})},
-                             {MutableTensorView(logits, DataType::Float32(), {1, c.vocab})}));
+                             {MutableTensorView(lg, DataType::Float32(), {1, c.vocab})}));
     AM_RETURN_IF_ERROR(b.Add(OpType::kArgmax, {}, Sel(false, ph), nullptr,
-                             {TensorView(logits, DataType::Float32(), {1, c.vocab}),
+                             {TensorView(lg, DataType::Float32(), {1, c.vocab}),
                               TensorView(am_ws, DataType::UInt(8), {am_ws_bytes})},
-                             {MutableTensorView(token_ptr(), DataType::Int(64), {1}),
-                              MutableTensorView(hist, DataType::Int(64), {c.max_tokens}),
-                              MutableTensorView(pos_ptr(), DataType::Int(64), {1}),
+                             {MutableTensorView(token_ptr(row), DataType::Int(64), {1}),
+                              MutableTensorView(hist_ptr(row), DataType::Int(64), {c.max_tokens}),
+                              MutableTensorView(pos_ptr(row), DataType::Int(64), {1}),
                               MutableTensorView(step_ptr(), DataType::Int(64), {1})}));
     return Status::Ok();
   }
@@ -506,6 +559,9 @@ class LlamaSession {
     }
   }
 
+  // Decode plan for the B sequences: one token of each per step.  B > 1 runs the
+  // batched forms of the fused kernels (rows = B, per-row positions, sequence r's KV
+  // planes kv_row_elems after sequence r-1's).
   Status BuildDecodePlan() {
     MakeViews();
     const auto& c = m->cfg;
@@ -514,53 +570,60 @@ class LlamaSession {
     decode_bind.ClearStepTensorBindings();
     Builder b{this, ExecPhase::kDecode, {}, &decode_bind};
     const auto ph = ExecPhase::kDecode;
-    AM_RETURN_IF_ERROR(b.Add(OpType::kEmbedToken, {}, Sel(false, ph), nullptr,
-                             {TensorView(token_ptr(), DataType::Int(64), {1}), TensorView(m->embed, A, {c.vocab, H}),
-                              TensorView(err, DataType::Int(32), {1})},
-                             {MutableTensorView(h, A, {1, H})}));
+    if (B == 1) {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kEmbedToken, {}, Sel(false, ph), nullptr,
+                               {TensorView(token_ptr(), DataType::Int(64), {1}), TensorView(m->embed, A, {c.vocab, H}),
+                                TensorView(err, DataType::Int(32), {1})},
+                               {MutableTensorView(h, A, {1, H})}));
+    } else {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kEmbedding, {}, Sel(false, ph), nullptr,
+                               {TensorView(token_ptr(), DataType::Int(64), {B}), TensorView(m->embed, A, {c.vocab, H}),
+                                TensorView(err, DataType::Int(32), {1})},
+                               {MutableTensorView(h, A, {B, H})}));
+    }
     for (int64_t l = 0; l < c.num_layers; ++l) {
       if (!opt.fused_decode) {
-        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, 1, ph, pos_ptr(), pos_ptr()));
+        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, 1, ph, pos_ptr(), pos_ptr(), 0));
         continue;
       }
-      auto kp = view.KeyPlane(static_cast<size_t>(l));
-      auto vp = view.ValuePlane(static_cast<size_t>(l));
+      auto kp = views[0].KeyPlane(static_cast<size_t>(l));
+      auto vp = views[0].ValuePlane(static_cast<size_t>(l));
       if (!kp.ok()) return kp.status();
       if (!vp.ok()) return vp.status();
       const TensorView kplane(kp.value(), A, {c.num_kv_heads, c.max_tokens, d});
       const TensorView vplane(vp.value(), A, {c.num_kv_heads, c.max_tokens, d});
-      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
+      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens, kv_row_elems};
       AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormQkvRoPEKVUpdate, PackAttrs(qa), Sel(true, ph), &m->qkv[l],
-                               {TensorView(h, A, {1, H}), TensorView(m->in_norm[l], A, {H}),
-                                TensorView(pos_ptr(), DataType::Int(64), {1}),
+                               {TensorView(h, A, {B, H}), TensorView(m->in_norm[l], A, {H}),
+                                TensorView(pos_ptr(), DataType::Int(64), {B}),
                                 TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
                                 TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2}), kplane, vplane},
-                               {MutableTensorView(q, A, {1, Q})}));
-      const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0};
+                               {MutableTensorView(q, A, {B, Q})}));
+      const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, B, kv_row_elems};
       AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
-                               {TensorView(q, A, {1, Q}), kplane, vplane, TensorView(pos_ptr(), DataType::Int(64), {1})},
-                               {MutableTensorView(attn, A, {1, Q})}, attn_ws_bytes));
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {1, Q})},
-                               {MutableTensorView(h, A, {1, H})}));
+                               {TensorView(q, A, {B, Q}), kplane, vplane, TensorView(pos_ptr(), DataType::Int(64), {B})},
+                               {MutableTensorView(attn, A, {B, Q})}, attn_ws_bytes));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {B, Q})},
+                               {MutableTensorView(h, A, {B, H})}));
       const gfx950::NormAttrs na{c.rms_eps};
       AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormGateUpSiluMul, PackAttrs(na), Sel(true, ph), &m->gate_up[l],
-                               {TensorView(h, A, {1, H}), TensorView(m->post_norm[l], A, {H})},
-                               {MutableTensorView(act, A, {1, F})}));
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {1, F})},
-                               {MutableTensorView(h, A, {1, H})}));
+                               {TensorView(h, A, {B, H}), TensorView(m->post_norm[l], A, {H})},
+                               {MutableTensorView(act, A, {B, F})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {B, F})},
+                               {MutableTensorView(h, A, {B, H})}));
     }
     if (opt.fused_decode) {
       const gfx950::NormAttrs na{c.rms_eps};
       AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormLmHeadArgmax, PackAttrs(na), Sel(true, ph), &m->lm_head,
-                               {TensorView(h, A, {1, H}), TensorView(m->final_norm, A, {H}),
+                               {TensorView(h, A, {B, H}), TensorView(m->final_norm, A, {H}),
                                 TensorView(lm_ws, DataType::UInt(8), {am_gfx950_lm_head_workspace_bytes()})},
-                               {MutableTensorView(logits, DataType::Float32(), {c.vocab}),
-                                MutableTensorView(token_ptr(), DataType::Int(64), {1}),
-                                MutableTensorView(hist, DataType::Int(64), {c.max_tokens}),
-                                MutableTensorView(pos_ptr(), DataType::Int(64), {1}),
+                               {MutableTensorView(logits, DataType::Float32(), {B, c.vocab}),
+                                MutableTensorView(token_ptr(), DataType::Int(64), {B}),
+                                MutableTensorView(hist, DataType::Int(64), {B, HistStride()}),
+                                MutableTensorView(pos_ptr(), DataType::Int(64), {B}),
                                 MutableTensorView(step_ptr(), DataType::Int(64), {1})}));
     } else {
-      AM_RETURN_IF_ERROR(AddHeadUnfused(b, 0, ph));
+      AM_RETURN_IF_ERROR(AddHeadUnfused(b, 0, ph, 0));
     }
     auto plan = ExecutionPlan::Create(std::move(b.steps));
     if (!plan.ok()) return plan.status();
@@ -569,18 +632,21 @@ class LlamaSession {
   }
 
   // ---------------------------------------------------------------- execution
-  Status Prefill(const int64_t* prompt, int64_t n, int64_t* first_token) {
+  // Prefill sequence `row` from position 0 (its own KV reservation); the other rows
+  // keep their state.  The shared step counter restarts at 1.
+  Status Prefill(int64_t row, const int64_t* prompt, int64_t n, int64_t* first_token) {
     const auto& c = m->cfg;
+    if (row < 0 || row >= B) return Status::OutOfRange("prefill: sequence row out of range");
     if (n <= 0) return Status::InvalidArgument("prompt must contain at least one token");
     if (n + 1 > c.max_tokens) return Status::OutOfRange("KV session reservation exceeds physical KV capacity");
     for (int64_t i = 0; i < n; ++i)
       if (prompt[i] < 0 || prompt[i] >= c.vocab) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
-    AM_RETURN_IF_ERROR(kv.ReleaseSession(view));
-    auto vw = kv.ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+    const size_t ri = static_cast<size_t>(row);
+    AM_RETURN_IF_ERROR(kvs[ri]->ReleaseSession(views[ri]));
+    auto vw = kvs[ri]->ReserveForSession(0, static_cast<size_t>(c.max_tokens));
     if (!vw.ok()) return vw.status();
-    view = vw.value();
-    if (graph_exec) {  // KV planes are unchanged (same slab), the graph stays valid
-    }
+    views[ri] = vw.value();  // same slot planes: the decode plan and graph stay valid
+    row_ready[ri] = 0;
     const int64_t chunk = c.max_prefill_chunk;
     std::vector<int64_t> pos_host(static_cast<size_t>(chunk));
     for (int64_t p0 = 0; p0 < n; p0 += chunk) {
@@ -598,35 +664,55 @@ class LlamaSession {
                                 TensorView(err, DataType::Int(32), {1})},
                                {MutableTensorView(h, A, {S, c.hidden})}));
       for (int64_t l = 0; l < c.num_layers; ++l)
-        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, S, ExecPhase::kPrefill, positions, positions));
+        AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, S, ExecPhase::kPrefill, positions, positions, row));
       const bool last = p0 + S == n;
       if (last) {
         // decode state before the head: pos = n-1, step = 0 (the head advances both)
-        const int64_t st[3] = {0, n - 1, 0};
-        AM_HIP_OK(hipMemcpyAsync(state, st, sizeof(st), hipMemcpyHostToDevice, stream));
-        AM_RETURN_IF_ERROR(AddHeadUnfused(b, S - 1, ExecPhase::kPrefill));
+        const int64_t zero = 0, pm1 = n - 1;
+        AM_HIP_OK(hipMemcpyAsync(token_ptr(row), &zero, 8, hipMemcpyHostToDevice, stream));
+        AM_HIP_OK(hipMemcpyAsync(pos_ptr(row), &pm1, 8, hipMemcpyHostToDevice, stream));
+        AM_HIP_OK(hipMemcpyAsync(step_ptr(), &zero, 8, hipMemcpyHostToDevice, stream));
+        AM_RETURN_IF_ERROR(AddHeadUnfused(b, S - 1, ExecPhase::kPrefill, row));
       }
       auto plan = ExecutionPlan::Create(std::move(b.steps));
       if (!plan.ok()) return plan.status();
       AM_RETURN_IF_ERROR(Executor::Execute(plan.value(), bind));
       AM_HIP_OK(hipStreamSynchronize(stream));  // pos_host / state staging reuse
     }
-    AM_RETURN_IF_ERROR(view.CommitUntil(static_cast<size_t>(n)));
+    AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(n)));
     int64_t tok = 0;
-    AM_HIP_OK(hipMemcpy(&tok, token_ptr(), 8, hipMemcpyDeviceToHost));
+    AM_HIP_OK(hipMemcpy(&tok, token_ptr(row), 8, hipMemcpyDeviceToHost));
     int32_t e = 0;
     AM_HIP_OK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
     if (e != 0) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
-    host_pos = n;
+    row_pos[ri] = n;
+    row_ready[ri] = 1;
     host_step = 1;
     if (first_token) *first_token = tok;
     return Status::Ok();
   }
 
-  Status EnqueueDecode(int64_t n) {
+  Status CheckDecode(int64_t n) const {
     const auto& c = m->cfg;
-    if (host_step == 0) return Status::FailedPrecondition("decode requires a prefilled session");
-    if (host_pos + n > c.max_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
+    for (int64_t r = 0; r < B; ++r) {
+      if (!row_ready[static_cast<size_t>(r)]) return Status::FailedPrecondition("decode requires a prefilled session");
+      if (row_pos[static_cast<size_t>(r)] + n > c.max_tokens)
+        return Status::OutOfRange("KV write exceeds reserved session token capacity");
+    }
+    return Status::Ok();
+  }
+
+  Status Advance(int64_t n) {
+    for (int64_t r = 0; r < B; ++r) {
+      const size_t ri = static_cast<size_t>(r);
+      row_pos[ri] += n;
+      AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(row_pos[ri])));
+    }
+    return Status::Ok();
+  }
+
+  Status EnqueueDecode(int64_t n) {
+    AM_RETURN_IF_ERROR(CheckDecode(n));
     if (opt.use_graph) {
       if (!graph_exec) {
         AM_HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
@@ -645,16 +731,18 @@ class LlamaSession {
     } else {
       for (int64_t i = 0; i < n; ++i) AM_RETURN_IF_ERROR(Executor::Execute(*decode_plan, decode_bind));
     }
-    host_pos += n;
-    AM_RETURN_IF_ERROR(view.CommitUntil(static_cast<size_t>(host_pos)));
-    return Status::Ok();
+    return Advance(n);
   }
 
+  // n decode steps; out (host) receives [B][n] tokens, sequence-major.
   Status Decode(int64_t n, int64_t* out) {
     const int64_t first_step = host_step;
     AM_RETURN_IF_ERROR(EnqueueDecode(n));
     host_step += n;
-    if (out) AM_HIP_OK(hipMemcpyAsync(out, hist + first_step, static_cast<size_t>(n) * 8, hipMemcpyDeviceToHost, stream));
+    if (out)
+      for (int64_t r = 0; r < B; ++r)
+        AM_HIP_OK(hipMemcpyAsync(out + r * n, hist_ptr(r) + first_step, static_cast<size_t>(n) * 8,
+                                 hipMemcpyDeviceToHost, stream));
     AM_HIP_OK(hipStreamSynchronize(stream));
     int32_t e = 0;
     AM_HIP_OK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
@@ -666,8 +754,7 @@ class LlamaSession {
   // session stream.  Weight-GEMV steps are timed with events bound to their single
   // dispatch (hipExtLaunchKernelGGL start/stop), other steps with events around the step.
   Status Profile(int64_t n, double* ms_by_op, int64_t* count_by_op) {
-    if (host_step == 0) return Status::FailedPrecondition("decode requires a prefilled session");
-    if (host_pos + n > m->cfg.max_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
+    AM_RETURN_IF_ERROR(CheckDecode(n));
     const auto& steps = decode_plan->steps();
     std::vector<hipEvent_t> e0(steps.size(), nullptr), e1(steps.size(), nullptr);
     Status st;
@@ -679,7 +766,8 @@ class LlamaSession {
       for (size_t i = 0; i < steps.size() && st.ok(); ++i) {
         const OpType t = steps[i].op->Type();
         const bool gemv = t == OpType::kFusedRmsNormQkvRoPEKVUpdate || t == OpType::kFusedLinearAdd ||
-                          t == OpType::kFusedRmsNormGateUpSiluMul || t == OpType::kFusedRmsNormLmHeadArgmax;
+                          t == OpType::kFusedRmsNormGateUpSiluMul ||
+                          (t == OpType::kFusedRmsNormLmHeadArgmax && B == 1);
         if (gemv) {
           lt = {e0[i], e1[i], false};
           st = LayerRunner::RunStep(i, steps[i], decode_bind);
@@ -716,9 +804,8 @@ class LlamaSession {
       if (e1[i]) (void)hipEventDestroy(e1[i]);
     }
     if (st.ok()) {
-      host_pos += n;
       host_step += n;
-      st = view.CommitUntil(static_cast<size_t>(host_pos));
+      st = Advance(n);
     }
     return st;
   }
@@ -882,8 +969,16 @@ void am_session_destroy(am_session* s) {
 
 am_status_code am_session_prefill(am_session* s, const int64_t* prompt, int64_t n, int64_t* first_token) {
   if (!s || !prompt) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "prefill: null argument");
-  return Ret(s->impl->Prefill(prompt, n, first_token));
+  return Ret(s->impl->Prefill(0, prompt, n, first_token));
 }
+
+am_status_code am_session_prefill_row(am_session* s, int64_t row, const int64_t* prompt, int64_t n,
+                                      int64_t* first_token) {
+  if (!s || !prompt) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "prefill_row: null argument");
+  return Ret(s->impl->Prefill(row, prompt, n, first_token));
+}
+
+int64_t am_session_batch(am_session* s) { return s ? s->impl->B : 0; }
 
 am_status_code am_session_decode(am_session* s, int64_t n, int64_t* tokens_out) {
   if (!s || n < 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "decode: bad argument");
@@ -901,8 +996,9 @@ am_status_code am_session_decode_async(am_session* s, int64_t n) {
 am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new, int64_t eos,
                                    int64_t* tokens_out, int64_t* n_out) {
   if (!s || !prompt || !tokens_out || max_new <= 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "generate: bad argument");
+  if (s->impl->B != 1) return am::SetLastError(AM_STATUS_UNIMPLEMENTED, "generate: single-sequence sessions only");
   int64_t first = 0;
-  Status st = s->impl->Prefill(prompt, n_prompt, &first);
+  Status st = s->impl->Prefill(0, prompt, n_prompt, &first);
   if (!st.ok()) return Ret(st);
   tokens_out[0] = first;
   int64_t produced = 1;
@@ -930,12 +1026,17 @@ am_status_code am_session_logits(am_session* s, float* out) {
   if (!s || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "logits: null argument");
   auto& S = *s->impl;
   if (hipStreamSynchronize(S.stream) != hipSuccess ||
-      hipMemcpy(out, S.logits, static_cast<size_t>(S.m->cfg.vocab) * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      hipMemcpy(out, S.logits, static_cast<size_t>(S.B * S.m->cfg.vocab) * 4, hipMemcpyDeviceToHost) != hipSuccess)
     return am::SetLastError(AM_STATUS_INTERNAL, "logits copy failed");
   return AM_STATUS_OK;
 }
 
-int64_t am_session_position(am_session* s) { return s ? s->impl->host_pos : -1; }
+int64_t am_session_position(am_session* s) { return s ? s->impl->host_pos() : -1; }
+
+int64_t am_session_row_position(am_session* s, int64_t row) {
+  if (!s || row < 0 || row >= s->impl->B) return -1;
+  return s->impl->row_pos[static_cast<size_t>(row)];
+}
 
 int64_t am_session_decode_plan_size(am_session* s) {
   return s && s->impl->decode_plan ? static_cast<int64_t>(s->impl->decode_plan->size()) : 0;

@@ -28,6 +28,15 @@ inline int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Number of compute units of the current device (cached per device).
 int DeviceCUs();
 
+// Batched decode GEMV (gemv_batch.hip): 1..16 token rows share one weight read.
+bool BatchLinearEligible(int32_t act, const am_gfx950_weight& w, int64_t m, const void* x);
+am_status_code BatchLinear(const void* x, int64_t m, const am_gfx950_weight& w, void* out, int32_t out_dtype,
+                           const void* residual, hipStream_t s);
+am_status_code BatchQkv(const am_gfx950_fused_qkv_args* a, hipStream_t s);
+am_status_code BatchLinearResidual(const am_gfx950_fused_linear_residual_args* a, hipStream_t s);
+am_status_code BatchGateUp(const am_gfx950_fused_gate_up_args* a, hipStream_t s);
+am_status_code BatchNormLogits(const am_gfx950_fused_lm_head_args* a, hipStream_t s);
+
 // ---- device: numeric helpers ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

@@ -341,6 +341,8 @@ extern "C" am_status_code am_gfx950_linear(const am_gfx950_linear_args* a, void*
   const bool gemm_ok = a->x_dtype == AM_DT_BF16 && w.format != AM_WF_F32 && w.k % BK == 0 &&
                        (w.format != AM_WF_INT4 || (w.group_size % BK == 0 && w.k % w.group_size == 0)) &&
                        (reinterpret_cast<uintptr_t>(a->x) & 15u) == 0;
+  if (a->mode == 3 || (a->mode == 0 && a->m >= 2 && BatchLinearEligible(a->x_dtype, w, a->m, a->x)))
+    return BatchLinear(a->x, a->m, w, a->out, a->out_dtype, a->residual, s);
   const bool use_gemm = a->mode == 2 || (a->mode == 0 && a->m > 8 && gemm_ok);
   if (use_gemm) {
     AM_CHECK_ARG(gemm_ok, "linear: MFMA GEMM needs bf16 activations, bf16/int8/int4 weights, K % 128 == 0");

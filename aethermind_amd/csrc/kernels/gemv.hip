@@ -1147,6 +1147,7 @@ using namespace am;
 
 extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a, void* stream) {
   AM_CHECK_ARG(a != nullptr, "fused_qkv: null args");
+  AM_CHECK_ARG(a->rows >= 0, "fused_qkv: negative rows");
   if (auto st = ValidateWeight(a->w_qkv); st != AM_STATUS_OK) return st;
   AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_qkv: dtype");
   AM_CHECK_ARG(a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0 && a->head_dim > 0 && a->head_dim % 2 == 0,
@@ -1157,6 +1158,7 @@ extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a,
   AM_CHECK_ARG(a->h && a->norm_w && a->cos_tab && a->sin_tab && a->pos && a->q_out && a->k_cache && a->v_cache,
                "fused_qkv: null pointer");
   AM_CHECK_ARG(a->eps > 0.0f, "fused_qkv: eps must be positive");
+  if (a->rows > 1) return BatchQkv(a, AsStream(stream));
   GemvArgs g = BaseArgs(a->w_qkv);
   g.units = a->w_qkv.n / 2;
   g.x = a->h;
@@ -1181,6 +1183,8 @@ extern "C" am_status_code am_gfx950_fused_linear_residual(const am_gfx950_fused_
   if (auto st = ValidateWeight(a->w); st != AM_STATUS_OK) return st;
   AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_linear_residual: dtype");
   AM_CHECK_ARG(a->x && a->h, "fused_linear_residual: null pointer");
+  AM_CHECK_ARG(a->rows >= 0, "fused_linear_residual: negative rows");
+  if (a->rows > 1) return BatchLinearResidual(a, AsStream(stream));
   GemvArgs g = BaseArgs(a->w);
   g.x = a->x;
   g.out = a->h;
@@ -1194,6 +1198,8 @@ extern "C" am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_
   AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "fused_gate_up: dtype");
   AM_CHECK_ARG(a->w_gate_up.n % 2 == 0, "fused_gate_up: gate/up weight needs an even row count");
   AM_CHECK_ARG(a->h && a->norm_w && a->act_out && a->eps > 0.0f, "fused_gate_up: bad pointer/eps");
+  AM_CHECK_ARG(a->rows >= 0, "fused_gate_up: negative rows");
+  if (a->rows > 1) return BatchGateUp(a, AsStream(stream));
   GemvArgs g = BaseArgs(a->w_gate_up);
   g.x = a->h;
   g.norm_w = a->norm_w;
@@ -1215,6 +1221,26 @@ extern "C" am_status_code am_gfx950_fused_lm_head(const am_gfx950_fused_lm_head_
   AM_CHECK_ARG(a->workspace_bytes >= am_gfx950_lm_head_workspace_bytes(), "fused_lm_head: workspace too small");
   AM_CHECK_ARG(a->tokens_hist == nullptr || (a->pos != nullptr && a->step != nullptr),
                "fused_lm_head: tokens_hist needs pos and step");
+  AM_CHECK_ARG(a->rows >= 0, "fused_lm_head: negative rows");
+  if (a->rows > 1) {
+    // batched rows: RMSNorm + logits on the batched GEMV, then per-row argmax and the
+    // decode-state update
+    hipStream_t s = AsStream(stream);
+    AM_CHECK_ARG(a->tokens_hist == nullptr || a->hist_stride > 0, "fused_lm_head: batched rows need hist_stride");
+    if (auto st = BatchNormLogits(a, s); st != AM_STATUS_OK) return st;
+    am_gfx950_argmax_args am{};
+    am.x = a->logits;
+    am.dtype = AM_DT_F32;
+    am.rows = a->rows;
+    am.n = a->w.n;
+    am.out = a->token_out;
+    am.workspace = a->workspace;
+    am.workspace_bytes = a->workspace_bytes;
+    if (auto st = am_gfx950_argmax(&am, stream); st != AM_STATUS_OK) return st;
+    if (a->pos == nullptr) return AM_STATUS_OK;
+    return am_gfx950_decode_advance_rows(a->token_out, a->rows, a->tokens_hist, a->hist_stride, a->pos, a->step,
+                                         stream);
+  }
   GemvArgs g = BaseArgs(a->w);
   g.x = a->h;
   g.norm_w = a->norm_w;

@@ -471,6 +471,18 @@ __global__ void decode_advance_kernel(const int64_t* token, int64_t* hist, int64
     *pos = *pos + 1;
   }
 }
+
+// one thread per row; the shared step is read by every row before thread 0 bumps it
+__global__ void decode_advance_rows_kernel(const int64_t* token, int64_t rows, int64_t* hist, int64_t hist_stride,
+                                           int64_t* pos, int64_t* step) {
+  const int64_t st = *step;
+  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) {
+    if (hist != nullptr) hist[r * hist_stride + st] = token[r];
+    pos[r] = pos[r] + 1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *step = st + 1;
+}
 }  // namespace
 }  // namespace am
 
@@ -479,5 +491,17 @@ extern "C" am_status_code am_gfx950_decode_advance(const int64_t* token, int64_t
   AM_CHECK_ARG(token && pos && step, "decode_advance: null pointer");
   hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, AsStream(stream), token, tokens_hist, pos, step);
   AM_RETURN_IF_LAUNCH_FAILED("decode_advance");
+  return AM_STATUS_OK;
+}
+
+extern "C" am_status_code am_gfx950_decode_advance_rows(const int64_t* token, int64_t rows, int64_t* tokens_hist,
+                                                        int64_t hist_stride, int64_t* pos, int64_t* step,
+                                                        void* stream) {
+  AM_CHECK_ARG(token && pos && step, "decode_advance_rows: null pointer");
+  AM_CHECK_ARG(rows >= 1 && rows <= 65536, "decode_advance_rows: rows must be 1..65536");
+  AM_CHECK_ARG(tokens_hist == nullptr || hist_stride > 0, "decode_advance_rows: hist_stride must be positive");
+  hipLaunchKernelGGL(decode_advance_rows_kernel, dim3(1), dim3(256), 0, AsStream(stream), token, rows, tokens_hist,
+                     hist_stride, pos, step);
+  AM_RETURN_IF_LAUNCH_FAILED("decode_advance_rows");
   return AM_STATUS_OK;
 }

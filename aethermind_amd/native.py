@@ -94,21 +94,22 @@ class SynthArgs(C.Structure):
 class FusedQkvArgs(C.Structure):
     _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_qkv", Weight), ("cos_tab", vp), ("sin_tab", vp),
                 ("pos", vp), ("q_out", vp), ("k_cache", vp), ("v_cache", vp), ("hq", i64), ("hkv", i64),
-                ("head_dim", i64), ("capacity", i64), ("dtype", i32)]
+                ("head_dim", i64), ("capacity", i64), ("dtype", i32), ("rows", i64), ("cache_batch_stride", i64)]
 
 
 class FusedLinearResidualArgs(C.Structure):
-    _fields_ = [("x", vp), ("w", Weight), ("h", vp), ("dtype", i32)]
+    _fields_ = [("x", vp), ("w", Weight), ("h", vp), ("dtype", i32), ("rows", i64)]
 
 
 class FusedGateUpArgs(C.Structure):
-    _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_gate_up", Weight), ("act_out", vp), ("dtype", i32)]
+    _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_gate_up", Weight), ("act_out", vp), ("dtype", i32),
+                ("rows", i64)]
 
 
 class FusedLmHeadArgs(C.Structure):
     _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w", Weight), ("logits", vp), ("token_out", vp),
                 ("tokens_hist", vp), ("pos", vp), ("step", vp), ("dtype", i32), ("workspace", vp),
-                ("workspace_bytes", i64)]
+                ("workspace_bytes", i64), ("rows", i64), ("hist_stride", i64)]
 
 
 class ModelConfig(C.Structure):
@@ -119,7 +120,7 @@ class ModelConfig(C.Structure):
 
 
 class SessionOptions(C.Structure):
-    _fields_ = [("fused_decode", i32), ("use_graph", i32)]
+    _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32)]
 
 
 _SIGS = {
@@ -158,6 +159,7 @@ _SIGS = {
     "am_gfx950_fused_lm_head": (i32, [C.POINTER(FusedLmHeadArgs), vp]),
     "am_gfx950_lm_head_workspace_bytes": (i64, []),
     "am_gfx950_decode_advance": (i32, [vp, vp, vp, vp, vp]),
+    "am_gfx950_decode_advance_rows": (i32, [vp, i64, vp, i64, vp, vp, vp]),
     "am_runtime_create": (i32, [i32, C.POINTER(vp)]),
     "am_runtime_destroy": (None, [vp]),
     "am_runtime_stream": (vp, [vp]),
@@ -171,6 +173,9 @@ _SIGS = {
     "am_session_create": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
     "am_session_destroy": (None, [vp]),
     "am_session_prefill": (i32, [vp, vp, i64, C.POINTER(i64)]),
+    "am_session_prefill_row": (i32, [vp, i64, vp, i64, C.POINTER(i64)]),
+    "am_session_batch": (i64, [vp]),
+    "am_session_row_position": (i64, [vp, i64]),
     "am_session_decode": (i32, [vp, i64, vp]),
     "am_session_decode_async": (i32, [vp, i64]),
     "am_session_generate": (i32, [vp, vp, i64, i64, i64, vp, C.POINTER(i64)]),

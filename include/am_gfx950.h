@@ -101,7 +101,10 @@ am_status_code am_gfx950_rmsnorm(const am_gfx950_rmsnorm_args* args, void* hip_s
 /* OpType::kLinear (linear_op.h:87-92): out[m,:] = x[m,:] @ W^T (+ residual[m,:]).
  * fp32 accumulation; out rounded once to out_dtype, and with a residual the sum is
  * rounded again (two op boundaries: Linear then Add).  residual may alias out.
- * mode: 0 auto (m <= 8 -> GEMV, else MFMA GEMM), 1 GEMV, 2 GEMM. */
+ * mode: 0 auto (bf16 activations with 2 <= m <= 16 -> batched decode GEMV when the
+ * weight format allows it; otherwise m <= 8 -> GEMV, else MFMA GEMM), 1 GEMV per row,
+ * 2 GEMM, 3 batched decode GEMV (m <= 16, bf16 activations, bf16/int8 weights or
+ * int4 with group 128). */
 typedef struct am_gfx950_linear_args {
   const void* x;
   int32_t x_dtype;
@@ -283,8 +286,11 @@ am_status_code am_gfx950_fill(void* out, int32_t dtype, int64_t n, float value,
 /* ---------------- fused decode kernels (fusion of reference node runs) ------------- */
 
 /* RmsNorm(input_layernorm) -> Linear q|k|v (one concatenated weight, rows q then k
- * then v) -> RoPE(q, k) -> KVCacheUpdate(k_rope, v), for m = 1 token at position
- * *pos (device).  Rounds at every reference op boundary. */
+ * then v) -> RoPE(q, k) -> KVCacheUpdate(k_rope, v), for one token at position *pos
+ * (device).  Rounds at every reference op boundary.
+ * rows > 1 (up to 16, bf16 activations): one token of each of `rows` independent
+ * sequences: h [rows][hidden], pos [rows], q_out [rows][hq*d], and sequence r's cache
+ * planes start cache_batch_stride elements after sequence r-1's.  rows 0 means 1. */
 typedef struct am_gfx950_fused_qkv_args {
   const void* h;
   const void* norm_w;
@@ -298,21 +304,26 @@ typedef struct am_gfx950_fused_qkv_args {
   void* v_cache;
   int64_t hq, hkv, head_dim, capacity;
   int32_t dtype;
+  int64_t rows;
+  int64_t cache_batch_stride;
 } am_gfx950_fused_qkv_args;
 am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* args, void* hip_stream);
 
-/* Linear (x @ W^T) -> Add(residual): h = round(h + round(W x)), in place on h. */
+/* Linear (x @ W^T) -> Add(residual): h = round(h + round(W x)), in place on h.
+ * rows > 1 (up to 16, bf16): x [rows][k], h [rows][n].  rows 0 means 1. */
 typedef struct am_gfx950_fused_linear_residual_args {
   const void* x;
   am_gfx950_weight w;
   void* h;
   int32_t dtype;
+  int64_t rows;
 } am_gfx950_fused_linear_residual_args;
 am_status_code am_gfx950_fused_linear_residual(const am_gfx950_fused_linear_residual_args* a,
                                                void* hip_stream);
 
 /* RmsNorm(post_attention_layernorm) -> Linear gate, up (one weight: rows [0, F) are
- * gate, rows [F, 2F) are up) -> SiluMul. */
+ * gate, rows [F, 2F) are up) -> SiluMul.
+ * rows > 1 (up to 16, bf16): h [rows][hidden], act_out [rows][F].  rows 0 means 1. */
 typedef struct am_gfx950_fused_gate_up_args {
   const void* h;
   const void* norm_w;
@@ -320,6 +331,7 @@ typedef struct am_gfx950_fused_gate_up_args {
   am_gfx950_weight w_gate_up;
   void* act_out;
   int32_t dtype;
+  int64_t rows;
 } am_gfx950_fused_gate_up_args;
 am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_args* a, void* hip_stream);
 
@@ -327,7 +339,11 @@ am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_args* a, vo
  * (if non-NULL) and token_out[0]; with tokens_hist != NULL also tokens_hist[*step]
  * = token and increments *pos and *step (device-resident decode state).
  * workspace: am_gfx950_lm_head_workspace_bytes() bytes, first 4 bytes zero before
- * the first call (left zero). */
+ * the first call (left zero).
+ * rows > 1 (up to 16, bf16): h [rows][hidden], logits [rows][vocab] (required),
+ * token_out [rows], pos [rows]; tokens_hist row r starts hist_stride elements after
+ * row r-1 and *step is shared (incremented once).  The first 256 bytes of the
+ * workspace must be zero before the first call (left zero).  rows 0 means 1. */
 typedef struct am_gfx950_fused_lm_head_args {
   const void* h;
   const void* norm_w;
@@ -341,6 +357,8 @@ typedef struct am_gfx950_fused_lm_head_args {
   int32_t dtype;
   void* workspace;
   int64_t workspace_bytes;
+  int64_t rows;
+  int64_t hist_stride;
 } am_gfx950_fused_lm_head_args;
 am_status_code am_gfx950_fused_lm_head(const am_gfx950_fused_lm_head_args* a, void* hip_stream);
 int64_t am_gfx950_lm_head_workspace_bytes(void);
@@ -354,6 +372,13 @@ am_status_code am_gfx950_embed_token(const int64_t* token, const void* table, in
  * ++*step, ++*pos.  The fused lm_head kernel does the same in its epilogue. */
 am_status_code am_gfx950_decode_advance(const int64_t* token, int64_t* tokens_hist, int64_t* pos,
                                         int64_t* step, void* hip_stream);
+
+/* The same for `rows` sequences decoded together: for each r, tokens_hist[r *
+ * hist_stride + *step] = token[r] (when tokens_hist != NULL) and ++pos[r]; then
+ * ++*step once. */
+am_status_code am_gfx950_decode_advance_rows(const int64_t* token, int64_t rows, int64_t* tokens_hist,
+                                             int64_t hist_stride, int64_t* pos, int64_t* step,
+                                             void* hip_stream);
 
 /* Library / device information. */
 int32_t am_gfx950_device_count(void);

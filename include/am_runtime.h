@@ -83,24 +83,37 @@ int64_t am_model_weight_bytes_total(am_model* m); /* repacked linear weights inc
 typedef struct am_session_options {
   int32_t fused_decode; /* 1: fused decode plan (default), 0: one kernel per reference node */
   int32_t use_graph;    /* 1: replay decode steps as a HIP graph */
+  int32_t batch;        /* sequences decoded together, 1..16 (0 means 1); > 1 needs the
+                           fused plan, bf16 activations and bf16/int8/int4 weights */
 } am_session_options;
 
 am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out);
 void am_session_destroy(am_session* s);
-/* Prefill the prompt (host ids) from position 0; returns the first generated token. */
+/* Prefill the prompt (host ids) from position 0; returns the first generated token.
+ * In a batched session this prefills sequence 0. */
 am_status_code am_session_prefill(am_session* s, const int64_t* prompt, int64_t n, int64_t* first_token);
+/* Prefill sequence `row` (0 <= row < batch) of a batched session from position 0, in
+ * its own KV reservation; the other sequences keep their caches and positions. */
+am_status_code am_session_prefill_row(am_session* s, int64_t row, const int64_t* prompt, int64_t n,
+                                      int64_t* first_token);
+/* Number of sequences the session decodes together. */
+int64_t am_session_batch(am_session* s);
 /* Run n decode steps (enqueued, no host sync between steps); copies the n generated
- * tokens to tokens_out (host) at the end. */
+ * tokens to tokens_out (host) at the end: [batch][n], sequence-major.  Every
+ * sequence must have been prefilled. */
 am_status_code am_session_decode(am_session* s, int64_t n, int64_t* tokens_out);
 /* Enqueue n decode steps without reading anything back (benchmark timing). */
 am_status_code am_session_decode_async(am_session* s, int64_t n);
-/* Prefill + greedy decode up to max_new tokens (stops after eos if eos >= 0). */
+/* Prefill + greedy decode up to max_new tokens (stops after eos if eos >= 0).
+ * Single-sequence sessions only. */
 am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
                                    int64_t eos, int64_t* tokens_out, int64_t* n_out);
-/* fp32 logits [vocab] of the most recent step (host copy). */
+/* fp32 logits [batch][vocab] of the most recent step (host copy). */
 am_status_code am_session_logits(am_session* s, float* out);
-/* Current position (tokens committed to the KV cache). */
+/* Current position (tokens committed to the KV cache) of sequence 0. */
 int64_t am_session_position(am_session* s);
+/* Current position of sequence `row` (-1 for a bad row). */
+int64_t am_session_row_position(am_session* s, int64_t row);
 /* Number of kernels launched per decode step by the active decode plan. */
 int64_t am_session_decode_plan_size(am_session* s);
 
