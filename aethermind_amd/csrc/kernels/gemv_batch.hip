@@ -11,7 +11,8 @@
 //     (word >> 4t) & 0x000F000F | 0x43004300 is the bf16 pair (136+q_2t, 136+q_2t+1),
 //     so the four shifted words are the eight bf16 of one MFMA operand in k order.
 //     Each 128-k step is one quantisation group: its MFMA sum starts at -136 * sum(x)
-//     (per-row step sums staged with x) and is scaled by the fp16 group scale.
+//     (one more MFMA per 32 k, x times an all -136 operand) and is scaled by the fp16
+//     group scale, staged per unit in LDS.
 //   * INT8 bytes q+128 convert exactly to bf16 q; the fp32 row scale is applied once.
 //   * bf16 weights are the operand as loaded.
 // Products are exact (bf16 x times an integer below 256), sums are fp32.
@@ -20,7 +21,7 @@
 // RMSNorm'd; rows padded by 16 bytes so the 16-lane column reads are conflict-free).
 // A unit is TPB tiles of 16 features (TPB = 2 pairs the gate and up rows of SiLU-Mul or
 // the two halves of a RoPE rotation); its k steps (64 bytes of every tile row) are
-// dealt to the waves round-robin, and each wave keeps kRing steps of loads in flight,
+// dealt to the waves round-robin, and each wave keeps R steps of loads in flight,
 // running on into the block's next unit.  The waves' partial tiles are summed in LDS
 // and the epilogue runs on one thread per (token row, feature), with the reference
 // op-boundary roundings of the nodes it replaces.
@@ -40,7 +41,6 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBatchMaxRows = 16;
 constexpr int kBWaves = 8;
-constexpr int kRing = 4;  // k steps of loads in flight per wave
 
 enum BEpi { kBStore = 0, kBResidual = 1, kBGateUp = 2, kBQkv = 3 };
 
@@ -110,6 +110,15 @@ __device__ __forceinline__ float bsilu(float g) {
   return g * e / (1.0f + e);
 }
 
+// Block barrier for LDS traffic only: the fences are scoped to LDS, so the barrier
+// waits for this wave's LDS accesses but leaves its global loads in flight
+// (__syncthreads would also drain every outstanding weight load).
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 __device__ __forceinline__ float rnd(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 
@@ -127,9 +136,10 @@ __device__ __forceinline__ int tile_row(const BatchArgs& p, int u, int tt) {
   }
 }
 
-template <int WF, int EPI, bool NORM, int TPB>
+// R: k steps of loads in flight per wave (per tile)
+template <int WF, int EPI, bool NORM, int TPB, int R>
 __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
-  constexpr int NW = kBWaves, NT = NW * 64, R = kRing;
+  constexpr int NW = kBWaves, NT = NW * 64;
   constexpr int KS = BFmt<WF>::ks, MI = BFmt<WF>::mi;
   extern __shared__ __align__(16) uint8_t bsm[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -139,79 +149,142 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
   const int XR = K + 8;                        // LDS row stride (elements)
   const int cnt = ((S + NW - 1) / NW + R - 1) / R * R;  // steps per wave and unit (padded)
   uint16_t* xs = reinterpret_cast<uint16_t*>(bsm);
-  float* xsum = reinterpret_cast<float*>(bsm + ((static_cast<size_t>(rows) * XR * 2 + 15) & ~size_t{15}));
-  float* red = xsum + (WF == AM_WF_INT4 ? S * 16 : 0);  // [NW][TPB][64][4]
+  float* red = reinterpret_cast<float*>(bsm + ((static_cast<size_t>(rows) * XR * 2 + 15) & ~size_t{15}));
+  // [NW][TPB][64][4]
   float* nred = red + NW * TPB * 256;                   // [NW][16]
+  // INT4 group scales of a unit as fp32, double-buffered: [2][TPB][16 rows][S + 1]
+  // (rows padded by one float: the 16 rows of a step read different banks)
+  float* scl = nred + NW * 16;
+  const int SP = S + 1, stile = TPB * 16 * SP;
 
   const int fl = lane & 15, g = lane >> 4;
   uint32_t mask = 0x000F000Fu, magic = 0x43004300u;  // VGPR operands (VOP3 takes no literal)
   asm volatile("" : "+v"(mask), "+v"(magic));
+  const bf16x8_t neg136 = __builtin_bit_cast(bf16x8_t, u32x4_t{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
 
   // ---- weight loads: (unit, wave step t) -> slot; step s = wave + NW * t, dead steps
   // (s >= S) re-read step S - 1 and are not accumulated ----
-  u32x4_t wv[R][TPB];
-  uint32_t sv[R][TPB];
-  auto issue = [&](int r, const int (&rb)[TPB], int t) {
-    const int s = min(wave + NW * t, S - 1);
+  // ---- prologue loads go out first (the memory counter is in order): the first
+  // XB 16-byte pieces of the token rows per thread and the first gain piece, then the
+  // weight ring, so staging x waits for those loads only ----
+  const int pieces = K / 8;       // 16-byte pieces per token row
+  const int tp = rows * pieces;   // pieces of all token rows
+  constexpr int XB = 4;
+  auto xsrc = [&](int e) {
+    e = min(e, tp - 1);
+    const int b = e / pieces;
+    return reinterpret_cast<const u32x4_t*>(p.x + b * p.x_stride) + (e - b * pieces);
+  };
+  auto xdst = [&](int e) {  // clamped like xsrc: a duplicate writes the same piece again
+    e = min(e, tp - 1);
+    const int b = e / pieces;
+    return reinterpret_cast<u32x4_t*>(xs + b * XR + 8 * (e - b * pieces));
+  };
+  u32x4_t xv[XB];
 #pragma unroll
-    for (int tt = 0; tt < TPB; ++tt) {
-      const int row = min(rb[tt] + fl, p.n - 1);
-      const uint8_t* src = p.w + static_cast<int64_t>(row) * p.row_bytes + s * 64 + 16 * g;
-      wv[r][tt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
-      if constexpr (WF == AM_WF_INT4)
-        sv[r][tt] = static_cast<const uint16_t*>(p.scales)[static_cast<int64_t>(row) * S + s];
+  for (int j = 0; j < XB; ++j) xv[j] = *xsrc(tid + NT * j);
+  const uint4* nw = reinterpret_cast<const uint4*>(p.norm_w);
+  uint4 nw0 = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (NORM) nw0 = nw[min(tid, pieces - 1)];
+
+  // INT4 scales of a unit (TPB x 16 rows x S fp16) are loaded by the whole block as
+  // coalesced 2-byte loads, up to kScl per thread, and kept in LDS; loads and stores
+  // are unconditional (clamped: a duplicate rewrites the same value).
+  constexpr int kScl = 4;
+  const int stot = TPB * 16 * S;
+  uint32_t scr[kScl];
+  auto issue_scales = [&](const int (&rb)[TPB]) {
+    if constexpr (WF == AM_WF_INT4) {
+#pragma unroll
+      for (int j = 0; j < kScl; ++j) {
+        const int e = min(tid + NT * j, stot - 1);
+        const int tt = e / (16 * S), rem = e - tt * 16 * S;
+        const int rr = rem / S;
+        const int row = min(rb[tt] + rr, p.n - 1);
+        scr[j] = static_cast<const uint16_t*>(p.scales)[static_cast<int64_t>(row) * S + (rem - rr * S)];
+      }
     }
+  };
+  auto store_scales = [&](int buf) {
+    if constexpr (WF == AM_WF_INT4) {
+#pragma unroll
+      for (int j = 0; j < kScl; ++j) {
+        const int e = min(tid + NT * j, stot - 1);
+        const int tt = e / (16 * S), rem = e - tt * 16 * S;
+        const int rr = rem / S;
+        scl[buf * stile + (tt * 16 + rr) * SP + (rem - rr * S)] =
+            static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(scr[j])));
+      }
+    }
+  };
+
+  // Slots refilled past the block's last unit are never read; they load the token
+  // rows this block has just read (cached) instead of re-streaming weights, and stay
+  // unconditional: a conditional refill makes the compiler's memory-counter waits
+  // conservative at the loop head.
+  u32x4_t wv[R][TPB];
+  const uint8_t* tail_src = reinterpret_cast<const uint8_t*>(p.x) + (lane * 16) % (rows * K * 2);
+  // lane's row pointers of the tiles of a unit (computed once per unit)
+  auto row_ptrs = [&](const int (&rb)[TPB], bool tail, const uint8_t* (&wp)[TPB]) {
+#pragma unroll
+    for (int tt = 0; tt < TPB; ++tt)
+      wp[tt] = tail ? tail_src : p.w + static_cast<int64_t>(min(rb[tt] + fl, p.n - 1)) * p.row_bytes + 16 * g;
+  };
+  auto issue = [&](int r, const uint8_t* const (&wp)[TPB], int t, bool tail) {
+    const int off = tail ? 0 : min(wave + NW * t, S - 1) * 64;  // wave-uniform
+#pragma unroll
+    for (int tt = 0; tt < TPB; ++tt)
+      wv[r][tt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp[tt] + off));
   };
   const int grid = gridDim.x;
   int u = blockIdx.x;
   int rb_cur[TPB];  // first weight row of each tile of unit u
 #pragma unroll
   for (int tt = 0; tt < TPB; ++tt) rb_cur[tt] = tile_row<EPI, TPB>(p, u, tt);
+  issue_scales(rb_cur);
+  const uint8_t* wp_cur[TPB];
+  row_ptrs(rb_cur, false, wp_cur);
 #pragma unroll
-  for (int r = 0; r < R; ++r) issue(r, rb_cur, r);
+  for (int r = 0; r < R; ++r) issue(r, wp_cur, r, false);
 
   // ---- prologue: token rows -> LDS (bf16), RMSNorm'd when NORM ----
-  const int pieces = K / 8;  // 16-byte pieces per row
-  for (int b = 0; b < rows; ++b) {
-    const uint4* src = reinterpret_cast<const uint4*>(p.x + b * p.x_stride);
-    for (int c = tid; c < pieces; c += NT) *reinterpret_cast<uint4*>(xs + b * XR + 8 * c) = src[c];
+  // stores are unconditional (clamped): a store under a branch would pull its load
+  // into the branch, behind a wait for every weight load issued above
+#pragma unroll
+  for (int j = 0; j < XB; ++j) *xdst(tid + NT * j) = xv[j];
+  for (int e0 = XB * NT; e0 < tp; e0 += XB * NT) {  // more than XB pieces per thread
+#pragma unroll
+    for (int j = 0; j < XB; ++j) xv[j] = *xsrc(e0 + tid + NT * j);
+#pragma unroll
+    for (int j = 0; j < XB; ++j) *xdst(e0 + tid + NT * j) = xv[j];
   }
+  store_scales(0);
   if constexpr (NORM) {
-    __syncthreads();
-    float ss[kBatchMaxRows];
+    lds_sync();
+    // one wave per token row: sum of squares, then 1/rms into nred[b]
+    for (int b = wave; b < rows; b += NW) {
+      float ss = 0.0f;
+      for (int c = lane; c < pieces; c += 64) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xs + b * XR + 8 * c);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int b = 0; b < kBatchMaxRows; ++b) {
-      ss[b] = 0.0f;
-      if (b < rows)
-        for (int c = tid; c < pieces; c += NT) {
-          const uint4 v = *reinterpret_cast<const uint4*>(xs + b * XR + 8 * c);
-          const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float a0 = __uint_as_float(wd[t] << 16), a1 = __uint_as_float(wd[t] & 0xFFFF0000u);
-            ss[b] = fmaf(a0, a0, ss[b]);
-            ss[b] = fmaf(a1, a1, ss[b]);
-          }
+        for (int t = 0; t < 4; ++t) {
+          const float a0 = __uint_as_float(wd[t] << 16), a1 = __uint_as_float(wd[t] & 0xFFFF0000u);
+          ss = fmaf(a0, a0, ss);
+          ss = fmaf(a1, a1, ss);
         }
-      ss[b] = wave_sum(ss[b]);
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) nred[b] = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
     }
-    if (lane < kBatchMaxRows) {
-      float v = 0.0f;
-#pragma unroll
-      for (int b = 0; b < kBatchMaxRows; ++b) v = lane == b ? ss[b] : v;
-      nred[wave * 16 + lane] = v;
-    }
-    __syncthreads();
-    const uint4* nw = reinterpret_cast<const uint4*>(p.norm_w);
-    for (int b = 0; b < rows; ++b) {
-      float t = 0.0f;
-#pragma unroll
-      for (int w2 = 0; w2 < NW; ++w2) t += nred[w2 * 16 + b];
-      const float inv = 1.0f / sqrtf(t / static_cast<float>(K) + p.eps);
-      for (int c = tid; c < pieces; c += NT) {
+    lds_sync();
+    auto norm_piece = [&](int c, const uint4& wn) {
+      const uint32_t nn[4] = {wn.x, wn.y, wn.z, wn.w};
+      for (int b = 0; b < rows; ++b) {
+        const float inv = nred[b];
         uint4* dst = reinterpret_cast<uint4*>(xs + b * XR + 8 * c);
-        const uint4 v = *dst, wn = nw[c];
-        const uint32_t xw[4] = {v.x, v.y, v.z, v.w}, nn[4] = {wn.x, wn.y, wn.z, wn.w};
+        const uint4 v = *dst;
+        const uint32_t xw[4] = {v.x, v.y, v.z, v.w};
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -221,49 +294,25 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
         }
         *dst = make_uint4(o[0], o[1], o[2], o[3]);
       }
-    }
+    };
+    if (tid < pieces) norm_piece(tid, nw0);  // the gain piece loaded with the rows
+    for (int c = tid + NT; c < pieces; c += NT) norm_piece(c, nw[c]);
   }
-  if constexpr (WF == AM_WF_INT4) {
-    __syncthreads();
-    // per-row sums of x over each 128-k step; rows past the batch read zero
-    uint32_t ones = 0x3F803F80u;  // bf16 pair (1, 1)
-    asm volatile("" : "+v"(ones));
-    for (int e = tid; e < S * 16; e += NT) {
-      const int s = e >> 4, b = e & 15;
-      float acc = 0.0f;
-      if (b < rows) {
-        const uint4* src = reinterpret_cast<const uint4*>(xs + b * XR + s * KS);
-#pragma unroll 4
-        for (int c = 0; c < KS / 8; ++c) {
-          const uint4 v = src[c];
-          acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, v.x),
-                                                __builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, ones),
-                                                acc, false);
-          acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, v.y),
-                                                __builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, ones),
-                                                acc, false);
-          acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, v.z),
-                                                __builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, ones),
-                                                acc, false);
-          acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, v.w),
-                                                __builtin_bit_cast(__attribute__((ext_vector_type(2))) __bf16, ones),
-                                                acc, false);
-        }
-      }
-      xsum[e] = -136.0f * acc;
-    }
-  }
-  __syncthreads();
+  lds_sync();
 
   // A operand rows: lanes past the batch use zeros
   const bool xrow_ok = fl < rows;
   const uint16_t* xrow = xs + min(fl, rows - 1) * XR + g * (KS / 4);
 
-  for (; u < units; u += grid) {
+  for (int buf = 0; u < units; u += grid, buf ^= 1) {
     const bool more = u + grid < units;  // the block has a next unit
     int rb_nxt[TPB];
 #pragma unroll
     for (int tt = 0; tt < TPB; ++tt) rb_nxt[tt] = more ? tile_row<EPI, TPB>(p, u + grid, tt) : rb_cur[tt];
+    issue_scales(rb_nxt);  // next unit's scales, ahead of this unit's refills
+    const uint8_t* wp_nxt[TPB];
+    row_ptrs(rb_nxt, !more, wp_nxt);
+    const float* sct = scl + buf * stile + fl * SP;
     f32x4_t acc[TPB];
 #pragma unroll
     for (int tt = 0; tt < TPB; ++tt) acc[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -272,7 +321,7 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
       for (int r = 0; r < R; ++r) {
         const int t = t0 + r;
         const int s_raw = wave + NW * t;
-        const bool live = s_raw < S;  // wave-uniform
+        const float live = s_raw < S ? 1.0f : 0.0f;  // wave-uniform: dead steps add nothing
         const int s = min(s_raw, S - 1);
         bf16x8_t xa[MI];
 #pragma unroll
@@ -280,8 +329,13 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
           const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(xrow + s * KS + 8 * i);
           xa[i] = xrow_ok ? v : bf16x8_t{};
         }
+        // INT4: the step's MFMA sums start at -136 * sum(x) of each token row, itself an
+        // MFMA of x with an all -136 operand (exact products, fp32 sums)
         f32x4_t c0 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (WF == AM_WF_INT4) c0 = *reinterpret_cast<const f32x4_t*>(xsum + s * 16 + 4 * g);
+        if constexpr (WF == AM_WF_INT4) {
+#pragma unroll
+          for (int i = 0; i < MI; ++i) c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], neg136, c0, 0, 0, 0);
+        }
 #pragma unroll
         for (int tt = 0; tt < TPB; ++tt) {
           f32x4_t part = c0;
@@ -289,24 +343,17 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
           for (int i = 0; i < MI; ++i)
             part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[i], w_operand<WF>(wv[r][tt], i, mask, magic), part, 0,
                                                            0, 0);
-          if constexpr (WF == AM_WF_INT4) {
-            const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sv[r][tt])));
-            const f32x4_t na = acc[tt] + sc * part;
-            acc[tt] = live ? na : acc[tt];
-          } else {
-            const f32x4_t na = acc[tt] + part;
-            acc[tt] = live ? na : acc[tt];
-          }
+          float sc = live;
+          if constexpr (WF == AM_WF_INT4) sc *= sct[tt * 16 * SP + s];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[tt][e] = fmaf(sc, part[e], acc[tt][e]);
         }
         // refill the slot: the next step of this unit, or the first steps of the next
-        // unit; past the block's last unit it re-reads this step's rows
+        // unit; nothing past the block's last unit (those slots are never read again)
         int tn = t + R;
         const bool wrap = tn >= cnt;
-        int rb[TPB];
-#pragma unroll
-        for (int tt = 0; tt < TPB; ++tt) rb[tt] = wrap ? rb_nxt[tt] : rb_cur[tt];
-        if (wrap) tn = more ? tn - cnt : t;
-        issue(r, rb, tn);
+        if (wrap) tn -= cnt;
+        issue(r, wrap ? wp_nxt : wp_cur, tn, wrap && !more);
       }
     }
 
@@ -314,7 +361,8 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
 #pragma unroll
     for (int tt = 0; tt < TPB; ++tt)
       *reinterpret_cast<f32x4_t*>(red + ((wave * TPB + tt) * 64 + lane) * 4) = acc[tt];
-    __syncthreads();
+    store_scales(buf ^ 1);  // every wave is past its last read of that buffer (unit u-1)
+    lds_sync();
     if (tid < rows * 16) {
       const int b = tid >> 4, f = tid & 15;
       const int src = (f + 16 * (b >> 2)) * 4 + (b & 3);
@@ -384,16 +432,19 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
         }
       }
     }
-    __syncthreads();
+    lds_sync();
 #pragma unroll
-    for (int tt = 0; tt < TPB; ++tt) rb_cur[tt] = rb_nxt[tt];
+    for (int tt = 0; tt < TPB; ++tt) {
+      rb_cur[tt] = rb_nxt[tt];
+      wp_cur[tt] = wp_nxt[tt];
+    }
   }
 }
 
 // ---- host ----
-template <int WF, int EPI, bool NORM, int TPB>
+template <int WF, int EPI, bool NORM, int TPB, int R>
 am_status_code LaunchBatch(const BatchArgs& a, size_t lds, hipStream_t s) {
-  auto fn = gemv_batch_kernel<WF, EPI, NORM, TPB>;
+  auto fn = gemv_batch_kernel<WF, EPI, NORM, TPB, R>;
   static thread_local size_t cached_lds = 0;
   static thread_local int cached_blocks = 0;
   if (cached_lds != lds) {
@@ -419,12 +470,23 @@ am_status_code LaunchBatch(const BatchArgs& a, size_t lds, hipStream_t s) {
   return AM_STATUS_OK;
 }
 
+// Single-tile units keep 8 steps in flight per wave once a wave has that many steps
+// (long rows); paired units (two loads per step) and short rows keep 4.
+template <int WF, int EPI, bool NORM, int TPB>
+am_status_code LaunchBatchR(const BatchArgs& a, size_t lds, hipStream_t s) {
+  if constexpr (TPB == 1) {
+    const int S = a.k / BFmt<WF>::ks;
+    if ((S + kBWaves - 1) / kBWaves >= 8) return LaunchBatch<WF, EPI, NORM, TPB, 8>(a, lds, s);
+  }
+  return LaunchBatch<WF, EPI, NORM, TPB, 4>(a, lds, s);
+}
+
 template <int EPI, bool NORM, int TPB>
 am_status_code DispatchBatch(int32_t fmt, const BatchArgs& a, size_t lds, hipStream_t s) {
   switch (fmt) {
-    case AM_WF_BF16: return LaunchBatch<AM_WF_BF16, EPI, NORM, TPB>(a, lds, s);
-    case AM_WF_INT8: return LaunchBatch<AM_WF_INT8, EPI, NORM, TPB>(a, lds, s);
-    default: return LaunchBatch<AM_WF_INT4, EPI, NORM, TPB>(a, lds, s);
+    case AM_WF_BF16: return LaunchBatchR<AM_WF_BF16, EPI, NORM, TPB>(a, lds, s);
+    case AM_WF_INT8: return LaunchBatchR<AM_WF_INT8, EPI, NORM, TPB>(a, lds, s);
+    default: return LaunchBatchR<AM_WF_INT4, EPI, NORM, TPB>(a, lds, s);
   }
 }
 
@@ -447,8 +509,11 @@ am_status_code PrepareBatch(const am_gfx950_weight& w, int64_t rows, const void*
                "batched decode: weights and token rows must be 16-byte aligned");
   const int64_t S = w.k / ks;
   size_t b = ((static_cast<size_t>(rows) * (w.k + 8) * 2 + 15) & ~size_t{15});
-  if (w.format == AM_WF_INT4) b += static_cast<size_t>(S) * 16 * 4;
   b += static_cast<size_t>(kBWaves) * tpb * 256 * 4 + kBWaves * 16 * 4;
+  if (w.format == AM_WF_INT4) {
+    AM_CHECK_ARG(tpb * 16 * S <= 4 * kBWaves * 64, "batched decode: int4 rows too long for the scale tile");
+    b += static_cast<size_t>(2) * tpb * 16 * (S + 1) * 4;
+  }
   AM_CHECK_ARG(b <= 160 * 1024, "batched decode: token rows do not fit in LDS (rows x in_features too large)");
   a->x = static_cast<const uint16_t*>(x);
   a->x_stride = x_stride;
@@ -471,8 +536,11 @@ bool BatchLinearEligible(int32_t act, const am_gfx950_weight& w, int64_t m, cons
   if (w.format == AM_WF_F32 || (w.format == AM_WF_INT4 && w.group_size != 128)) return false;
   const int64_t ks = w.format == AM_WF_BF16 ? 32 : (w.format == AM_WF_INT8 ? 64 : 128);
   if (w.k % ks != 0 || !Aligned16(x) || !Aligned16(w.data)) return false;
-  size_t b = static_cast<size_t>(m) * (w.k + 8) * 2 + (w.format == AM_WF_INT4 ? (w.k / 128) * 64 : 0) +
-             kBWaves * 256 * 4 + kBWaves * 64 + 16;
+  size_t b = static_cast<size_t>(m) * (w.k + 8) * 2 + kBWaves * 256 * 4 + kBWaves * 64 + 16;
+  if (w.format == AM_WF_INT4) {
+    if (16 * (w.k / 128) > 4 * kBWaves * 64) return false;
+    b += static_cast<size_t>(2) * 16 * (w.k / 128 + 1) * 4;
+  }
   return b <= 160 * 1024;
 }
 

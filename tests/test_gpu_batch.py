@@ -210,6 +210,28 @@ def test_fused_lm_head_batched_argmax_and_state():
     assert not host(ws)[:256].any(), "argmax tickets must be left zero"
 
 
+def test_attention_decode_long_context_batch4():
+    """The long-context decode of BASELINE configs[4]: four sequences at positions near
+    8k (and one at the last cache row) over their own cache planes, 8B head shape."""
+    B, hq, hkv, d, cap = 4, 32, 8, 128, 8448
+    starts = [8191, 8300, 5000, cap - 1]
+    q = rbf(O.synth_f32(70, 1, B * hq * d, std=1.0).reshape(B, hq * d))
+    kc = rbf(O.synth_f32(70, 2, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    vc = rbf(O.synth_f32(70, 3, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
+    qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+    out = empty((B, hq * d), torch.int16)
+    posd = dev(np.array(starts, np.int64))
+    wsb = L.am_gfx950_attention_workspace_bytes(B, 1, hq, hkv, d, cap, 0)
+    ws = zeros((max(wsb, 1),), torch.uint8)
+    a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), 1, hq, hkv, d, cap, 0, p(posd), B, hkv * cap * d, 1, 0,
+                        p(ws), wsb)
+    L.call("am_gfx950_attention", a, stream())
+    got = rd(out)
+    for r in range(B):
+        ref = O.attention(q[r:r + 1], kc[r], vc[r], 1, hq, hkv, d, cap, starts[r])[0]
+        close(got[r], ref, TOL, f"row {r} start {starts[r]}")
+
+
 # ---------------------------------------------------------------- batched session
 class _Rt:
     def __init__(self):
