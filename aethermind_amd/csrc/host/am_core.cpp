@@ -99,6 +99,7 @@ const char* ToString(OpType op) noexcept {
     case OpType::kFusedRmsNormQkvRoPEKVUpdate: return "FusedRmsNormQkvRoPEKVUpdate";
     case OpType::kFusedLinearAdd: return "FusedLinearAdd";
     case OpType::kFusedRmsNormGateUpSiluMul: return "FusedRmsNormGateUpSiluMul";
+    case OpType::kFusedDecodeLayers: return "FusedDecodeLayers";
     case OpType::kFusedRmsNormLmHeadArgmax: return "FusedRmsNormLmHeadArgmax";
     case OpType::kEmbedToken: return "EmbedToken";
     default: return "Unknown";

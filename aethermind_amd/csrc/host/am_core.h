@@ -206,6 +206,7 @@ enum class OpType : uint16_t {
   kFusedRmsNormGateUpSiluMul,
   kFusedRmsNormLmHeadArgmax,
   kEmbedToken,
+  kFusedDecodeLayers,  // every layer of one decode token in one persistent launch
 };
 const char* ToString(OpType op) noexcept;
 

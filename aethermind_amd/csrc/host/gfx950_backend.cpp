@@ -248,6 +248,33 @@ Status FusedLinearAddKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_fused_linear_residual(&a, StreamOf(ctx)));
 }
 
+// in: h, pos, cos, sin, layer table (device am_gfx950_decode_layer[layers]),
+// workspace; out: h (the embedding in, the last layer's output out)
+Status FusedDecodeLayersKernel(const KernelContext& ctx) noexcept {
+  const GfxParams* p = P(ctx);
+  AM_RETURN_IF_ERROR(NeedArgs(p, 6, 1, "FusedDecodeLayers"));
+  DecodeLayersAttrs at{};
+  if (!ReadAttrs(ctx, &at)) return Status::InvalidArgument("FusedDecodeLayers: attrs missing");
+  am_gfx950_decode_layers_args a{};
+  a.layers = static_cast<const am_gfx950_decode_layer*>(p->in[4].p);
+  a.num_layers = at.layers;
+  a.hidden = at.hidden;
+  a.hq = at.hq;
+  a.hkv = at.hkv;
+  a.head_dim = at.d;
+  a.ffn = at.ffn;
+  a.capacity = at.cap;
+  a.eps = at.eps;
+  a.pos = static_cast<const int64_t*>(p->in[1].p);
+  a.cos_tab = static_cast<const float*>(p->in[2].p);
+  a.sin_tab = static_cast<const float*>(p->in[3].p);
+  a.h = p->out[0].p;
+  a.workspace = p->in[5].p;
+  a.workspace_bytes = p->in[5].d[0];
+  a.dtype = p->out[0].dt;
+  return FromC(am_gfx950_decode_layers(&a, StreamOf(ctx)));
+}
+
 // in: h, norm_w; out: act
 Status FusedGateUpKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
@@ -436,6 +463,8 @@ AM_REGISTER_KERNEL(HipArgmaxBF16, Desc(OpType::kArgmax, HipSelector(kBF16, kBF16
                                           &FusedLmHeadKernel, "gfx950::fused_norm_lmhead_argmax_" #TAG))
 
 namespace {
+AM_REGISTER_KERNEL(HipDecodeLayersBF16I4, Desc(OpType::kFusedDecodeLayers, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kDecode),
+                                             &FusedDecodeLayersKernel, "gfx950::persistent_decode_layers_bf16_int4"))
 AM_FUSED_REGS(f32_f32, kF32, kF32, WF::kPlain)
 AM_FUSED_REGS(f32_bf16, kF32, kBF16, WF::kPlain)
 AM_FUSED_REGS(f32_int8, kF32, kI8, WF::kQuantizedInt8)

@@ -37,6 +37,7 @@ struct KvAttrs { int64_t hkv, d, cap; };
 // start cbs elements after sequence r-1's (cbs is the same batch stride for QkvAttrs).
 struct AttnAttrs { int64_t hq, hkv, d, cap; int32_t splits; int64_t batch, cbs; };
 struct QkvAttrs { float eps; int64_t hq, hkv, d, cap, cbs; };
+struct DecodeLayersAttrs { float eps; int64_t layers, hidden, hq, hkv, d, ffn, cap; };
 
 template <typename T>
 std::vector<std::byte> PackAttrs(const T& v) {

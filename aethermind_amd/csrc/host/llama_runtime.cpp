@@ -283,7 +283,7 @@ class LlamaSession {
   std::unique_ptr<HipStream> hs;
   BackendRegistry backends;
   Backend* backend = nullptr;
-  am_session_options opt{1, 1, 1};
+  am_session_options opt{1, 1, 1, 0};
   int64_t B = 1;  // sequences decoded together
 
   // KV: one reference KVCacheManager per sequence, planes in kv_slab
@@ -309,6 +309,13 @@ class LlamaSession {
   void* am_ws = nullptr;
   int64_t am_ws_bytes = 0;
 
+  // persistent all-layers decode (am_gfx950_decode_layers): device layer table and
+  // exchange workspace (zero-filled at creation and after an aborted launch)
+  bool persistent = false;
+  void* dl_table = nullptr;
+  void* dl_ws = nullptr;
+  int64_t dl_ws_bytes = 0;
+
   // decode plan
   std::unique_ptr<ExecutionPlan> decode_plan;
   RuntimeBindingContext decode_bind;
@@ -325,6 +332,8 @@ class LlamaSession {
     kvs.clear();
     if (kv_slab) (void)hipFree(kv_slab);
     if (act_slab) (void)hipFree(act_slab);
+    if (dl_table) (void)hipFree(dl_table);
+    if (dl_ws) (void)hipFree(dl_ws);
   }
 
   int64_t HistStride() const { return static_cast<int64_t>(m->cfg.max_tokens) + 1; }
@@ -427,7 +436,87 @@ class LlamaSession {
     decode_bind.SetStream(hs.get());
     decode_bind.SetWorkspace(attn_ws, attn_ws_bytes);
     AM_HIP_OK(hipStreamSynchronize(stream));
+    AM_RETURN_IF_ERROR(SetupPersistent());
     return BuildDecodePlan();
+  }
+
+  am_gfx950_decode_layers_args DecodeLayersArgs() const {
+    const auto& c = m->cfg;
+    am_gfx950_decode_layers_args a{};
+    a.layers = static_cast<const am_gfx950_decode_layer*>(dl_table);
+    a.num_layers = c.num_layers;
+    a.hidden = c.hidden;
+    a.hq = c.num_q_heads;
+    a.hkv = c.num_kv_heads;
+    a.head_dim = c.head_dim;
+    a.ffn = c.ffn;
+    a.capacity = c.max_tokens;
+    a.eps = c.rms_eps;
+    a.cos_tab = m->cos_tab;
+    a.sin_tab = m->sin_tab;
+    a.pos = pos_ptr();
+    a.h = h;
+    a.workspace = dl_ws;
+    a.workspace_bytes = dl_ws_bytes;
+    a.dtype = c.act_dtype;
+    return a;
+  }
+
+  // Decides whether batch-1 decode runs as one persistent launch for all layers
+  // (option persistent_decode: 1 requested, else the per-op fused plan) and prepares
+  // its device layer table and exchange workspace.
+  Status SetupPersistent() {
+    const auto& c = m->cfg;
+    persistent = false;
+    if (opt.persistent_decode <= 0) return Status::Ok();
+    const bool required = true;
+    if (B != 1 || !opt.fused_decode || c.act_dtype != AM_DT_BF16 || c.weight_format != AM_WF_INT4) {
+      if (required)
+        return Status::Unimplemented("persistent decode needs batch 1, the fused plan, bf16 activations and INT4 weights");
+      return Status::Ok();
+    }
+    const size_t L = static_cast<size_t>(c.num_layers);
+    std::vector<am_gfx950_decode_layer> host(L);
+    for (size_t l = 0; l < L; ++l) {
+      auto kp = views[0].KeyPlane(l);
+      auto vp = views[0].ValuePlane(l);
+      if (!kp.ok()) return kp.status();
+      if (!vp.ok()) return vp.status();
+      host[l] = am_gfx950_decode_layer{m->qkv[l], m->o[l], m->gate_up[l], m->down[l], m->in_norm[l], m->post_norm[l],
+                                       kp.value(), vp.value()};
+    }
+    dl_ws_bytes = am_gfx950_decode_layers_workspace_bytes(c.hidden, c.num_q_heads, c.num_kv_heads, c.head_dim, c.ffn);
+    if (dl_ws_bytes <= 0) {
+      if (required) return Status::Unimplemented("persistent decode: unsupported head_dim or shape");
+      return Status::Ok();
+    }
+    AM_HIP_OK(hipMalloc(&dl_ws, static_cast<size_t>(dl_ws_bytes)));
+    AM_HIP_OK(hipMalloc(&dl_table, L * sizeof(am_gfx950_decode_layer)));
+    const am_gfx950_decode_layers_args a = DecodeLayersArgs();
+    if (am_gfx950_decode_layers_validate(&a, host.data()) != AM_STATUS_OK) {
+      const std::string why = am_last_error_message();
+      (void)hipFree(dl_ws);
+      (void)hipFree(dl_table);
+      dl_ws = dl_table = nullptr;
+      dl_ws_bytes = 0;
+      if (required) return Status::Unimplemented("persistent decode: " + why);
+      return Status::Ok();
+    }
+    AM_HIP_OK(hipMemcpy(dl_table, host.data(), L * sizeof(am_gfx950_decode_layer), hipMemcpyHostToDevice));
+    AM_HIP_OK(hipMemset(dl_ws, 0, static_cast<size_t>(dl_ws_bytes)));
+    persistent = true;
+    return Status::Ok();
+  }
+
+  // After a synchronised decode: a persistent launch whose blocks were not all
+  // resident ends early with the workspace abort flag set.
+  Status CheckPersistentAbort() {
+    if (!persistent) return Status::Ok();
+    int32_t ab = 0;
+    if (am_gfx950_decode_layers_aborted(dl_ws, &ab) != AM_STATUS_OK) return Status::Internal(am_last_error_message());
+    if (ab == 0) return Status::Ok();
+    AM_HIP_OK(hipMemset(dl_ws, 0, static_cast<size_t>(dl_ws_bytes)));
+    return Status::Internal("persistent decode: a cross-block wait timed out (the grid was not resident at once)");
   }
 
   // ---------------------------------------------------------------- plan building
@@ -581,7 +670,18 @@ class LlamaSession {
                                 TensorView(err, DataType::Int(32), {1})},
                                {MutableTensorView(h, A, {B, H})}));
     }
-    for (int64_t l = 0; l < c.num_layers; ++l) {
+    if (persistent) {
+      const gfx950::DecodeLayersAttrs da{c.rms_eps, c.num_layers, H, c.num_q_heads, c.num_kv_heads, d, F, c.max_tokens};
+      AM_RETURN_IF_ERROR(b.Add(
+          OpType::kFusedDecodeLayers, PackAttrs(da), Sel(true, ph), nullptr,
+          {TensorView(h, A, {1, H}), TensorView(pos_ptr(), DataType::Int(64), {1}),
+           TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+           TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+           TensorView(dl_table, DataType::UInt(8), {static_cast<int64_t>(c.num_layers * sizeof(am_gfx950_decode_layer))}),
+           TensorView(dl_ws, DataType::UInt(8), {dl_ws_bytes})},
+          {MutableTensorView(h, A, {1, H})}));
+    }
+    for (int64_t l = 0; l < c.num_layers && !persistent; ++l) {
       if (!opt.fused_decode) {
         AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, 1, ph, pos_ptr(), pos_ptr(), 0));
         continue;
@@ -744,6 +844,7 @@ class LlamaSession {
         AM_HIP_OK(hipMemcpyAsync(out + r * n, hist_ptr(r) + first_step, static_cast<size_t>(n) * 8,
                                  hipMemcpyDeviceToHost, stream));
     AM_HIP_OK(hipStreamSynchronize(stream));
+    AM_RETURN_IF_ERROR(CheckPersistentAbort());
     int32_t e = 0;
     AM_HIP_OK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
     if (e != 0) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
@@ -766,6 +867,7 @@ class LlamaSession {
       for (size_t i = 0; i < steps.size() && st.ok(); ++i) {
         const OpType t = steps[i].op->Type();
         const bool gemv = t == OpType::kFusedRmsNormQkvRoPEKVUpdate || t == OpType::kFusedLinearAdd ||
+                          t == OpType::kFusedDecodeLayers ||
                           t == OpType::kFusedRmsNormGateUpSiluMul ||
                           (t == OpType::kFusedRmsNormLmHeadArgmax && B == 1);
         if (gemv) {
@@ -803,6 +905,7 @@ class LlamaSession {
       if (e0[i]) (void)hipEventDestroy(e0[i]);
       if (e1[i]) (void)hipEventDestroy(e1[i]);
     }
+    if (st.ok()) st = CheckPersistentAbort();
     if (st.ok()) {
       host_step += n;
       st = Advance(n);
@@ -1037,6 +1140,8 @@ int64_t am_session_row_position(am_session* s, int64_t row) {
   if (!s || row < 0 || row >= s->impl->B) return -1;
   return s->impl->row_pos[static_cast<size_t>(row)];
 }
+
+int32_t am_session_persistent_decode(am_session* s) { return s && s->impl->persistent ? 1 : 0; }
 
 int64_t am_session_decode_plan_size(am_session* s) {
   return s && s->impl->decode_plan ? static_cast<int64_t>(s->impl->decode_plan->size()) : 0;

@@ -112,6 +112,17 @@ class FusedLmHeadArgs(C.Structure):
                 ("workspace_bytes", i64), ("rows", i64), ("hist_stride", i64)]
 
 
+class DecodeLayer(C.Structure):
+    _fields_ = [("w_qkv", Weight), ("w_o", Weight), ("w_gate_up", Weight), ("w_down", Weight), ("in_norm", vp),
+                ("post_norm", vp), ("k_cache", vp), ("v_cache", vp)]
+
+
+class DecodeLayersArgs(C.Structure):
+    _fields_ = [("layers", vp), ("num_layers", i64), ("hidden", i64), ("hq", i64), ("hkv", i64), ("head_dim", i64),
+                ("ffn", i64), ("capacity", i64), ("eps", f32), ("cos_tab", vp), ("sin_tab", vp), ("pos", vp),
+                ("h", vp), ("workspace", vp), ("workspace_bytes", i64), ("dtype", i32), ("timeline", vp)]
+
+
 class ModelConfig(C.Structure):
     _fields_ = [("num_layers", i32), ("hidden", i32), ("num_q_heads", i32), ("num_kv_heads", i32),
                 ("head_dim", i32), ("ffn", i32), ("vocab", i32), ("rms_eps", f32), ("rope_theta", f64),
@@ -120,7 +131,7 @@ class ModelConfig(C.Structure):
 
 
 class SessionOptions(C.Structure):
-    _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32)]
+    _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32)]
 
 
 _SIGS = {
@@ -158,6 +169,10 @@ _SIGS = {
     "am_gfx950_fused_gate_up": (i32, [C.POINTER(FusedGateUpArgs), vp]),
     "am_gfx950_fused_lm_head": (i32, [C.POINTER(FusedLmHeadArgs), vp]),
     "am_gfx950_lm_head_workspace_bytes": (i64, []),
+    "am_gfx950_decode_layers": (i32, [C.POINTER(DecodeLayersArgs), vp]),
+    "am_gfx950_decode_layers_workspace_bytes": (i64, [i64, i64, i64, i64, i64]),
+    "am_gfx950_decode_layers_validate": (i32, [C.POINTER(DecodeLayersArgs), C.POINTER(DecodeLayer)]),
+    "am_gfx950_decode_layers_aborted": (i32, [vp, C.POINTER(i32)]),
     "am_gfx950_decode_advance": (i32, [vp, vp, vp, vp, vp]),
     "am_gfx950_decode_advance_rows": (i32, [vp, i64, vp, i64, vp, vp, vp]),
     "am_runtime_create": (i32, [i32, C.POINTER(vp)]),
@@ -182,6 +197,7 @@ _SIGS = {
     "am_session_logits": (i32, [vp, vp]),
     "am_session_position": (i64, [vp]),
     "am_session_decode_plan_size": (i64, [vp]),
+    "am_session_persistent_decode": (i32, [vp]),
     "am_session_profile_decode": (i32, [vp, i64, vp, vp]),
 }
 

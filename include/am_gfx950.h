@@ -380,6 +380,61 @@ am_status_code am_gfx950_decode_advance_rows(const int64_t* token, int64_t rows,
                                              int64_t hist_stride, int64_t* pos, int64_t* step,
                                              void* hip_stream);
 
+/* ---------------- persistent decode of all layers (one launch per token) ----------
+ * The per-layer node sequence of model_graph_builder.cpp:133-290 (RmsNorm -> Linear
+ * q|k|v -> RoPE -> KVCacheUpdate -> Attention -> Linear o -> Add -> RmsNorm -> Linear
+ * gate|up -> SiluMul -> Linear down -> Add) for every layer of one token (batch 1),
+ * with the roundings of the fused kernels above.  Replaces the per-layer sequence of
+ * am_gfx950_fused_qkv / am_gfx950_attention / am_gfx950_fused_linear_residual /
+ * am_gfx950_fused_gate_up / am_gfx950_fused_linear_residual (the executor's steps,
+ * layer_runner.cpp:24-67) by one grid of one block per CU that exchanges step
+ * outputs through the workspace.  Scope: bf16 activations, INT4 group-128 weights,
+ * head_dim 128, hidden = q heads x 128 in {2048, 4096}, ffn a multiple of 128 up to
+ * 16384, q heads <= 8 x kv heads, a 256-CU device (else UNIMPLEMENTED). */
+typedef struct am_gfx950_decode_layer {
+  am_gfx950_weight w_qkv;     /* [(hq + 2 hkv) * 128, hidden], rows q then k then v */
+  am_gfx950_weight w_o;       /* [hidden, hq * 128] */
+  am_gfx950_weight w_gate_up; /* [2 ffn, hidden], rows gate then up */
+  am_gfx950_weight w_down;    /* [hidden, ffn] */
+  const void* in_norm;        /* [hidden] input_layernorm gain */
+  const void* post_norm;      /* [hidden] post_attention_layernorm gain */
+  void* k_cache;              /* this layer's key plane [hkv][capacity][128] */
+  void* v_cache;              /* this layer's value plane */
+} am_gfx950_decode_layer;
+
+typedef struct am_gfx950_decode_layers_args {
+  const am_gfx950_decode_layer* layers; /* DEVICE array of num_layers entries */
+  int64_t num_layers, hidden, hq, hkv, head_dim, ffn, capacity;
+  float eps;
+  const float* cos_tab; /* [capacity][64] */
+  const float* sin_tab;
+  const int64_t* pos; /* device: position of the token (KV row written) */
+  void* h;            /* [hidden] bf16: the embedding in, the last layer's output out */
+  void* workspace;    /* am_gfx950_decode_layers_workspace_bytes(), 256-byte aligned,
+                         zero-filled once before the first call; calls on one
+                         workspace must not overlap */
+  int64_t workspace_bytes;
+  int32_t dtype;  /* AM_DT_BF16 */
+  void* timeline; /* optional (NULL = off): uint64 [num_layers][256 blocks][16] wall-clock
+                     stamps (100 MHz) per block at the step points: 0 layer entry,
+                     1 h gathered, 2 q|k|v done, 3 attention output gathered, 4 o done,
+                     5 h gathered for the MLP, 6 gate|up done, 7 SiLU-Mul gathered;
+                     attention blocks: 8 q|k|v flags seen, 9 q gathered, 10 partials
+                     published; merge blocks: 11 partial flags seen, 12 partials read,
+                     13 output published; 14 output flags seen (o step) */
+} am_gfx950_decode_layers_args;
+am_status_code am_gfx950_decode_layers(const am_gfx950_decode_layers_args* args, void* hip_stream);
+int64_t am_gfx950_decode_layers_workspace_bytes(int64_t hidden, int64_t hq, int64_t hkv, int64_t head_dim,
+                                                int64_t ffn);
+/* Host-side check of the scalar arguments and (when host_layers != NULL, a host copy
+ * of args->layers) of every layer's weight formats, shapes and alignment. */
+am_status_code am_gfx950_decode_layers_validate(const am_gfx950_decode_layers_args* args,
+                                                const am_gfx950_decode_layer* host_layers);
+/* *out = 1 when a launch on this workspace ended early because a cross-block wait
+ * timed out (the grid was not resident at once); the workspace must then be
+ * zero-filled again.  Synchronous. */
+am_status_code am_gfx950_decode_layers_aborted(const void* workspace, int32_t* out);
+
 /* Library / device information. */
 int32_t am_gfx950_device_count(void);
 const char* am_gfx950_version(void);

@@ -85,6 +85,10 @@ typedef struct am_session_options {
   int32_t use_graph;    /* 1: replay decode steps as a HIP graph */
   int32_t batch;        /* sequences decoded together, 1..16 (0 means 1); > 1 needs the
                            fused plan, bf16 activations and bf16/int8/int4 weights */
+  int32_t persistent_decode; /* 1: batch-1 fused decode as one persistent launch for
+                                all layers (am_gfx950_decode_layers); session creation
+                                fails when the model does not qualify.  0 or -1: the
+                                per-op fused plan (default) */
 } am_session_options;
 
 am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out);
@@ -116,6 +120,8 @@ int64_t am_session_position(am_session* s);
 int64_t am_session_row_position(am_session* s, int64_t row);
 /* Number of kernels launched per decode step by the active decode plan. */
 int64_t am_session_decode_plan_size(am_session* s);
+/* 1 when the session decodes with the persistent all-layers kernel, else 0. */
+int32_t am_session_persistent_decode(am_session* s);
 
 /* Per-op-type kernel time of eager decode steps, measured with HIP events on the
  * session stream around every step of the decode plan.  Runs n steps eagerly and
