@@ -1,0 +1,573 @@
+// Hugging Face Llama checkpoint reader: see hf_checkpoint.h.
+#include "hf_checkpoint.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cerrno>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <set>
+#include <sstream>
+
+namespace aethermind::hf {
+
+// ------------------------------------------------------------------ JSON
+const Json* Json::Get(std::string_view key) const {
+  if (kind != kObject) return nullptr;
+  for (const auto& [k, v] : obj)
+    if (k == key) return &v;
+  return nullptr;
+}
+
+namespace {
+
+class JsonParser {
+ public:
+  explicit JsonParser(std::string_view t) : t_(t) {}
+
+  StatusOr<Json> Document() {
+    Json v;
+    AM_RETURN_IF_ERROR(Value(&v, 0));
+    Ws();
+    if (i_ != t_.size()) return Err("trailing content");
+    return v;
+  }
+
+ private:
+  static constexpr int kMaxDepth = 64;
+
+  Status Err(const std::string& what) const {
+    return Status::InvalidArgument("JSON: " + what + " at offset " + std::to_string(i_));
+  }
+  void Ws() {
+    while (i_ < t_.size() && (t_[i_] == ' ' || t_[i_] == '\n' || t_[i_] == '\r' || t_[i_] == '\t')) ++i_;
+  }
+  bool Lit(std::string_view w) {
+    if (t_.substr(i_, w.size()) != w) return false;
+    i_ += w.size();
+    return true;
+  }
+
+  Status Value(Json* out, int depth) {
+    if (depth > kMaxDepth) return Err("nesting too deep");
+    Ws();
+    if (i_ >= t_.size()) return Err("unexpected end");
+    const char c = t_[i_];
+    if (c == '{') return Object(out, depth);
+    if (c == '[') return Array(out, depth);
+    if (c == '"') {
+      out->kind = Json::kString;
+      return String(&out->str);
+    }
+    if (Lit("true")) {
+      out->kind = Json::kBool;
+      out->boolean = true;
+      return Status::Ok();
+    }
+    if (Lit("false")) {
+      out->kind = Json::kBool;
+      return Status::Ok();
+    }
+    if (Lit("null")) {
+      out->kind = Json::kNull;
+      return Status::Ok();
+    }
+    return Number(out);
+  }
+
+  Status Object(Json* out, int depth) {
+    out->kind = Json::kObject;
+    ++i_;
+    Ws();
+    if (i_ < t_.size() && t_[i_] == '}') {
+      ++i_;
+      return Status::Ok();
+    }
+    for (;;) {
+      Ws();
+      std::string key;
+      if (i_ >= t_.size() || t_[i_] != '"') return Err("expected an object key");
+      AM_RETURN_IF_ERROR(String(&key));
+      Ws();
+      if (i_ >= t_.size() || t_[i_] != ':') return Err("expected ':'");
+      ++i_;
+      Json v;
+      AM_RETURN_IF_ERROR(Value(&v, depth + 1));
+      out->obj.emplace_back(std::move(key), std::move(v));
+      Ws();
+      if (i_ < t_.size() && t_[i_] == ',') {
+        ++i_;
+        continue;
+      }
+      if (i_ < t_.size() && t_[i_] == '}') {
+        ++i_;
+        return Status::Ok();
+      }
+      return Err("expected ',' or '}'");
+    }
+  }
+
+  Status Array(Json* out, int depth) {
+    out->kind = Json::kArray;
+    ++i_;
+    Ws();
+    if (i_ < t_.size() && t_[i_] == ']') {
+      ++i_;
+      return Status::Ok();
+    }
+    for (;;) {
+      Json v;
+      AM_RETURN_IF_ERROR(Value(&v, depth + 1));
+      out->arr.push_back(std::move(v));
+      Ws();
+      if (i_ < t_.size() && t_[i_] == ',') {
+        ++i_;
+        continue;
+      }
+      if (i_ < t_.size() && t_[i_] == ']') {
+        ++i_;
+        return Status::Ok();
+      }
+      return Err("expected ',' or ']'");
+    }
+  }
+
+  static void PutUtf8(std::string* s, uint32_t cp) {
+    if (cp < 0x80) {
+      s->push_back(static_cast<char>(cp));
+    } else if (cp < 0x800) {
+      s->push_back(static_cast<char>(0xC0 | (cp >> 6)));
+      s->push_back(static_cast<char>(0x80 | (cp & 0x3F)));
+    } else if (cp < 0x10000) {
+      s->push_back(static_cast<char>(0xE0 | (cp >> 12)));
+      s->push_back(static_cast<char>(0x80 | ((cp >> 6) & 0x3F)));
+      s->push_back(static_cast<char>(0x80 | (cp & 0x3F)));
+    } else {
+      s->push_back(static_cast<char>(0xF0 | (cp >> 18)));
+      s->push_back(static_cast<char>(0x80 | ((cp >> 12) & 0x3F)));
+      s->push_back(static_cast<char>(0x80 | ((cp >> 6) & 0x3F)));
+      s->push_back(static_cast<char>(0x80 | (cp & 0x3F)));
+    }
+  }
+
+  Status Hex4(uint32_t* v) {
+    if (i_ + 4 > t_.size()) return Err("short \\u escape");
+    uint32_t x = 0;
+    for (int k = 0; k < 4; ++k) {
+      const char h = t_[i_++];
+      x <<= 4;
+      if (h >= '0' && h <= '9') x |= static_cast<uint32_t>(h - '0');
+      else if (h >= 'a' && h <= 'f') x |= static_cast<uint32_t>(h - 'a' + 10);
+      else if (h >= 'A' && h <= 'F') x |= static_cast<uint32_t>(h - 'A' + 10);
+      else return Err("bad \\u escape");
+    }
+    *v = x;
+    return Status::Ok();
+  }
+
+  Status String(std::string* out) {
+    ++i_;  // opening quote
+    for (;;) {
+      if (i_ >= t_.size()) return Err("unterminated string");
+      const char c = t_[i_++];
+      if (c == '"') return Status::Ok();
+      if (static_cast<unsigned char>(c) < 0x20) return Err("control character in string");
+      if (c != '\\') {
+        out->push_back(c);
+        continue;
+      }
+      if (i_ >= t_.size()) return Err("unterminated escape");
+      const char e = t_[i_++];
+      switch (e) {
+        case '"': out->push_back('"'); break;
+        case '\\': out->push_back('\\'); break;
+        case '/': out->push_back('/'); break;
+        case 'b': out->push_back('\b'); break;
+        case 'f': out->push_back('\f'); break;
+        case 'n': out->push_back('\n'); break;
+        case 'r': out->push_back('\r'); break;
+        case 't': out->push_back('\t'); break;
+        case 'u': {
+          uint32_t cp = 0;
+          AM_RETURN_IF_ERROR(Hex4(&cp));
+          if (cp >= 0xD800 && cp < 0xDC00) {  // surrogate pair
+            uint32_t lo = 0;
+            if (!Lit("\\u")) return Err("lone high surrogate");
+            AM_RETURN_IF_ERROR(Hex4(&lo));
+            if (lo < 0xDC00 || lo >= 0xE000) return Err("bad low surrogate");
+            cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+          }
+          PutUtf8(out, cp);
+          break;
+        }
+        default: return Err("unknown escape");
+      }
+    }
+  }
+
+  Status Number(Json* out) {
+    const size_t b = i_;
+    if (i_ < t_.size() && t_[i_] == '-') ++i_;
+    bool digits = false, integral = true;
+    while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') {
+      ++i_;
+      digits = true;
+    }
+    if (i_ < t_.size() && t_[i_] == '.') {
+      integral = false;
+      ++i_;
+      while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') ++i_;
+    }
+    if (i_ < t_.size() && (t_[i_] == 'e' || t_[i_] == 'E')) {
+      integral = false;
+      ++i_;
+      if (i_ < t_.size() && (t_[i_] == '+' || t_[i_] == '-')) ++i_;
+      while (i_ < t_.size() && t_[i_] >= '0' && t_[i_] <= '9') ++i_;
+    }
+    if (!digits) return Err("expected a value");
+    const std::string tok(t_.substr(b, i_ - b));
+    out->kind = Json::kNumber;
+    out->number = std::strtod(tok.c_str(), nullptr);
+    if (integral && tok[0] != '-') {
+      errno = 0;
+      const unsigned long long u = std::strtoull(tok.c_str(), nullptr, 10);
+      if (errno == 0) {
+        out->is_uint = true;
+        out->uint = u;
+      }
+    }
+    return Status::Ok();
+  }
+
+  std::string_view t_;
+  size_t i_ = 0;
+};
+
+bool CheckedMul(uint64_t a, uint64_t b, uint64_t* out) {
+  if (a != 0 && b > UINT64_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+
+StDType ParseDType(const std::string& s, uint64_t* elem_bytes) {
+  static const std::pair<const char*, uint64_t> kBytes[] = {
+      {"F64", 8}, {"F32", 4}, {"F16", 2}, {"BF16", 2}, {"I64", 8}, {"I32", 4}, {"I16", 2}, {"I8", 1},
+      {"U64", 8}, {"U32", 4}, {"U16", 2}, {"U8", 1},   {"BOOL", 1}, {"F8_E4M3", 1}, {"F8_E5M2", 1}};
+  *elem_bytes = 0;
+  for (const auto& [n, b] : kBytes)
+    if (s == n) *elem_bytes = b;
+  if (s == "F32") return StDType::kF32;
+  if (s == "F16") return StDType::kF16;
+  if (s == "BF16") return StDType::kBF16;
+  return StDType::kOther;
+}
+
+StatusOr<std::string> ReadFile(const std::string& path) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) return Status::NotFound("cannot open " + path);
+  std::ostringstream ss;
+  ss << f.rdbuf();
+  return ss.str();
+}
+
+bool FileExists(const std::string& path) {
+  struct stat st {};
+  return ::stat(path.c_str(), &st) == 0 && S_ISREG(st.st_mode);
+}
+
+}  // namespace
+
+StatusOr<Json> ParseJson(std::string_view text) { return JsonParser(text).Document(); }
+
+// ------------------------------------------------------------------ safetensors
+StatusOr<std::vector<TensorView>> ParseSafetensorsHeader(std::string_view header, const uint8_t* data_base,
+                                                         uint64_t data_size) {
+  auto doc = ParseJson(header);
+  if (!doc.ok()) return doc.status();
+  const Json& j = doc.value();
+  if (j.kind != Json::kObject) return Status::InvalidArgument("safetensors header must be a JSON object");
+  std::vector<TensorView> out;
+  std::vector<std::pair<uint64_t, uint64_t>> ranges;
+  std::set<std::string> names;
+  for (const auto& [name, e] : j.obj) {
+    if (name == "__metadata__") continue;
+    if (!names.insert(name).second) return Status::InvalidArgument("duplicate safetensors tensor name '" + name + "'");
+    if (e.kind != Json::kObject) return Status::InvalidArgument("safetensors tensor '" + name + "': entry is not an object");
+    const Json* dt = e.Get("dtype");
+    const Json* shape = e.Get("shape");
+    const Json* offs = e.Get("data_offsets");
+    if (dt == nullptr || dt->kind != Json::kString)
+      return Status::InvalidArgument("safetensors tensor '" + name + "': missing 'dtype'");
+    if (offs == nullptr || offs->kind != Json::kArray || offs->arr.size() != 2 || !offs->arr[0].is_uint ||
+        !offs->arr[1].is_uint)
+      return Status::InvalidArgument("safetensors tensor '" + name + "': missing or malformed 'data_offsets'");
+    TensorView v;
+    v.name = name;
+    v.dtype_text = dt->str;
+    uint64_t eb = 0;
+    v.dtype = ParseDType(dt->str, &eb);
+    if (eb == 0) return Status::InvalidArgument("safetensors tensor '" + name + "': unknown dtype '" + dt->str + "'");
+    uint64_t numel = 1;
+    if (shape != nullptr) {
+      if (shape->kind != Json::kArray) return Status::InvalidArgument("safetensors tensor '" + name + "': bad 'shape'");
+      for (const Json& d : shape->arr) {
+        if (!d.is_uint || d.uint > static_cast<uint64_t>(INT64_MAX))
+          return Status::InvalidArgument("safetensors tensor '" + name + "': negative or non-integer shape");
+        if (!CheckedMul(numel, d.uint, &numel))
+          return Status::OutOfRange("safetensors tensor '" + name + "': shape overflows");
+        v.shape.push_back(static_cast<int64_t>(d.uint));
+      }
+    }
+    const uint64_t b = offs->arr[0].uint, en = offs->arr[1].uint;
+    if (b > en) return Status::InvalidArgument("safetensors tensor '" + name + "': data_offsets begin > end");
+    if (en > data_size) return Status::OutOfRange("safetensors tensor '" + name + "': data outside the file");
+    uint64_t nbytes = 0;
+    if (!CheckedMul(numel, eb, &nbytes)) return Status::OutOfRange("safetensors tensor '" + name + "': size overflows");
+    if (nbytes != en - b)
+      return Status::InvalidArgument("safetensors tensor '" + name + "': shape and dtype do not match data_offsets");
+    v.data = data_base + b;
+    v.bytes = nbytes;
+    ranges.emplace_back(b, en);
+    out.push_back(std::move(v));
+  }
+  std::sort(ranges.begin(), ranges.end());
+  uint64_t at = 0;
+  for (const auto& [b, e] : ranges) {
+    if (b != at) return Status::InvalidArgument("safetensors data_offsets overlap or leave gaps");
+    at = e;
+  }
+  if (at != data_size) return Status::InvalidArgument("safetensors tensors do not cover the whole data region");
+  return out;
+}
+
+StatusOr<std::unique_ptr<MappedFile>> MappedFile::Open(const std::string& path) {
+  const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return Status::NotFound("cannot open " + path + ": " + std::strerror(errno));
+  struct stat st {};
+  if (::fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
+    ::close(fd);
+    return Status::InvalidArgument(path + " is not a regular file");
+  }
+  std::unique_ptr<MappedFile> f(new MappedFile());
+  f->size_ = static_cast<uint64_t>(st.st_size);
+  if (f->size_ > 0) {
+    void* p = ::mmap(nullptr, f->size_, PROT_READ, MAP_PRIVATE, fd, 0);
+    if (p == MAP_FAILED) {
+      ::close(fd);
+      return Status::Internal("mmap failed for " + path);
+    }
+    (void)::madvise(p, f->size_, MADV_SEQUENTIAL);  // tensors are streamed in file order
+    f->data_ = static_cast<const uint8_t*>(p);
+  }
+  ::close(fd);
+  return f;
+}
+
+MappedFile::~MappedFile() {
+  if (data_ != nullptr) (void)::munmap(const_cast<uint8_t*>(data_), size_);
+}
+
+// ------------------------------------------------------------------ config
+namespace {
+StatusOr<int64_t> PosInt(const Json& cfg, const char* key, bool required, int64_t dflt) {
+  const Json* v = cfg.Get(key);
+  if (v == nullptr || v->kind == Json::kNull) {
+    if (required) return Status::InvalidArgument(std::string("config.json: missing '") + key + "'");
+    return dflt;
+  }
+  if (!v->is_uint || v->uint == 0 || v->uint > (uint64_t{1} << 31))
+    return Status::InvalidArgument(std::string("config.json: '") + key + "' must be a positive integer");
+  return static_cast<int64_t>(v->uint);
+}
+}  // namespace
+
+StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view text) {
+  auto doc = ParseJson(text);
+  if (!doc.ok()) return doc.status();
+  const Json& c = doc.value();
+  if (c.kind != Json::kObject) return Status::InvalidArgument("config.json must be a JSON object");
+  const Json* mt = c.Get("model_type");
+  if (mt == nullptr || mt->kind != Json::kString) return Status::InvalidArgument("config.json: 'model_type' must be provided");
+  if (mt->str != "llama") return Status::InvalidArgument("config.json: only model_type=llama is supported");
+  LlamaConfig m;
+  auto get = [&](const char* k, bool req, int64_t d, int64_t* out) -> Status {
+    auto v = PosInt(c, k, req, d);
+    if (!v.ok()) return v.status();
+    *out = v.value();
+    return Status::Ok();
+  };
+  AM_RETURN_IF_ERROR(get("hidden_size", true, 0, &m.hidden));
+  AM_RETURN_IF_ERROR(get("intermediate_size", true, 0, &m.ffn));
+  AM_RETURN_IF_ERROR(get("num_hidden_layers", true, 0, &m.num_layers));
+  AM_RETURN_IF_ERROR(get("num_attention_heads", true, 0, &m.num_q_heads));
+  AM_RETURN_IF_ERROR(get("num_key_value_heads", false, m.num_q_heads, &m.num_kv_heads));
+  AM_RETURN_IF_ERROR(get("vocab_size", true, 0, &m.vocab));
+  if (m.hidden % m.num_q_heads != 0)
+    return Status::InvalidArgument("config.json: hidden_size must be divisible by num_attention_heads");
+  AM_RETURN_IF_ERROR(get("head_dim", false, m.hidden / m.num_q_heads, &m.head_dim));
+  if (m.head_dim != m.hidden / m.num_q_heads)
+    return Status::InvalidArgument("config.json: head_dim must equal hidden_size / num_attention_heads");
+  if (m.num_kv_heads > m.num_q_heads || m.num_q_heads % m.num_kv_heads != 0)
+    return Status::InvalidArgument("config.json: num_attention_heads must be a multiple of num_key_value_heads");
+  if (const Json* e = c.Get("rms_norm_eps"); e != nullptr) {
+    if (e->kind != Json::kNumber || !(e->number > 0.0)) return Status::InvalidArgument("config.json: rms_norm_eps must be positive");
+    m.rms_eps = e->number;
+  }
+  if (const Json* t = c.Get("rope_theta"); t != nullptr) {
+    if (t->kind != Json::kNumber || !(t->number > 0.0)) return Status::InvalidArgument("config.json: rope_theta must be positive");
+    m.rope_theta = t->number;
+  }
+  if (const Json* t = c.Get("tie_word_embeddings"); t != nullptr && t->kind == Json::kBool) m.tie_word_embeddings = t->boolean;
+  for (const char* k : {"attention_bias", "mlp_bias"})
+    if (const Json* b = c.Get(k); b != nullptr && b->kind == Json::kBool && b->boolean)
+      return Status::InvalidArgument(std::string("config.json: ") + k + " is not supported");
+  for (const char* k : {"rope_scaling", "rope_parameters"})
+    if (const Json* r = c.Get(k); r != nullptr && r->kind != Json::kNull)
+      return Status::InvalidArgument("config.json: RoPE scaling is not supported");
+  if (const Json* a = c.Get("hidden_act"); a != nullptr && a->kind == Json::kString && a->str != "silu")
+    return Status::InvalidArgument("config.json: hidden_act must be silu");
+  return m;
+}
+
+std::string LayerName(int64_t layer, std::string_view suffix) {
+  return "model.layers." + std::to_string(layer) + std::string(suffix);
+}
+
+// ------------------------------------------------------------------ checkpoint
+namespace {
+Status AddFile(const std::string& path, std::vector<std::unique_ptr<MappedFile>>* files,
+               std::map<std::string, TensorView>* tensors, const std::map<std::string, std::string>* owner,
+               const std::string& shard_name) {
+  auto mf = MappedFile::Open(path);
+  if (!mf.ok()) return mf.status();
+  const MappedFile& f = *mf.value();
+  if (f.size() < 8) return Status::InvalidArgument(path + ": too small for a safetensors header");
+  uint64_t hl = 0;
+  for (int i = 0; i < 8; ++i) hl |= static_cast<uint64_t>(f.data()[i]) << (8 * i);
+  if (hl > f.size() - 8) return Status::InvalidArgument(path + ": header length exceeds the file");
+  const std::string_view header(reinterpret_cast<const char*>(f.data() + 8), static_cast<size_t>(hl));
+  auto views = ParseSafetensorsHeader(header, f.data() + 8 + hl, f.size() - 8 - hl);
+  if (!views.ok()) return Status::InvalidArgument(path + ": " + views.status().message());
+  for (auto& v : views.value()) {
+    if (owner != nullptr) {
+      const auto it = owner->find(v.name);
+      if (it == owner->end())
+        return Status::InvalidArgument(path + ": tensor '" + v.name + "' is not listed in the index");
+      if (it->second != shard_name)
+        return Status::FailedPrecondition("the index assigns '" + v.name + "' to " + it->second + ", found in " + shard_name);
+    }
+    const std::string name = v.name;
+    if (!tensors->emplace(name, std::move(v)).second)
+      return Status::AlreadyExists("tensor '" + name + "' appears in more than one shard");
+  }
+  files->push_back(std::move(mf.value()));
+  return Status::Ok();
+}
+
+Status ExpectTensor(const std::map<std::string, TensorView>& t, const std::string& name, std::vector<int64_t> shape) {
+  const auto it = t.find(name);
+  if (it == t.end()) return Status::InvalidArgument("checkpoint is missing required weight '" + name + "'");
+  const TensorView& v = it->second;
+  if (v.dtype == StDType::kOther)
+    return Status::InvalidArgument("tensor " + name + ": dtype " + v.dtype_text + " (expected F32, F16 or BF16)");
+  if (v.shape != shape) {
+    std::string want, got;
+    for (int64_t d : shape) want += std::to_string(d) + ",";
+    for (int64_t d : v.shape) got += std::to_string(d) + ",";
+    return Status::InvalidArgument("tensor " + name + ": shape [" + got + "] (expected [" + want + "])");
+  }
+  return Status::Ok();
+}
+}  // namespace
+
+StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir) {
+  std::unique_ptr<Checkpoint> ck(new Checkpoint());
+  auto cfg_text = ReadFile(dir + "/config.json");
+  if (!cfg_text.ok()) return cfg_text.status();
+  auto cfg = ParseLlamaConfig(cfg_text.value());
+  if (!cfg.ok()) return cfg.status();
+  ck->cfg_ = cfg.value();
+  const std::string single = dir + "/model.safetensors", index = dir + "/model.safetensors.index.json";
+  if (FileExists(index)) {
+    auto idx_text = ReadFile(index);
+    if (!idx_text.ok()) return idx_text.status();
+    auto idx = ParseJson(idx_text.value());
+    if (!idx.ok()) return Status::InvalidArgument("model.safetensors.index.json: " + idx.status().message());
+    const Json* wm = idx.value().Get("weight_map");
+    if (wm == nullptr || wm->kind != Json::kObject)
+      return Status::InvalidArgument("model.safetensors.index.json: missing 'weight_map'");
+    std::map<std::string, std::string> owner;
+    std::set<std::string> shards;
+    for (const auto& [name, file] : wm->obj) {
+      if (file.kind != Json::kString) return Status::InvalidArgument("weight_map: shard name must be a string");
+      // a shard is a plain file name inside the model directory
+      if (file.str.empty() || file.str.find('/') != std::string::npos || file.str == "." || file.str == "..")
+        return Status::InvalidArgument("weight_map: shard '" + file.str + "' escapes the model directory");
+      owner[name] = file.str;
+      shards.insert(file.str);
+    }
+    for (const auto& s : shards) AM_RETURN_IF_ERROR(AddFile(dir + "/" + s, &ck->files_, &ck->tensors_, &owner, s));
+    for (const auto& [name, s] : owner)
+      if (ck->tensors_.find(name) == ck->tensors_.end())
+        return Status::NotFound("tensor '" + name + "' listed in the index is missing from " + s);
+  } else if (FileExists(single)) {
+    AM_RETURN_IF_ERROR(AddFile(single, &ck->files_, &ck->tensors_, nullptr, ""));
+  } else {
+    return Status::NotFound(dir + ": neither model.safetensors nor model.safetensors.index.json");
+  }
+
+  // names, dtypes and shapes against the config (hf_weight_resolver.cpp:17-110,
+  // hf_model_validator.cpp:168-644); every other tensor is rejected
+  const LlamaConfig& c = ck->cfg_;
+  const int64_t H = c.hidden, Q = c.num_q_heads * c.head_dim, KV = c.num_kv_heads * c.head_dim;
+  std::set<std::string> known;
+  auto need = [&](const std::string& n, std::vector<int64_t> shape) -> Status {
+    known.insert(n);
+    return ExpectTensor(ck->tensors_, n, std::move(shape));
+  };
+  AM_RETURN_IF_ERROR(need("model.embed_tokens.weight", {c.vocab, H}));
+  AM_RETURN_IF_ERROR(need("model.norm.weight", {H}));
+  if (ck->tensors_.count("lm_head.weight")) {
+    AM_RETURN_IF_ERROR(need("lm_head.weight", {c.vocab, H}));
+  } else if (!c.tie_word_embeddings) {
+    return Status::InvalidArgument("required weight 'lm_head.weight' is missing and tie_word_embeddings is false");
+  }
+  for (int64_t l = 0; l < c.num_layers; ++l) {
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".input_layernorm.weight"), {H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".post_attention_layernorm.weight"), {H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.q_proj.weight"), {Q, H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.k_proj.weight"), {KV, H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.v_proj.weight"), {KV, H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.o_proj.weight"), {H, Q}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.gate_proj.weight"), {c.ffn, H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.up_proj.weight"), {c.ffn, H}));
+    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.down_proj.weight"), {H, c.ffn}));
+  }
+  for (const auto& [name, v] : ck->tensors_)
+    if (!known.count(name)) return Status::InvalidArgument("unexpected tensor found: " + name);
+  return ck;
+}
+
+const TensorView* Checkpoint::Find(const std::string& name) const {
+  const auto it = tensors_.find(name);
+  return it == tensors_.end() ? nullptr : &it->second;
+}
+
+const TensorView& Checkpoint::LmHead() const {
+  const TensorView* h = Find("lm_head.weight");
+  return h != nullptr ? *h : Get("model.embed_tokens.weight");
+}
+
+uint64_t Checkpoint::total_bytes() const {
+  uint64_t b = 0;
+  for (const auto& [n, v] : tensors_) b += v.bytes;
+  return b;
+}
+
+}  // namespace aethermind::hf

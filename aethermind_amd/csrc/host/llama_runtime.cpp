@@ -23,6 +23,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <memory>
 #include <vector>
 
@@ -30,6 +31,7 @@
 #include "am_runtime.h"
 #include "gfx950_backend.h"
 #include "am_launch_timing.h"
+#include "hf_checkpoint.h"
 
 namespace am {
 am_status_code SetLastError(am_status_code code, const char* msg);
@@ -185,7 +187,8 @@ class LlamaModel {
     return Status::Ok();
   }
 
-  Status CreateSynthetic(uint64_t seed) {
+  // One device slab for every weight of the model (layout in the file header).
+  Status Allocate() {
     AM_RETURN_IF_ERROR(Validate());
     const auto& c = cfg;
     const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers, d = c.head_dim;
@@ -223,7 +226,24 @@ class LlamaModel {
     cos_tab = static_cast<float*>(slab.Take(static_cast<size_t>(c.max_tokens) * (d / 2) * 4));
     sin_tab = static_cast<float*>(slab.Take(static_cast<size_t>(c.max_tokens) * (d / 2) * 4));
     if (slab.off > slab.size) return Status::Internal("weight slab overflow");
+    return Status::Ok();
+  }
 
+  Status FillRope() {
+    const auto& c = cfg;
+    const int64_t d = c.head_dim;
+    std::vector<float> ct(static_cast<size_t>(c.max_tokens) * (d / 2)), stb(ct.size());
+    AM_C_OK(am_gfx950_rope_table(c.max_tokens, d, c.rope_theta, ct.data(), stb.data()));
+    AM_HIP_OK(hipMemcpyAsync(cos_tab, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, stream));
+    AM_HIP_OK(hipMemcpyAsync(sin_tab, stb.data(), stb.size() * 4, hipMemcpyHostToDevice, stream));
+    AM_HIP_OK(hipStreamSynchronize(stream));
+    return Status::Ok();
+  }
+
+  Status CreateSynthetic(uint64_t seed) {
+    AM_RETURN_IF_ERROR(Allocate());
+    const auto& c = cfg;
+    const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers;
     // scratch for one logical source matrix (largest: lm_head / embedding)
     const int64_t max_elems = std::max({V * H, F * H, QRows() * H});
     void* scratch = nullptr;
@@ -245,14 +265,93 @@ class LlamaModel {
       }
       AM_C_OK(am_gfx950_fill(final_norm, c.act_dtype, H, 1.0f, stream));
       AM_RETURN_IF_ERROR(SynthInto(seed, kLmHeadId, V, H, scratch, lm_head, 0));
-      std::vector<float> ct(static_cast<size_t>(c.max_tokens) * (d / 2)), stb(ct.size());
-      AM_C_OK(am_gfx950_rope_table(c.max_tokens, d, c.rope_theta, ct.data(), stb.data()));
-      AM_HIP_OK(hipMemcpyAsync(cos_tab, ct.data(), ct.size() * 4, hipMemcpyHostToDevice, stream));
-      AM_HIP_OK(hipMemcpyAsync(sin_tab, stb.data(), stb.size() * 4, hipMemcpyHostToDevice, stream));
-      AM_HIP_OK(hipStreamSynchronize(stream));
-      return Status::Ok();
+      return FillRope();
     }();
     (void)hipFree(scratch);
+    return st;
+  }
+
+  // Streams a Hugging Face checkpoint into the slab: each tensor goes from the
+  // memory-mapped shard through a pinned two-buffer ring (host copy of one buffer
+  // overlaps the DMA of the other) into a device staging area, then is converted,
+  // quantized and placed by the repack kernels (q|k|v concatenated, gate|up stacked,
+  // norms and embedding in the activation dtype).
+  Status LoadCheckpoint(const hf::Checkpoint& ck) {
+    AM_RETURN_IF_ERROR(Allocate());
+    const auto& c = cfg;
+    const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers;
+    const int32_t act_fmt = c.act_dtype == AM_DT_BF16 ? AM_WF_BF16 : AM_WF_F32;
+    uint64_t max_bytes = ck.LmHead().bytes;
+    max_bytes = std::max<uint64_t>(max_bytes, ck.Get("model.embed_tokens.weight").bytes);
+    for (int64_t l = 0; l < L; ++l)
+      for (const char* sfx : {".mlp.gate_proj.weight", ".mlp.down_proj.weight", ".self_attn.q_proj.weight"})
+        max_bytes = std::max<uint64_t>(max_bytes, ck.Get(hf::LayerName(l, sfx)).bytes);
+    constexpr size_t kRing = size_t{32} << 20;
+    void* dsrc = nullptr;
+    void* pinned[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    Status st = [&]() -> Status {
+      AM_HIP_OK(hipMalloc(&dsrc, static_cast<size_t>(max_bytes)));
+      for (int i = 0; i < 2; ++i) {
+        AM_HIP_OK(hipHostMalloc(&pinned[i], kRing, hipHostMallocDefault));
+        AM_HIP_OK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+      }
+      int slot = 0;
+      auto upload = [&](const hf::TensorView& t) -> Status {
+        for (uint64_t off = 0; off < t.bytes;) {
+          const size_t n = static_cast<size_t>(std::min<uint64_t>(kRing, t.bytes - off));
+          if (pending[slot]) AM_HIP_OK(hipEventSynchronize(ev[slot]));
+          std::memcpy(pinned[slot], t.data + off, n);
+          AM_HIP_OK(hipMemcpyAsync(static_cast<char*>(dsrc) + off, pinned[slot], n, hipMemcpyHostToDevice, stream));
+          AM_HIP_OK(hipEventRecord(ev[slot], stream));
+          pending[slot] = true;
+          off += n;
+          slot ^= 1;
+        }
+        return Status::Ok();
+      };
+      // tensor -> rows [row_off, row_off + rows) of dst (the stream orders the next
+      // upload after the kernel that reads the staging area)
+      auto place = [&](const hf::TensorView& t, int64_t rows, const am_gfx950_weight& dst, int64_t row_off) -> Status {
+        AM_RETURN_IF_ERROR(upload(t));
+        am_gfx950_quantize_args qa{};
+        qa.src = dsrc;
+        qa.src_dtype = t.dtype == hf::StDType::kF32 ? AM_DT_F32 : t.dtype == hf::StDType::kF16 ? AM_DT_F16 : AM_DT_BF16;
+        qa.src_rows = rows;
+        qa.dst = dst;
+        qa.dst_row_offset = row_off;
+        qa.dst_row_stride = 1;
+        if (dst.format >= AM_WF_INT8)
+          AM_C_OK(am_gfx950_quantize(&qa, stream));
+        else
+          AM_C_OK(am_gfx950_pack_plain(&qa, stream));
+        return Status::Ok();
+      };
+      auto act = [&](void* p, int64_t rows) { return am_gfx950_weight{p, nullptr, rows, H, act_fmt, 0}; };
+      auto get = [&](int64_t l, const char* sfx) -> const hf::TensorView& { return ck.Get(hf::LayerName(l, sfx)); };
+      AM_RETURN_IF_ERROR(place(ck.Get("model.embed_tokens.weight"), V, act(embed, V), 0));
+      for (int64_t l = 0; l < L; ++l) {
+        AM_RETURN_IF_ERROR(place(get(l, ".input_layernorm.weight"), 1, act(in_norm[l], 1), 0));
+        AM_RETURN_IF_ERROR(place(get(l, ".post_attention_layernorm.weight"), 1, act(post_norm[l], 1), 0));
+        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.q_proj.weight"), QRows(), qkv[l], 0));
+        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.k_proj.weight"), KvRows(), qkv[l], QRows()));
+        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.v_proj.weight"), KvRows(), qkv[l], QRows() + KvRows()));
+        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.o_proj.weight"), H, o[l], 0));
+        AM_RETURN_IF_ERROR(place(get(l, ".mlp.gate_proj.weight"), F, gate_up[l], 0));
+        AM_RETURN_IF_ERROR(place(get(l, ".mlp.up_proj.weight"), F, gate_up[l], F));
+        AM_RETURN_IF_ERROR(place(get(l, ".mlp.down_proj.weight"), H, down[l], 0));
+      }
+      AM_RETURN_IF_ERROR(place(ck.Get("model.norm.weight"), 1, act(final_norm, 1), 0));
+      AM_RETURN_IF_ERROR(place(ck.LmHead(), V, lm_head, 0));
+      return FillRope();  // synchronises the stream
+    }();
+    (void)hipStreamSynchronize(stream);
+    for (int i = 0; i < 2; ++i) {
+      if (ev[i]) (void)hipEventDestroy(ev[i]);
+      if (pinned[i]) (void)hipHostFree(pinned[i]);
+    }
+    if (dsrc) (void)hipFree(dsrc);
     return st;
   }
 };
@@ -1000,6 +1099,58 @@ am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* 
   const Status s = m->impl->CreateSynthetic(seed);
   if (!s.ok()) return Ret(s);
   *out = m.release();
+  return AM_STATUS_OK;
+}
+
+am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
+                                am_model** out) {
+  if (!rt || !model_dir || !opt || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_load_hf: null argument");
+  auto ck = aethermind::hf::Checkpoint::Open(model_dir);
+  if (!ck.ok()) return Ret(ck.status());
+  const auto& hc = ck.value()->config();
+  am_model_config mc{};
+  mc.num_layers = static_cast<int32_t>(hc.num_layers);
+  mc.hidden = static_cast<int32_t>(hc.hidden);
+  mc.num_q_heads = static_cast<int32_t>(hc.num_q_heads);
+  mc.num_kv_heads = static_cast<int32_t>(hc.num_kv_heads);
+  mc.head_dim = static_cast<int32_t>(hc.head_dim);
+  mc.ffn = static_cast<int32_t>(hc.ffn);
+  mc.vocab = static_cast<int32_t>(hc.vocab);
+  mc.rms_eps = static_cast<float>(hc.rms_eps);
+  mc.rope_theta = hc.rope_theta;
+  mc.act_dtype = opt->act_dtype;
+  mc.weight_format = opt->weight_format;
+  mc.group_size = opt->group_size;
+  mc.max_tokens = opt->max_tokens;
+  mc.max_prefill_chunk = opt->max_prefill_chunk;
+  auto m = std::make_unique<am_model>();
+  m->rt = rt;
+  m->impl = std::make_unique<LlamaModel>();
+  m->impl->cfg = mc;
+  m->impl->stream = rt->stream;
+  const Status s = m->impl->LoadCheckpoint(*ck.value());
+  if (!s.ok()) return Ret(s);
+  *out = m.release();
+  return AM_STATUS_OK;
+}
+
+am_status_code am_hf_inspect(const char* model_dir, am_model_config* cfg, int64_t* n_tensors, int64_t* total_bytes) {
+  if (!model_dir || !cfg) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "hf_inspect: null argument");
+  auto ck = aethermind::hf::Checkpoint::Open(model_dir);
+  if (!ck.ok()) return Ret(ck.status());
+  const auto& hc = ck.value()->config();
+  *cfg = am_model_config{};
+  cfg->num_layers = static_cast<int32_t>(hc.num_layers);
+  cfg->hidden = static_cast<int32_t>(hc.hidden);
+  cfg->num_q_heads = static_cast<int32_t>(hc.num_q_heads);
+  cfg->num_kv_heads = static_cast<int32_t>(hc.num_kv_heads);
+  cfg->head_dim = static_cast<int32_t>(hc.head_dim);
+  cfg->ffn = static_cast<int32_t>(hc.ffn);
+  cfg->vocab = static_cast<int32_t>(hc.vocab);
+  cfg->rms_eps = static_cast<float>(hc.rms_eps);
+  cfg->rope_theta = hc.rope_theta;
+  if (n_tensors) *n_tensors = static_cast<int64_t>(ck.value()->num_tensors());
+  if (total_bytes) *total_bytes = static_cast<int64_t>(ck.value()->total_bytes());
   return AM_STATUS_OK;
 }
 

@@ -144,8 +144,10 @@ __global__ __launch_bounds__(256) void token_ids_kernel(uint64_t key, int64_t vo
 
 // ---------------- quantization into device tiles ----------------
 __device__ __forceinline__ float load_src(const void* src, int32_t dt, int64_t i) {
-  return dt == AM_DT_F32 ? static_cast<const float*>(src)[i]
-                         : bf16_bits_to_f32(static_cast<const uint16_t*>(src)[i]);
+  if (dt == AM_DT_F32) return static_cast<const float*>(src)[i];
+  const uint16_t b = static_cast<const uint16_t*>(src)[i];
+  if (dt == AM_DT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, b));  // exact
+  return bf16_bits_to_f32(b);
 }
 
 __device__ __forceinline__ float block_max_256(float v, float* red) {
@@ -331,7 +333,8 @@ extern "C" am_status_code am_gfx950_synth_token_ids(uint64_t seed, uint64_t stre
 namespace {
 am_status_code CheckQuantArgs(const am_gfx950_quantize_args* a) {
   AM_CHECK_ARG(a != nullptr && a->src != nullptr, "quantize: null args");
-  AM_CHECK_ARG(a->src_dtype == AM_DT_F32 || a->src_dtype == AM_DT_BF16, "quantize: src dtype must be f32 or bf16");
+  AM_CHECK_ARG(a->src_dtype == AM_DT_F32 || a->src_dtype == AM_DT_BF16 || a->src_dtype == AM_DT_F16,
+               "quantize: src dtype must be f32, bf16 or f16");
   AM_CHECK_ARG(a->dst.data != nullptr && a->dst.n > 0 && a->dst.k > 0, "quantize: bad destination");
   AM_CHECK_ARG(a->dst_row_offset >= 0 && a->dst_row_stride >= 1, "quantize: bad row mapping");
   AM_CHECK_ARG(a->src_rows > 0 && a->src_rows <= 0x7FFFFFFF, "quantize: src_rows must be positive");

@@ -130,6 +130,11 @@ class ModelConfig(C.Structure):
                 ("max_prefill_chunk", i32)]
 
 
+class ModelLoadOptions(C.Structure):
+    _fields_ = [("act_dtype", i32), ("weight_format", i32), ("group_size", i32), ("max_tokens", i32),
+                ("max_prefill_chunk", i32)]
+
+
 class SessionOptions(C.Structure):
     _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32)]
 
@@ -183,6 +188,8 @@ _SIGS = {
     "am_model_create_synthetic": (i32, [vp, C.POINTER(ModelConfig), u64, C.POINTER(vp)]),
     "am_model_destroy": (None, [vp]),
     "am_model_weight": (i32, [vp, i32, i32, C.POINTER(Weight)]),
+    "am_model_load_hf": (i32, [vp, C.c_char_p, C.POINTER(ModelLoadOptions), C.POINTER(vp)]),
+    "am_hf_inspect": (i32, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(i64), C.POINTER(i64)]),
     "am_model_buffer": (i32, [vp, i32, i32, C.POINTER(vp), C.POINTER(i64)]),
     "am_model_weight_bytes_total": (i64, [vp]),
     "am_session_create": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),

@@ -223,7 +223,7 @@ int64_t am_gfx950_argmax_workspace_bytes(int64_t rows);
 
 /* ---------------- weight loader / repack (WeightPrepackPlanner + prepacker) -------- */
 
-/* Quantize a device fp32/bf16 matrix src [n][k] into a device weight of `format`
+/* Quantize a device fp32/bf16/fp16 matrix src [n][k] into a device weight of `format`
  * (INT8 per-channel or INT4 group) following the build SPEC:
  *   INT8: s = max|w|/127 (1 for an all-zero row), q = clamp(rint(w/s), -127, 127)
  *   INT4: s = fp16(max|w|/7) per group, q = clamp(rint(w/s), -8, 7), q = 0 if s == 0
@@ -238,8 +238,9 @@ typedef struct am_gfx950_quantize_args {
 } am_gfx950_quantize_args;
 am_status_code am_gfx950_quantize(const am_gfx950_quantize_args* args, void* hip_stream);
 
-/* Copies a device fp32/bf16 matrix into an F32/BF16 device weight, same row mapping
- * as am_gfx950_quantize (dst_row_offset / dst_row_stride). */
+/* Copies a device fp32/bf16/fp16 matrix into an F32/BF16 device weight (one RNE
+ * rounding when narrowing), same row mapping as am_gfx950_quantize
+ * (dst_row_offset / dst_row_stride). */
 am_status_code am_gfx950_pack_plain(const am_gfx950_quantize_args* args, void* hip_stream);
 
 /* Converts the logical INT4 interchange format (uint8 [n][k/2], low nibble = even k,

@@ -76,6 +76,26 @@ am_status_code am_synth_token_ids_host(uint64_t seed, uint64_t stream, int64_t v
 am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* cfg, uint64_t seed,
                                          am_model** out);
 void am_model_destroy(am_model* m);
+/* Loads a Hugging Face Llama checkpoint directory (config.json plus model.safetensors
+ * or model.safetensors.index.json with its shards; F32/F16/BF16 tensors) straight into
+ * HBM, converted to the requested activation dtype and weight format (quantized on the
+ * device).  The reference's HF reader / validator / weight resolver contract
+ * (hf_directory_reader.cpp:333-412, hf_model_validator.cpp:168-644,
+ * hf_weight_resolver.cpp:17-110): model_type llama, no bias, no RoPE scaling, every
+ * layer tensor present with its exact shape, no unknown tensors, lm_head.weight absent
+ * only with tie_word_embeddings (the embedding is then the head). */
+typedef struct am_model_load_options {
+  int32_t act_dtype;         /* AM_DT_F32 or AM_DT_BF16 */
+  int32_t weight_format;     /* am_weight_format */
+  int32_t group_size;        /* INT4 group (SPEC: 128) */
+  int32_t max_tokens;        /* static KV capacity (positions) */
+  int32_t max_prefill_chunk; /* rows per prefill pass */
+} am_model_load_options;
+am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
+                                am_model** out);
+/* Host only (no device work): reads and validates the checkpoint directory and fills
+ * the shape fields of cfg (num_layers .. rope_theta), the tensor count and bytes. */
+am_status_code am_hf_inspect(const char* model_dir, am_model_config* cfg, int64_t* n_tensors, int64_t* total_bytes);
 am_status_code am_model_weight(am_model* m, int32_t layer, int32_t role, am_gfx950_weight* out);
 am_status_code am_model_buffer(am_model* m, int32_t kind, int32_t layer, void** ptr, int64_t* bytes);
 int64_t am_model_weight_bytes_total(am_model* m); /* repacked linear weights incl. scales */
