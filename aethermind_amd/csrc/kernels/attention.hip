@@ -207,23 +207,42 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
   __syncthreads();
   if (!last) return;
   // Merge the splits: thread t owns (head, dim) pairs t, t + NT, ...; the records are
-  // read with device-scope loads.
+  // read with device-scope loads, kMergeBatch splits at a time with all of a batch's
+  // loads in flight together (slots past the last split reread it and are skipped).
+  // Each batch rescales the running sums to the batch's new maximum.
+  constexpr int kMergeBatch = 8;
   const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
   const int64_t rs = G * (D + 2);  // record stride between splits
   for (int t = threadIdx.x; t < G * D; t += NT) {
     const int hh = t / D, dd = t % D;
     const float* base = base0 + hh * (D + 2);
-    float mx = -INFINITY;
-    for (int64_t sp = 0; sp < nsplit; ++sp)
-      mx = fmaxf(mx, __hip_atomic_load(&base[sp * rs], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float den = 0.0f, acc = 0.0f;
-    if (mx != -INFINITY) {
-      for (int64_t sp = 0; sp < nsplit; ++sp) {
-        const float* r = base + sp * rs;
-        const float c = exp2f(__hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
-        den = fmaf(__hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, den);
-        acc = fmaf(__hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), c, acc);
+    float mx = -INFINITY, den = 0.0f, acc = 0.0f;
+    for (int64_t s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+      float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const float* r = base + (s0 + u < nsplit ? s0 + u : nsplit - 1) * rs;
+        mv[u] = __hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lv[u] = __hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ov[u] = __hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+      float bm = mx;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (s0 + u < nsplit) bm = fmaxf(bm, mv[u]);
+      if (bm == -INFINITY) continue;
+      const float c0 = exp2f(mx - bm);  // 0 while nothing has been summed
+      den *= c0;
+      acc *= c0;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (s0 + u < nsplit) {
+          const float c = exp2f(mv[u] - bm);
+          den = fmaf(lv[u], c, den);
+          acc = fmaf(ov[u], c, acc);
+        }
+      }
+      mx = bm;
     }
     T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
     A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
@@ -409,21 +428,27 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
 // grid = (splits, kv_heads, batch).  A block of kDecWaves waves owns one (row, kv head)
 // and a slice of positions; wave w takes the 32-position steps w, w + kDecWaves, ...
 // of the slice, with the next step's K and V loads in flight while a step computes.
-//   * Scores: S^T = K Q^T on v_mfma_f32_16x16x32_bf16, A = 16 cache rows (each lane
-//     loads 16 contiguous bytes of a K row), B = the G query heads of the group
-//     (columns >= G are zero).  Lane (j, h) receives the scores of head j for positions
-//     4h + r of a 16-position tile, so the softmax state of head j lives in the lanes
-//     with lane % 16 == j.  Products are exact and sums fp32; the log2(e)/sqrt(d)
-//     scale is applied to the fp32 scores.
-//   * O += P V on the same MFMA: the reduction index runs over positions, and the lane
-//     that holds a score is exactly the lane that supplies it as an A element (the k
-//     order of the product is free), so P never moves between lanes.  P is split into
-//     bf16 hi + lo parts (two MFMAs), which keeps it to about 16 significant bits.  V
-//     is the B operand with k = position; it is staged row-major in a per-wave LDS tile
-//     and gathered by column.
+// Nothing is staged in LDS on the way: every MFMA operand is built in the registers of
+// the lane that loaded it.
+//   * Scores: S^T = K Q^T on v_mfma_f32_16x16x32_bf16.  A = 16 cache rows (position
+//     16 tt + i of the step is row i of tile tt; each lane loads 16 contiguous bytes
+//     of its row per k step), B = the G query heads of the group (columns >= G are
+//     zero), loaded by every wave into registers.  Lane (j, h) receives the scores of
+//     head j for positions 16 tt + 4 h + r, so the softmax state of head j lives in
+//     the lanes with lane % 16 == j.  Products are exact and sums fp32; the
+//     log2(e)/sqrt(d) scale is applied to the fp32 scores.
+//   * O += P V on the same MFMA.  The reduction index runs over positions and its
+//     order is free: k slot e of lane group h is position 16 (e >> 2) + 4 h + (e & 3),
+//     exactly the positions whose scores lane (j, h) holds, so P never moves between
+//     lanes (A = P split into bf16 hi + lo parts, two MFMAs, about 16 significant
+//     bits).  The output column order is free too: lane n of tile t holds dimension
+//     (D/16) n + t.  So B lane (n, h) needs V[its 8 positions][(D/16) n + t] for
+//     t < D/16, which is exactly what it loads as 8 rows x D/16 contiguous columns
+//     (16 lanes cover a whole row, coalesced); tile t's operand is column t of that
+//     8 x D/16 block, gathered with byte permutes in the lane's own registers.
 //   * The per-wave states are merged in LDS, and split blocks merge through the same
 //     records and ticket as the general kernel.
-constexpr int kDecWaves = 8;
+constexpr int kDecWaves = 4;
 // Split policy of the decode kernel, measured on MI355X with a cold cache (the layer's
 // K/V evicted by the weight stream, as in decode): at least 128 positions per split
 // block and at most 8 split blocks per (row, kv head) minimise the kernel time from
@@ -435,14 +460,12 @@ constexpr int kDecMaxSplits = 8;
 template <int D, int G>
 __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnArgs p) {
   constexpr int NW = kDecWaves;
-  constexpr int KK = D / 32;                 // MFMA k steps of one score tile
-  constexpr int DT = D / 16;                 // 16-wide output tiles
-  constexpr int VR = D + 8;                  // padded LDS row of the staged V tile (bf16)
-  constexpr int VCH = 32 * (D / 8) / 64;     // 16-byte V pieces per lane per step
-  __shared__ __align__(16) uint16_t sv[NW][32 * VR];
+  constexpr int KK = D / 32;  // MFMA k steps of one score tile
+  constexpr int CW = D / 16;  // V columns per lane = output tiles
+  constexpr int VW = CW / 2;  // 32-bit words of one lane's V row piece
   __shared__ float sm_m[NW][G], sm_l[NW][G];
   __shared__ float sm_o[NW][G][D];
-  __shared__ uint4 sq[D / 32][64];  // the score B operand, per lane
+  __shared__ uint4 sq[NW][KK][64];  // each wave's copy of the score B operand
   __shared__ bool last;
 
   const int lane = threadIdx.x & 63;
@@ -463,19 +486,29 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
   const int64_t nsteps = (hi - lo + 31) / 32;
   const int64_t my = nsteps > wave ? (nsteps - wave + NW - 1) / NW : 0;  // this wave's steps
 
+  // B operand of the scores: lane (j, h) holds query head j of the group at
+  // d = 32 kk + 8 h .. +8; columns j >= G repeat head 0 and only feed score columns,
+  // softmax states and output rows that are never read.  Loaded first, so waiting for
+  // it never waits for the cache loads behind it; every wave keeps its own copy in
+  // LDS, so no block barrier (which would also drain the cache loads) is needed.
+  const uint16_t* qp = static_cast<const uint16_t*>(p.q) + (qr * p.hq + g * G + (j < G ? j : 0)) * D + 8 * h;
+  const uint4 q0 = *reinterpret_cast<const uint4*>(qp), q1 = *reinterpret_cast<const uint4*>(qp + 32);
+  uint4 q2 = q0, q3 = q1;
+  if constexpr (KK == 4) {
+    q2 = *reinterpret_cast<const uint4*>(qp + 64);
+    q3 = *reinterpret_cast<const uint4*>(qp + 96);
+  }
+
   const uint16_t* kbase = static_cast<const uint16_t*>(p.kc) + b * p.cbs + g * p.cap * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.vc) + b * p.cbs + g * p.cap * D;
 
   struct Buf {
-    uint4 k[2][KK];  // two 16-row score tiles
-    uint4 v[VCH];    // the step's 32 V rows, 16 bytes per lane per piece
+    uint4 k[2][KK];    // two 16-row score tiles
+    uint32_t v[8][VW];  // V[position of k slot c][CW j .. CW j + CW)
   };
-  // Loads step (clamped to this wave's last step; rows past the slice read row lo).
   // Loads step i (clamped to this wave's last step; rows past the slice read row
-  // hi - 1).  Offsets are 32-bit element offsets from the (row, kv head) bases:
-  // one head's cache is cap * D elements.
-  constexpr int PR = D / 8;    // 16-byte pieces per cache row
-  constexpr int RPC = 64 / PR;  // V rows per load instruction
+  // hi - 1, whose scores are masked to -inf).  Offsets are 32-bit element offsets from
+  // the (row, kv head) bases: one head's cache is cap * D elements.
   const uint32_t last_row = static_cast<uint32_t>(hi - 1);
   auto issue = [&](Buf& bf, int64_t i) {
     if (i >= my) i = my - 1;
@@ -488,25 +521,28 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
       for (int kk = 0; kk < KK; ++kk) bf.k[tt][kk] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
     }
 #pragma unroll
-    for (int c = 0; c < VCH; ++c) {
-      const uint32_t pos = min(base + lane / PR + RPC * c, last_row);
-      bf.v[c] = *reinterpret_cast<const uint4*>(vbase + (pos * D + 8 * (lane % PR)));
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t pos = min(base + 16 * (c >> 2) + 4 * h + (c & 3), last_row);
+      const uint16_t* vp = vbase + (pos * D + CW * j);
+      if constexpr (VW == 4) {
+        const uint4 t = *reinterpret_cast<const uint4*>(vp);
+        bf.v[c][0] = t.x, bf.v[c][1] = t.y, bf.v[c][2] = t.z, bf.v[c][3] = t.w;
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(vp);
+        bf.v[c][0] = t.x, bf.v[c][1] = t.y;
+      }
     }
   };
 
   float m_run = -INFINITY, l_run = 0.0f;  // head j's state over this lane's positions
-  f32x4_t o[DT];                          // O[4h + r][16 dt + j]
+  f32x4_t o[CW];                          // O[4h + r][CW j + t]
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint16_t* const tile = sv[wave];
+  for (int t = 0; t < CW; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](const Buf& bf, int64_t i) {
-    const int64_t base = lo + 32 * (wave + i * NW);
-    // stage V row-major: piece c of the lane is row piece / (D/8), 8 columns
-#pragma unroll
-    for (int c = 0; c < VCH; ++c)
-      *reinterpret_cast<uint4*>(tile + (lane / PR + RPC * c) * VR + 8 * (lane % PR)) = bf.v[c];
-    // scores of positions base + 16 tt + 4 h + r for head j
+    // scores of positions base + 16 tt + 4 h + r for head j; lim = positions of the
+    // step left in the slice, seen from this lane group's first row
+    const int32_t lim = static_cast<int32_t>(hi - (lo + 32 * (wave + i * NW))) - 4 * h;
     float sc[2][4];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -514,9 +550,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, bf.k[tt][kk]),
-                                                       __builtin_bit_cast(bf16x8_t, sq[kk][lane]), acc, 0, 0, 0);
+                                                       __builtin_bit_cast(bf16x8_t, sq[wave][kk][lane]), acc, 0, 0,
+                                                       0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[tt][r] = base + 16 * tt + 4 * h + r < hi ? acc[r] * p.scale : -INFINITY;
+      for (int r = 0; r < 4; ++r) sc[tt][r] = 16 * tt + r < lim ? acc[r] * p.scale : -INFINITY;
     }
     float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                      fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
@@ -540,7 +577,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
     for (int r = 0; r < 4; ++r) {
       const float cr = __shfl(c, 16 * h + 4 * h + r);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][r] *= cr;
+      for (int t = 0; t < CW; ++t) o[t][r] *= cr;
     }
     // A operand: element e of lane (j, h) is position 16 (e >> 2) + 4 h + (e & 3)
     bf16x8_t phi, plo;
@@ -551,61 +588,59 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
       phi[e] = hb;
       plo[e] = static_cast<__bf16>(v - static_cast<float>(hb));
     }
-    // B operand per output tile: V[that position][16 dt + j], gathered from the tile
+    // B operand of tile t: element e is V[k slot e][CW j + t], the t-th bf16 of row
+    // piece e; pairs of k slots share a 32-bit word.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int t = 0; t < CW; ++t) {
       uint32_t w[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const int e0 = 2 * e2, e1 = 2 * e2 + 1;
-        const int r0 = 16 * (e0 >> 2) + 4 * h + (e0 & 3), r1 = 16 * (e1 >> 2) + 4 * h + (e1 & 3);
-        w[e2] = static_cast<uint32_t>(tile[r0 * VR + 16 * dt + j]) |
-                (static_cast<uint32_t>(tile[r1 * VR + 16 * dt + j]) << 16);
+        const uint32_t a0 = bf.v[2 * e2][t >> 1], a1 = bf.v[2 * e2 + 1][t >> 1];
+        w[e2] = (t & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
       }
       const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop, o[dt], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop, o[t], 0, 0, 0);
     }
   };
 
   // Steps alternate between two buffers; the step after next is issued once a buffer
-  // is consumed.  Every path after an issue consumes that buffer (the exits finish
-  // the pending steps), so the loads stay where they are issued instead of being
-  // moved down to the one path that uses them.
+  // is consumed.  The loop is entered and continued only with both buffers in flight
+  // (ba older), so its waits leave the younger buffer's loads outstanding; the last
+  // one or two steps are finished after it.  An issue past the wave's last step
+  // reloads that step (cache hits, never used).  The scheduling barriers keep each
+  // step's loads together where they are issued.
+  auto stage_q = [&]() {
+    sq[wave][0][lane] = q0;
+    sq[wave][1][lane] = q1;
+    if constexpr (KK == 4) {
+      sq[wave][2][lane] = q2;
+      sq[wave][3][lane] = q3;
+    }
+  };
   Buf ba, bb;
-  if (my > 0) {
+  if (my == 1) {
     issue(ba, 0);
+    stage_q();
+    compute(ba, 0);
+  } else if (my > 1) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ba, 0);
+    __builtin_amdgcn_sched_barrier(0);
     issue(bb, 1);
-  }
-  // B operand of the scores: lane (j, h) holds query head j of the group at
-  // d = 32 kk + 8 h .. +8 (zero for j >= G); staged once per block, behind the first
-  // cache loads.
-  if (wave == 0) {
-    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + (qr * p.hq + g * G + (j < G ? j : 0)) * D + 8 * h;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      uint4 v = *reinterpret_cast<const uint4*>(qp + 32 * kk);
-      if (j >= G) v = make_uint4(0, 0, 0, 0);
-      sq[kk][lane] = v;
-    }
-  }
-  __syncthreads();
-  if (my > 0) {
-    for (int64_t i = 0;;) {
+    __builtin_amdgcn_sched_barrier(0);
+    stage_q();
+    int64_t i = 0;
+    for (; i + 2 < my; i += 2) {
       compute(ba, i);
-      if (i + 2 >= my) {
-        if (i + 1 < my) compute(bb, i + 1);
-        break;
-      }
       issue(ba, i + 2);
+      __builtin_amdgcn_sched_barrier(0);
       compute(bb, i + 1);
-      if (i + 3 >= my) {
-        compute(ba, i + 2);
-        break;
-      }
       issue(bb, i + 3);
-      i += 2;
+      __builtin_amdgcn_sched_barrier(0);
     }
+    compute(ba, i);
+    if (i + 1 < my) compute(bb, i + 1);
   }
 
   // head j's sum over the four lane rows; all rows already share the running max
@@ -620,7 +655,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
     const int q = 4 * h + r;
     if (q < G) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) sm_o[wave][q][16 * dt + j] = o[dt][r];
+      for (int t = 0; t < CW; ++t) sm_o[wave][q][CW * j + t] = o[t][r];
     }
   }
   __syncthreads();
