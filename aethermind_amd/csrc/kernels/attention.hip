@@ -428,15 +428,15 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
 // grid = (splits, kv_heads, batch).  A block of kDecWaves waves owns one (row, kv head)
 // and a slice of positions; wave w takes the 32-position steps w, w + kDecWaves, ...
 // of the slice, with the next step's K and V loads in flight while a step computes.
-// Nothing is staged in LDS on the way: every MFMA operand is built in the registers of
-// the lane that loaded it.
+// No K or V byte is staged in LDS: their MFMA operands are built in the registers of
+// the lane that loaded them.
 //   * Scores: S^T = K Q^T on v_mfma_f32_16x16x32_bf16.  A = 16 cache rows (position
 //     16 tt + i of the step is row i of tile tt; each lane loads 16 contiguous bytes
-//     of its row per k step), B = the G query heads of the group (columns >= G are
-//     zero), loaded by every wave into registers.  Lane (j, h) receives the scores of
-//     head j for positions 16 tt + 4 h + r, so the softmax state of head j lives in
-//     the lanes with lane % 16 == j.  Products are exact and sums fp32; the
-//     log2(e)/sqrt(d) scale is applied to the fp32 scores.
+//     of its row per k step), B = the G query heads of the group (columns >= G
+//     repeat head 0 and are never read), each wave's own copy in LDS.  Lane (j, h)
+//     receives the scores of head j for positions 16 tt + 4 h + r, so the softmax
+//     state of head j lives in the lanes with lane % 16 == j.  Products are exact and
+//     sums fp32; the log2(e)/sqrt(d) scale is applied to the fp32 scores.
 //   * O += P V on the same MFMA.  The reduction index runs over positions and its
 //     order is free: k slot e of lane group h is position 16 (e >> 2) + 4 h + (e & 3),
 //     exactly the positions whose scores lane (j, h) holds, so P never moves between
