@@ -1,5 +1,6 @@
-// Status / error objects of the C ABI (replaces include/c_api.h:82-88 and
-// src/c_api_error.cpp:14-40 of the reference) and small device queries.
+// Status / error objects of the C ABI and small device queries.  The error objects
+// are this library's own (am_gfx950_error_*): the reference library keeps the
+// am_error_* names of its c_api.h:82-88.
 
 #include <hip/hip_runtime.h>
 
@@ -42,17 +43,17 @@ int DeviceCUs() {
 
 extern "C" {
 
-am_error_handle am_error_create(am_status_code code, const char* message) {
+am_error_handle am_gfx950_error_create(am_status_code code, const char* message) {
   return new ErrorObject{code, message ? message : ""};
 }
 
-void am_error_destroy(am_error_handle e) { delete static_cast<ErrorObject*>(e); }
+void am_gfx950_error_destroy(am_error_handle e) { delete static_cast<ErrorObject*>(e); }
 
-am_status_code am_error_code(am_error_handle e) {
+am_status_code am_gfx950_error_code(am_error_handle e) {
   return e ? static_cast<ErrorObject*>(e)->code : AM_STATUS_INVALID_ARGUMENT;
 }
 
-const char* am_error_message(am_error_handle e) { return e ? static_cast<ErrorObject*>(e)->message.c_str() : ""; }
+const char* am_gfx950_error_message(am_error_handle e) { return e ? static_cast<ErrorObject*>(e)->message.c_str() : ""; }
 
 const char* am_last_error_message(void) { return g_last_error.c_str(); }
 

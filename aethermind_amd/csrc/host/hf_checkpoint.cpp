@@ -381,8 +381,9 @@ StatusOr<int64_t> PosInt(const Json& cfg, const char* key, bool required, int64_
     if (required) return Status::InvalidArgument(std::string("config.json: missing '") + key + "'");
     return dflt;
   }
-  if (!v->is_uint || v->uint == 0 || v->uint > (uint64_t{1} << 31))
-    return Status::InvalidArgument(std::string("config.json: '") + key + "' must be a positive integer");
+  // the runtime keeps every dimension in int32, so 2^31 - 1 is the largest accepted
+  if (!v->is_uint || v->uint == 0 || v->uint > static_cast<uint64_t>(INT32_MAX))
+    return Status::InvalidArgument(std::string("config.json: '") + key + "' must be a positive integer below 2^31");
   return static_cast<int64_t>(v->uint);
 }
 }  // namespace
@@ -415,21 +416,59 @@ StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view text) {
     return Status::InvalidArgument("config.json: head_dim must equal hidden_size / num_attention_heads");
   if (m.num_kv_heads > m.num_q_heads || m.num_q_heads % m.num_kv_heads != 0)
     return Status::InvalidArgument("config.json: num_attention_heads must be a multiple of num_key_value_heads");
-  if (const Json* e = c.Get("rms_norm_eps"); e != nullptr) {
-    if (e->kind != Json::kNumber || !(e->number > 0.0)) return Status::InvalidArgument("config.json: rms_norm_eps must be positive");
-    m.rms_eps = e->number;
-  }
-  if (const Json* t = c.Get("rope_theta"); t != nullptr) {
-    if (t->kind != Json::kNumber || !(t->number > 0.0)) return Status::InvalidArgument("config.json: rope_theta must be positive");
-    m.rope_theta = t->number;
+  // rms_norm_eps has no default: the reference reads 0 when it is absent and rejects
+  // anything that is not positive (hf_model_validator.cpp:523-525)
+  const Json* eps = c.Get("rms_norm_eps");
+  if (eps == nullptr || eps->kind != Json::kNumber || !(eps->number > 0.0))
+    return Status::InvalidArgument("config.json: rms_norm_eps must be a positive number");
+  m.rms_eps = eps->number;
+  AM_RETURN_IF_ERROR(get("max_position_embeddings", true, 0, &m.max_position_embeddings));
+  if (m.ffn < m.hidden)
+    return Status::InvalidArgument("config.json: intermediate_size must be at least hidden_size");
+  // RoPE: a top-level rope_theta and a rope_scaling / rope_parameters object (the form
+  // recent transformers versions write: {"rope_theta": .., "rope_type": "default"}) are
+  // read in file order, so a later key overrides an earlier theta, as in the reference
+  // reader (hf_directory_reader.cpp:141-155, 170-219).  A scaling factor or a scaling
+  // type other than "" / "default" is RoPE scaling, which Phase 1 rejects
+  // (hf_model_validator.cpp:561-564; hf_model_config.h:28-41).
+  for (const auto& [key, val] : c.obj) {
+    if (key == "rope_theta") {
+      if (val.kind != Json::kNumber || !(val.number > 0.0)) return Status::InvalidArgument("config.json: rope_theta must be positive");
+      m.rope_theta = val.number;
+    } else if (key == "rope_scaling" || key == "rope_parameters") {
+      if (val.kind == Json::kNull) continue;
+      if (val.kind != Json::kObject) return Status::InvalidArgument("config.json: " + key + " must be an object or null");
+      for (const auto& [rk, rv] : val.obj) {
+        if (rk == "factor") {
+          if (rv.kind != Json::kNumber) return Status::InvalidArgument("config.json: " + key + ".factor must be a number");
+          return Status::InvalidArgument("config.json: RoPE scaling is not supported");
+        }
+        if (rk == "type" || rk == "rope_type") {
+          if (rv.kind != Json::kString) return Status::InvalidArgument("config.json: " + key + "." + rk + " must be a string");
+          if (!rv.str.empty() && rv.str != "default") return Status::InvalidArgument("config.json: RoPE scaling is not supported");
+        } else if (rk == "rope_theta") {
+          if (rv.kind != Json::kNumber || !(rv.number > 0.0))
+            return Status::InvalidArgument("config.json: " + key + ".rope_theta must be positive");
+          m.rope_theta = rv.number;
+        }
+      }
+    }
   }
   if (const Json* t = c.Get("tie_word_embeddings"); t != nullptr && t->kind == Json::kBool) m.tie_word_embeddings = t->boolean;
   for (const char* k : {"attention_bias", "mlp_bias"})
     if (const Json* b = c.Get(k); b != nullptr && b->kind == Json::kBool && b->boolean)
       return Status::InvalidArgument(std::string("config.json: ") + k + " is not supported");
-  for (const char* k : {"rope_scaling", "rope_parameters"})
-    if (const Json* r = c.Get(k); r != nullptr && r->kind != Json::kNull)
-      return Status::InvalidArgument("config.json: RoPE scaling is not supported");
+  // the weight dtype hint: absent, "auto" or a dense float type the loader converts
+  // (hf_directory_reader.cpp:221-240; hf_model_validator.cpp:30-38, 587-589)
+  for (const char* k : {"torch_dtype", "dtype"}) {
+    const Json* h = c.Get(k);
+    if (h == nullptr || h->kind == Json::kNull) continue;
+    if (h->kind != Json::kString) return Status::InvalidArgument(std::string("config.json: ") + k + " must be a string");
+    static constexpr std::string_view kDense[] = {"auto", "float32", "float", "float16", "half", "bfloat16"};
+    bool ok = false;
+    for (std::string_view d : kDense) ok = ok || h->str == d;
+    if (!ok) return Status::InvalidArgument("config.json: only dense float torch_dtype hints are supported (got '" + h->str + "')");
+  }
   if (const Json* a = c.Get("hidden_act"); a != nullptr && a->kind == Json::kString && a->str != "silu")
     return Status::InvalidArgument("config.json: hidden_act must be silu");
   return m;
@@ -551,6 +590,27 @@ StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir) {
   }
   for (const auto& [name, v] : ck->tensors_)
     if (!known.count(name)) return Status::InvalidArgument("unexpected tensor found: " + name);
+  // The embedding, the head and every projection share one dtype (the reference's
+  // default require_uniform_linear_dtype, hf_model_validator.cpp:433-500); a present
+  // head of a tied model has the embedding's dtype.  Norm gains may differ.
+  const TensorView& embed = ck->Get("model.embed_tokens.weight");
+  if (const TensorView* head = ck->Find("lm_head.weight"); head != nullptr && c.tie_word_embeddings &&
+                                                             head->dtype != embed.dtype)
+    return Status::InvalidArgument("tied embedding dtype mismatch: lm_head.weight is " + head->dtype_text +
+                                   ", model.embed_tokens.weight is " + embed.dtype_text);
+  auto same_as_embed = [&](const std::string& n) -> Status {
+    const TensorView& v = ck->Get(n);
+    if (v.dtype != embed.dtype)
+      return Status::InvalidArgument("mixed linear tensor dtype: " + n + " is " + v.dtype_text + ", expected " +
+                                     embed.dtype_text);
+    return Status::Ok();
+  };
+  if (ck->Find("lm_head.weight") != nullptr) AM_RETURN_IF_ERROR(same_as_embed("lm_head.weight"));
+  for (int64_t l = 0; l < c.num_layers; ++l)
+    for (const char* sfx : {".self_attn.q_proj.weight", ".self_attn.k_proj.weight", ".self_attn.v_proj.weight",
+                            ".self_attn.o_proj.weight", ".mlp.gate_proj.weight", ".mlp.up_proj.weight",
+                            ".mlp.down_proj.weight"})
+      AM_RETURN_IF_ERROR(same_as_embed(LayerName(l, sfx)));
   return ck;
 }
 
@@ -562,6 +622,12 @@ const TensorView* Checkpoint::Find(const std::string& name) const {
 const TensorView& Checkpoint::LmHead() const {
   const TensorView* h = Find("lm_head.weight");
   return h != nullptr ? *h : Get("model.embed_tokens.weight");
+}
+
+uint64_t Checkpoint::max_tensor_bytes() const {
+  uint64_t b = 0;
+  for (const auto& [n, v] : tensors_) b = std::max(b, v.bytes);
+  return b;
 }
 
 uint64_t Checkpoint::total_bytes() const {

@@ -69,11 +69,14 @@ class MappedFile {
 // ---- model ----
 struct LlamaConfig {
   int64_t num_layers = 0, hidden = 0, num_q_heads = 0, num_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0;
-  double rms_eps = 1e-6, rope_theta = 10000.0;
+  int64_t max_position_embeddings = 0;
+  double rms_eps = 0.0, rope_theta = 10000.0;
   bool tie_word_embeddings = false;
 };
 // config.json -> LlamaConfig with the reference's Phase-1 rules (model_type llama,
-// no bias, no RoPE scaling, head_dim = hidden / heads, heads divisible by kv heads).
+// positive integer dimensions below 2^31, rms_norm_eps and max_position_embeddings
+// present, no bias, no RoPE scaling, head_dim = hidden / heads, heads divisible by kv
+// heads, intermediate_size >= hidden_size, a dense float dtype hint).
 StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view config_json);
 
 class Checkpoint {
@@ -81,7 +84,7 @@ class Checkpoint {
   // Reads model_dir/config.json and model.safetensors (or the shards named by
   // model.safetensors.index.json), then checks every tensor name, dtype (F32, F16,
   // BF16) and shape against the config; lm_head.weight may be absent only when
-  // tie_word_embeddings is true.
+  // tie_word_embeddings is true; the embedding, head and projections share a dtype.
   static StatusOr<std::unique_ptr<Checkpoint>> Open(const std::string& model_dir);
 
   const LlamaConfig& config() const { return cfg_; }
@@ -91,6 +94,7 @@ class Checkpoint {
   const TensorView& LmHead() const;
   size_t num_tensors() const { return tensors_.size(); }
   uint64_t total_bytes() const;
+  uint64_t max_tensor_bytes() const;  // the largest single tensor (device staging size)
 
  private:
   LlamaConfig cfg_{};

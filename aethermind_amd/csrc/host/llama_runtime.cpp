@@ -281,11 +281,8 @@ class LlamaModel {
     const auto& c = cfg;
     const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers;
     const int32_t act_fmt = c.act_dtype == AM_DT_BF16 ? AM_WF_BF16 : AM_WF_F32;
-    uint64_t max_bytes = ck.LmHead().bytes;
-    max_bytes = std::max<uint64_t>(max_bytes, ck.Get("model.embed_tokens.weight").bytes);
-    for (int64_t l = 0; l < L; ++l)
-      for (const char* sfx : {".mlp.gate_proj.weight", ".mlp.down_proj.weight", ".self_attn.q_proj.weight"})
-        max_bytes = std::max<uint64_t>(max_bytes, ck.Get(hf::LayerName(l, sfx)).bytes);
+    // the staging area holds any one tensor of the checkpoint
+    const uint64_t max_bytes = ck.max_tensor_bytes();
     constexpr size_t kRing = size_t{32} << 20;
     void* dsrc = nullptr;
     void* pinned[2] = {nullptr, nullptr};
@@ -299,6 +296,7 @@ class LlamaModel {
       }
       int slot = 0;
       auto upload = [&](const hf::TensorView& t) -> Status {
+        if (t.bytes > max_bytes) return Status::Internal("tensor " + t.name + " exceeds the device staging area");
         for (uint64_t off = 0; off < t.bytes;) {
           const size_t n = static_cast<size_t>(std::min<uint64_t>(kRing, t.bytes - off));
           if (pending[slot]) AM_HIP_OK(hipEventSynchronize(ev[slot]));

@@ -142,10 +142,10 @@ class SessionOptions(C.Structure):
 _SIGS = {
     # name: (restype, argtypes)
     "am_last_error_message": (C.c_char_p, []),
-    "am_error_create": (vp, [i32, C.c_char_p]),
-    "am_error_destroy": (None, [vp]),
-    "am_error_code": (i32, [vp]),
-    "am_error_message": (C.c_char_p, [vp]),
+    "am_gfx950_error_create": (vp, [i32, C.c_char_p]),
+    "am_gfx950_error_destroy": (None, [vp]),
+    "am_gfx950_error_code": (i32, [vp]),
+    "am_gfx950_error_message": (C.c_char_p, [vp]),
     "am_gfx950_device_count": (i32, []),
     "am_gfx950_version": (C.c_char_p, []),
     "am_gfx950_embedding": (i32, [C.POINTER(EmbeddingArgs), vp]),

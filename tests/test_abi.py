@@ -69,3 +69,59 @@ def test_host_logic_cpp():
     r = subprocess.run([HOST_TEST], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "0 failures" in r.stdout
+
+
+REF_INCLUDE = "/root/reference/include"
+
+_UNIT_HEADERS = {
+    "reference_first": ['"c_api.h"', '"am_gfx950.h"', '"am_runtime.h"'],
+    "gfx950_first": ['"am_gfx950.h"', '"am_runtime.h"', '"c_api.h"'],
+}
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+@pytest.mark.parametrize("order", sorted(_UNIT_HEADERS))
+def test_headers_coexist_with_reference_c_api(tmp_path, lang, order):
+    """A drop-in unit includes the reference's c_api.h (am_status_code, am_error_*,
+    c_api.h:55-88) and this library's headers in either order: one definition of the
+    enum, no clashing declarations."""
+    if not os.path.exists(os.path.join(REF_INCLUDE, "c_api.h")):
+        pytest.skip("reference tree not present")
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / ("unit.c" if lang == "c" else "unit.cpp")
+    lines = [f"#include {h}" for h in _UNIT_HEADERS[order]]
+    lines += ["am_status_code probe(void) { return AM_STATUS_OUT_OF_RANGE; }",
+              "const char* probe_msg(am_error_handle e) { return am_error_message(e); }"]
+    src.write_text("\n".join(lines) + "\n")
+    std = ["-std=c11"] if lang == "c" else ["-std=c++17"]
+    r = subprocess.run([cc, *std, "-fsyntax-only", "-Wall", "-Werror", "-I", REF_INCLUDE, "-I", INCLUDE, str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_headers_standalone(tmp_path, lang):
+    """Without the reference tree the library's headers define the status enum."""
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / ("unit.c" if lang == "c" else "unit.cpp")
+    src.write_text('#include "am_gfx950.h"\n#include "am_runtime.h"\n'
+                   "am_status_code probe(void) { return AM_STATUS_UNAUTHENTICATED; }\n")
+    std = ["-std=c11"] if lang == "c" else ["-std=c++17"]
+    r = subprocess.run([cc, *std, "-fsyntax-only", "-Wall", "-Werror", "-I", INCLUDE, str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_library_does_not_export_reference_error_api():
+    """am_error_create/destroy/code/message belong to the reference library
+    (src/c_api_error.cpp); exporting them too would interpose one implementation
+    on the other inside a process that loads both."""
+    _ensure_built()
+    exported = _exported_symbols(LIB)
+    clash = sorted(n for n in ("am_error_create", "am_error_destroy", "am_error_code", "am_error_message")
+                   if n in exported)
+    assert not clash, clash

@@ -31,7 +31,7 @@ def hf_config(c, **kw):
          "intermediate_size": c["ffn"], "num_hidden_layers": c["num_layers"],
          "num_attention_heads": c["num_q_heads"], "num_key_value_heads": c["num_kv_heads"],
          "vocab_size": c["vocab"], "rms_norm_eps": 1e-5, "rope_theta": 10000.0, "hidden_act": "silu",
-         "tie_word_embeddings": False, "torch_dtype": "float32"}
+         "max_position_embeddings": 256, "tie_word_embeddings": False, "torch_dtype": "float32"}
     d.update(kw)
     return d
 
@@ -127,26 +127,71 @@ def test_inspect_single_and_sharded(tmp_path):
 
 
 def test_inspect_dtypes_and_tied_head(tmp_path):
+    """Each checkpoint has one linear dtype (embedding, head and projections; the
+    reference's require_uniform_linear_dtype default); norm gains may use any of F32,
+    F16 and BF16."""
     rng = np.random.default_rng(1)
     shapes = tensor_shapes(SMALL, tied=True)
-    t = {}
-    for i, (n, s) in enumerate(shapes.items()):
-        a = (rng.standard_normal(s) * 0.02).astype(np.float32)
-        t[n] = a.astype(np.float16) if i % 3 == 0 else (bf16_bytes(a), "BF16", list(s)) if i % 3 == 1 else a
-    d = str(tmp_path / "tied")
-    make_dir(d, SMALL, tensors=t, tied=True)
-    rc, _, nt, msg = inspect(d)
-    assert rc == 0, msg
-    assert nt == len(shapes)
+    norm_dt = ["f16", "bf16", "f32"]
+    for lin in ("f32", "f16", "bf16"):
+        t = {}
+        for i, (n, s) in enumerate(shapes.items()):
+            a = (rng.standard_normal(s) * 0.02).astype(np.float32)
+            dt = norm_dt[i % 3] if len(s) == 1 else lin
+            t[n] = a.astype(np.float16) if dt == "f16" else (bf16_bytes(a), "BF16", list(s)) if dt == "bf16" else a
+        d = str(tmp_path / f"tied_{lin}")
+        make_dir(d, SMALL, tensors=t, tied=True)
+        rc, _, nt, msg = inspect(d)
+        assert rc == 0, msg
+        assert nt == len(shapes)
     d2 = str(tmp_path / "untied_missing_head")
     make_dir(d2, SMALL, tensors=t, tied=False)
     rc, _, _, msg = inspect(d2)
     assert rc != 0 and "lm_head" in msg
 
 
+def test_inspect_reads_rope_parameters_object(tmp_path):
+    """transformers >= 5 writes RoPE as rope_parameters={rope_theta, rope_type:
+    'default'} with no top-level rope_theta; the reader takes theta from it
+    (hf_directory_reader.cpp:145-155) and treats 'default' as no scaling."""
+    for i, kw in enumerate([{"rope_parameters": {"rope_theta": 500000.0, "rope_type": "default"}},
+                            {"rope_scaling": {"rope_theta": 500000.0, "type": ""}},
+                            {"rope_theta": 1.0, "rope_parameters": {"rope_theta": 500000.0}},
+                            {"rope_scaling": None, "rope_theta": 500000.0}]):
+        d = str(tmp_path / f"r{i}")
+        make_dir(d, SMALL)
+        cfgd = hf_config(SMALL, **kw)
+        if "rope_theta" not in kw:
+            del cfgd["rope_theta"]
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(cfgd, f)
+        rc, cfg, _, msg = inspect(d)
+        assert rc == 0, (kw, msg)
+        assert cfg.rope_theta == 500000.0, kw
+
+
+def test_inspect_transformers_written_config(tmp_path):
+    """A config.json written by transformers' own LlamaConfig (CPU only)."""
+    tr = pytest.importorskip("transformers")
+    c = tr.LlamaConfig(vocab_size=SMALL["vocab"], hidden_size=SMALL["hidden"], intermediate_size=SMALL["ffn"],
+                       num_hidden_layers=SMALL["num_layers"], num_attention_heads=SMALL["num_q_heads"],
+                       num_key_value_heads=SMALL["num_kv_heads"], max_position_embeddings=128, rms_norm_eps=1e-6,
+                       rope_theta=500000.0, tie_word_embeddings=False)
+    d = str(tmp_path / "tf")
+    make_dir(d, SMALL)
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(c.to_dict(), f)
+    rc, cfg, _, msg = inspect(d)
+    assert rc == 0, msg
+    assert cfg.rope_theta == 500000.0 and abs(cfg.rms_eps - 1e-6) < 1e-12
+
+
 @pytest.mark.parametrize("case", ["missing", "shape", "unknown", "bias_cfg", "rope_scaling", "model_type",
                                   "dtype", "head_dim", "gap", "size", "truncated", "shard_escape",
-                                  "not_in_index"])
+                                  "not_in_index", "rope_params_scaling", "rope_params_factor", "int_2p31",
+                                  "eps_missing", "eps_zero", "maxpos_missing", "dtype_hint_int8",
+                                  "dtype_hint_f64", "dtype_hint_number", "mixed_linear", "tied_head_dtype",
+                                  "ffn_small"])
 def test_inspect_rejects(tmp_path, case):
     d = str(tmp_path / case)
     rng = np.random.default_rng(2)
@@ -169,7 +214,39 @@ def test_inspect_rejects(tmp_path, case):
         t["model.norm.weight"] = np.zeros(64, np.int32)
     elif case == "head_dim":
         cfg_kw = {"head_dim": 32}
-    make_dir(d, SMALL, tensors=t, cfg_kw=cfg_kw, shards=2 if case in ("shard_escape", "not_in_index") else 1)
+    elif case == "rope_params_scaling":
+        cfg_kw = {"rope_parameters": {"rope_theta": 1e4, "rope_type": "llama3"}}
+    elif case == "rope_params_factor":
+        cfg_kw = {"rope_parameters": {"rope_theta": 1e4, "factor": 8.0}}
+    elif case == "int_2p31":
+        cfg_kw = {"max_position_embeddings": 2 ** 31}
+    elif case == "eps_zero":
+        cfg_kw = {"rms_norm_eps": 0.0}
+    elif case == "dtype_hint_int8":
+        cfg_kw = {"torch_dtype": "int8"}
+    elif case == "dtype_hint_f64":
+        cfg_kw = {"torch_dtype": "float64"}
+    elif case == "dtype_hint_number":
+        cfg_kw = {"dtype": 16}
+    elif case == "mixed_linear":
+        t["model.layers.1.mlp.up_proj.weight"] = t["model.layers.1.mlp.up_proj.weight"].astype(np.float16)
+    elif case == "ffn_small":
+        cfg_kw = {"intermediate_size": 32}
+        for l in range(SMALL["num_layers"]):
+            for nm, shp in ((f"model.layers.{l}.mlp.gate_proj.weight", (32, 64)),
+                            (f"model.layers.{l}.mlp.up_proj.weight", (32, 64)),
+                            (f"model.layers.{l}.mlp.down_proj.weight", (64, 32))):
+                t[nm] = np.zeros(shp, np.float32)
+    if case == "tied_head_dtype":
+        t["lm_head.weight"] = t["lm_head.weight"].astype(np.float16)
+        make_dir(d, SMALL, tensors=t, tied=True)
+    else:
+        make_dir(d, SMALL, tensors=t, cfg_kw=cfg_kw, shards=2 if case in ("shard_escape", "not_in_index") else 1)
+    if case in ("eps_missing", "maxpos_missing"):
+        p = os.path.join(d, "config.json")
+        cj = json.load(open(p))
+        del cj["rms_norm_eps" if case == "eps_missing" else "max_position_embeddings"]
+        json.dump(cj, open(p, "w"))
     if case == "gap":  # 4 data bytes that no tensor covers
         with open(os.path.join(d, "model.safetensors"), "ab") as f:
             f.write(b"\0\0\0\0")
@@ -199,6 +276,12 @@ def test_inspect_rejects(tmp_path, case):
     rc, _, _, msg = inspect(d)
     assert rc != 0, case
     assert msg, case
+    expect = {"rope_params_scaling": "RoPE scaling", "rope_params_factor": "RoPE scaling", "int_2p31": "2^31",
+              "eps_missing": "rms_norm_eps", "eps_zero": "rms_norm_eps", "maxpos_missing": "max_position_embeddings",
+              "dtype_hint_int8": "torch_dtype", "dtype_hint_f64": "torch_dtype", "dtype_hint_number": "dtype",
+              "mixed_linear": "mixed linear", "tied_head_dtype": "tied", "ffn_small": "intermediate_size"}
+    if case in expect:
+        assert expect[case] in msg, (case, msg)
 
 
 # ---------------------------------------------------------------- GPU
@@ -331,4 +414,41 @@ def test_bf16_checkpoint_quantized_on_load_matches_synthetic_int4(tmp_path):
     assert np.array_equal(_generate(L, mq, prompt, 8), _generate(L, ml, prompt, 8))
     L.am_model_destroy(mq)
     L.am_model_destroy(ml)
+    L.am_runtime_destroy(rt)
+
+
+@pytest.mark.gpu
+def test_f16_linear_with_mixed_norm_dtypes_loads_exactly(tmp_path):
+    """F16 projections with F32 / BF16 / F16 norm gains (one linear dtype, any norm
+    dtype): every tensor reaches the device exactly (F16 and BF16 widen to fp32 without
+    rounding), through a staging area sized for the largest tensor."""
+    torch = _gpu()
+    L, rt = _runtime()
+    c = dict(SMALL)
+    rng = np.random.default_rng(4)
+    shapes = tensor_shapes(c)
+    src, t = {}, {}
+    for i, (n, s) in enumerate(shapes.items()):
+        a = (rng.standard_normal(s) * 0.02).astype(np.float16).astype(np.float32)
+        if len(s) == 1:
+            a = (1.0 + a).astype(np.float32)
+            kind = i % 3
+            if kind == 1:
+                b = np.frombuffer(bf16_bytes(a), np.uint16)
+                a = (b.astype(np.uint32) << 16).view(np.float32).reshape(s)
+                t[n] = (bf16_bytes(a), "BF16", list(s))
+            else:
+                t[n] = a.astype(np.float16) if kind == 2 else a
+        else:
+            t[n] = a.astype(np.float16)
+        src[n] = a
+    d = str(tmp_path / "mixed_norms")
+    make_dir(d, c, tensors=t)
+    m = N.vp()
+    L.call("am_model_load_hf", rt, d.encode(), C.byref(N.ModelLoadOptions(N.AM_DT_F32, N.AM_WF_F32, 128, 64, 16)),
+           C.byref(m))
+    got = _model_tensors(L, m, dict(c, rms_eps=1e-5), torch)
+    for n, a in src.items():
+        assert np.array_equal(got[n], a), n
+    L.am_model_destroy(m)
     L.am_runtime_destroy(rt)
