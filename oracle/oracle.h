@@ -121,6 +121,16 @@ int orc_model_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, in
 int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, float* logits);
 /* use the AVX2 fp32 kernels (the reference's fast path) instead of the fp64 scalar forms */
 void orc_model_set_fast(orc_model* m, int32_t fast);
+/* Plant one composition mistake (tests only: they show that the pins of the
+ * composition reject it).  0 = none. */
+enum {
+  ORC_SLIP_NONE = 0,
+  ORC_SLIP_RESIDUAL_NORMED = 1, /* attention residual added to the normed input, not h */
+  ORC_SLIP_ROPE_AFTER_KV = 2,   /* keys written to the cache without RoPE */
+  ORC_SLIP_GQA_MODULO = 3,      /* q head h reads kv head h % hkv instead of h / group */
+  ORC_SLIP_NO_FINAL_NORM = 4    /* final RMSNorm skipped before the head */
+};
+void orc_model_set_slip(orc_model* m, int32_t slip);
 /* OpenMP threads used by the oracle's parallel loops (cpu_baseline uses 1). */
 void orc_set_threads(int32_t n);
 

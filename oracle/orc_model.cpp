@@ -105,6 +105,7 @@ struct orc_model {
   QWeight lm_head;
   std::vector<float> cos_tab, sin_tab;
   int fast = 0;
+  int slip = 0;  // planted composition mistake for the tests that check the pins (0 = none)
 };
 
 namespace {
@@ -197,6 +198,8 @@ void orc_model_destroy(orc_model* m) { delete m; }
 
 void orc_model_set_fast(orc_model* m, int32_t fast) { m->fast = fast; }
 
+void orc_model_set_slip(orc_model* m, int32_t slip) { m->slip = slip; }
+
 void orc_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, float* logits) {
@@ -223,8 +226,10 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
     MaybeRound(m, v.data(), n * hkv * d);
     orc_rope(q.data(), n, hq, d, positions.data(), m->cos_tab.data(), m->sin_tab.data());
     MaybeRound(m, q.data(), n * hq * d);
-    orc_rope(k.data(), n, hkv, d, positions.data(), m->cos_tab.data(), m->sin_tab.data());
-    MaybeRound(m, k.data(), n * hkv * d);
+    if (m->slip != ORC_SLIP_ROPE_AFTER_KV) {
+      orc_rope(k.data(), n, hkv, d, positions.data(), m->cos_tab.data(), m->sin_tab.data());
+      MaybeRound(m, k.data(), n * hkv * d);
+    }
     for (int64_t s = 0; s < n; ++s)
       for (int64_t g = 0; g < hkv; ++g) {
         std::memcpy(&L.kc[static_cast<size_t>((g * cap + pos + s) * d)], &k[static_cast<size_t>((s * hkv + g) * d)],
@@ -232,11 +237,31 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
         std::memcpy(&L.vc[static_cast<size_t>((g * cap + pos + s) * d)], &v[static_cast<size_t>((s * hkv + g) * d)],
                     sizeof(float) * static_cast<size_t>(d));
       }
-    orc_attention(q.data(), L.kc.data(), L.vc.data(), n, hq, hkv, d, cap, pos, attn.data());
+    if (m->slip == ORC_SLIP_GQA_MODULO) {
+      // q head h reads kv head h % hkv: reorder the heads so the contiguous-group
+      // attention below sees that mapping, then put the outputs back
+      const int64_t grp = hq / hkv;
+      std::vector<float> qp(q.size()), ap(attn.size());
+      auto slot = [&](int64_t h) { return (h % hkv) * grp + h / hkv; };
+      for (int64_t s = 0; s < n; ++s)
+        for (int64_t hh = 0; hh < hq; ++hh)
+          std::memcpy(&qp[static_cast<size_t>((s * hq + slot(hh)) * d)], &q[static_cast<size_t>((s * hq + hh) * d)],
+                      sizeof(float) * static_cast<size_t>(d));
+      orc_attention(qp.data(), L.kc.data(), L.vc.data(), n, hq, hkv, d, cap, pos, ap.data());
+      for (int64_t s = 0; s < n; ++s)
+        for (int64_t hh = 0; hh < hq; ++hh)
+          std::memcpy(&attn[static_cast<size_t>((s * hq + hh) * d)], &ap[static_cast<size_t>((s * hq + slot(hh)) * d)],
+                      sizeof(float) * static_cast<size_t>(d));
+    } else {
+      orc_attention(q.data(), L.kc.data(), L.vc.data(), n, hq, hkv, d, cap, pos, attn.data());
+    }
     MaybeRound(m, attn.data(), n * hq * d);
     Linear(m, attn.data(), n, L.o, tmp.data());
     MaybeRound(m, tmp.data(), n * H);
-    for (size_t i = 0; i < h.size(); ++i) h[i] += tmp[i];
+    if (m->slip == ORC_SLIP_RESIDUAL_NORMED)
+      for (size_t i = 0; i < h.size(); ++i) h[i] = xn[i] + tmp[i];
+    else
+      for (size_t i = 0; i < h.size(); ++i) h[i] += tmp[i];
     MaybeRound(m, h.data(), n * H);
 
     Norm(m, h.data(), L.post_norm.data(), n, xn.data());
@@ -252,7 +277,10 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
     MaybeRound(m, h.data(), n * H);
   }
   // Only the last row's logits feed the next token.
-  Norm(m, h.data() + (n - 1) * H, m->final_norm.data(), 1, xn.data());
+  if (m->slip == ORC_SLIP_NO_FINAL_NORM)
+    std::memcpy(xn.data(), h.data() + (n - 1) * H, sizeof(float) * static_cast<size_t>(H));
+  else
+    Norm(m, h.data() + (n - 1) * H, m->final_norm.data(), 1, xn.data());
   Linear(m, xn.data(), 1, m->lm_head, logits);
   return 0;
 }

@@ -55,6 +55,7 @@ _SIGS = {
     "orc_model_generate": (i32, [vp, vp, i64, i64, vp, vp]),
     "orc_model_forward": (i32, [vp, vp, i64, i64, vp]),
     "orc_model_set_fast": (None, [vp, i32]),
+    "orc_model_set_slip": (None, [vp, i32]),
     "orc_set_threads": (None, [i32]),
 }
 
@@ -218,6 +219,9 @@ class OracleModel:
 
     def set_fast(self, fast: bool):
         lib().orc_model_set_fast(self.h, 1 if fast else 0)
+
+    def set_slip(self, slip: int):
+        lib().orc_model_set_slip(self.h, slip)
 
     def generate(self, prompt: np.ndarray, n_new: int):
         prompt = np.ascontiguousarray(prompt, np.int64)

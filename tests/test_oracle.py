@@ -285,3 +285,53 @@ def test_tiny_model_matches_committed_golden():
     toks, logits = m.generate(prompt, 33)
     assert np.array_equal(toks, g["tokens"])
     np.testing.assert_array_equal(logits, g["last_logits"])
+
+
+# ---------------------------------------------------------------- composition vs HF
+def _hf_golden_errors(m):
+    """Walks the oracle model through the golden's 33 steps (prefill, then KV-cached
+    decode steps fed with the golden's tokens) and returns the largest logit error
+    relative to the step's largest |logit| and the steps whose greedy token differs."""
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "hf_tiny_fp32_seed0.npz"))
+    prompt = g["prompt"]
+    stride = int(g["sample_stride"])
+    worst, bad_steps = 0.0, []
+    for step in range(len(g["tokens"])):
+        if step == 0:
+            logits = m.forward(prompt, 0)
+        else:
+            logits = m.forward(np.array([g["tokens"][step - 1]], np.int64), len(prompt) + step - 1)
+        scale = float(np.max(np.abs(g["top_val"][step])))
+        if step == 0:
+            worst = max(worst, float(np.max(np.abs(logits - g["prefill_logits"]))) / scale)
+        worst = max(worst, float(np.max(np.abs(logits[g["top_idx"][step]] - g["top_val"][step]))) / scale)
+        worst = max(worst, float(np.max(np.abs(logits[::stride] - g["sample"][step]))) / scale)
+        if O.argmax(logits) != int(g["tokens"][step]):
+            bad_steps.append(step)
+    return worst, bad_steps
+
+
+def test_oracle_composition_matches_hf_transformers_golden():
+    """The oracle's whole-model forward (prefill, then one KV-cached decode step at a
+    time) against transformers' LlamaForCausalLM on the same tiny fp32 weights
+    (tests/golden/make_hf_tiny_golden.py): identical greedy tokens at all 33 steps, and
+    logits within 1e-4 of the largest |logit| at every step (the prefill step in full;
+    the top-16 and every 97th vocabulary entry of every step)."""
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "hf_tiny_fp32_seed0.npz"))
+    assert np.array_equal(O.token_ids(0, 0, 32000, 16), g["prompt"])
+    for fast in (False, True):
+        m = O.OracleModel(O.TINY, 0)
+        m.set_fast(fast)
+        worst, bad = _hf_golden_errors(m)
+        assert worst <= 1e-4 and not bad, (fast, worst, bad)
+
+
+@pytest.mark.parametrize("slip", [1, 2, 3, 4])
+def test_hf_golden_rejects_planted_composition_slips(slip):
+    """Each planted wiring mistake in the oracle (normed-input residual, keys cached
+    without RoPE, h % Hkv GQA mapping, no final norm) fails the HF pin by a wide
+    margin, so the pin constrains the composition and not just the op kernels."""
+    m = O.OracleModel(O.TINY, 0)
+    m.set_slip(slip)
+    worst, bad = _hf_golden_errors(m)
+    assert worst > 1e-2, (slip, worst)
