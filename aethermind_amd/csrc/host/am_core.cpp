@@ -6,6 +6,7 @@
 
 #include "am_gfx950.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 
@@ -108,97 +109,92 @@ const char* ToString(OpType op) noexcept {
 
 // ---------------------------------------------------------------- registry
 Status ValidateKernelDescriptor(const KernelDescriptor& d) noexcept {
-  if (d.op_type == OpType::kUnknown) return Status::InvalidArgument("Kernel descriptor op_type cannot be kUnknown");
-  if (d.kernel_func == nullptr) return Status::InvalidArgument("Kernel descriptor function cannot be null");
-  if (d.name.empty()) return Status::InvalidArgument("Kernel descriptor name cannot be empty");
+  if (d.op_type == OpType::kUnknown) return Status::InvalidArgument("kernel descriptor: op type is unknown");
+  if (d.kernel_func == nullptr) return Status::InvalidArgument("kernel descriptor: no kernel function");
+  if (d.name.empty()) return Status::InvalidArgument("kernel descriptor: empty name");
   if (d.selector.device_type == DeviceType::kUndefined)
-    return Status::InvalidArgument("Kernel descriptor device_type cannot be kUndefined");
-  if (d.params_builder != nullptr) {
-    if (d.params_size == 0) return Status::InvalidArgument("params_size must be > 0 when params_builder is set");
-    if (d.params_size > kMaxKernelParamsSize) return Status::InvalidArgument("params_size exceeds kMaxKernelParamsSize");
-  }
+    return Status::InvalidArgument("kernel descriptor: device type is undefined");
+  if (d.params_builder != nullptr && (d.params_size == 0 || d.params_size > kMaxKernelParamsSize))
+    return Status::InvalidArgument("kernel descriptor: a params builder needs 0 < params_size <= " +
+                                   std::to_string(kMaxKernelParamsSize));
   return Status::Ok();
 }
 
-size_t KernelRegistry::KeyHash::operator()(const Key& k) const noexcept {
-  size_t h = static_cast<size_t>(k.op);
-  auto mix = [&h](size_t v) { h ^= v + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2); };
-  mix(static_cast<size_t>(k.sel.device_type));
-  mix((static_cast<size_t>(k.sel.act_dtype.code) << 24) | (static_cast<size_t>(k.sel.act_dtype.bits) << 16) |
-      k.sel.act_dtype.lanes);
-  mix((static_cast<size_t>(k.sel.weight_dtype.code) << 24) | (static_cast<size_t>(k.sel.weight_dtype.bits) << 16) |
-      k.sel.weight_dtype.lanes);
-  mix(static_cast<size_t>(k.sel.weight_format));
-  mix(static_cast<size_t>(k.sel.isa));
-  mix(static_cast<size_t>(k.sel.phase));
-  return h;
-}
-
 KernelRegistry& KernelRegistry::Global() noexcept {
-  static KernelRegistry r;
-  return r;
+  static KernelRegistry registry;
+  return registry;
 }
 
 Status KernelRegistry::Register(const KernelDescriptor& d) {
   std::lock_guard<std::mutex> lock(mutex_);
   if (frozen_.load(std::memory_order_relaxed))
-    return Status::FailedPrecondition("Cannot register kernel after registry has been frozen");
+    return Status::FailedPrecondition("kernel table is frozen; '" + d.name + "' registered too late");
   AM_RETURN_IF_ERROR(ValidateKernelDescriptor(d));
-  if (!keys_.insert(Key{d.op_type, d.selector}).second) return Status::AlreadyExists("Duplicate kernel registration");
-  kernels_.push_back(d);
+  if (static_cast<size_t>(d.op_type) >= kOpSlots)
+    return Status::InvalidArgument("kernel descriptor: op type beyond the table's range");
+  for (const KernelDescriptor& e : pending_)
+    if (e.op_type == d.op_type && e.selector == d.selector)
+      return Status::AlreadyExists("kernel '" + d.name + "' repeats the op type and selector of '" + e.name + "'");
+  pending_.push_back(d);
   return Status::Ok();
 }
 
 Status KernelRegistry::Freeze() {
   std::lock_guard<std::mutex> lock(mutex_);
   if (frozen_.load(std::memory_order_relaxed)) return Status::Ok();
-  std::unordered_map<uint16_t, std::vector<size_t>> b;
-  for (size_t i = 0; i < kernels_.size(); ++i) b[static_cast<uint16_t>(kernels_[i].op_type)].push_back(i);
-  buckets_.swap(b);
+  // order: op type, then priority high to low, then registration order (stable sort)
+  std::vector<KernelDescriptor> t = pending_;
+  std::stable_sort(t.begin(), t.end(), [](const KernelDescriptor& a, const KernelDescriptor& b) {
+    if (a.op_type != b.op_type) return static_cast<uint32_t>(a.op_type) < static_cast<uint32_t>(b.op_type);
+    return a.priority > b.priority;
+  });
+  for (Range& r : ranges_) r = Range{};
+  for (uint32_t i = 0; i < t.size();) {
+    const size_t op = static_cast<size_t>(t[i].op_type);
+    uint32_t j = i;
+    while (j < t.size() && static_cast<size_t>(t[j].op_type) == op) ++j;
+    ranges_[op] = Range{i, j};
+    i = j;
+  }
+  table_ = std::move(t);
   frozen_.store(true, std::memory_order_release);
   return Status::Ok();
 }
 
 StatusOr<const KernelDescriptor*> KernelRegistry::Resolve(OpType op_type, const KernelSelector& selector) const {
   if (!frozen_.load(std::memory_order_acquire))
-    return Status::FailedPrecondition("Cannot resolve kernel before registry has been frozen");
-  if (op_type == OpType::kUnknown) return Status::InvalidArgument("op_type cannot be kUnknown");
-  if (selector.device_type == DeviceType::kUndefined) return Status::InvalidArgument("device_type cannot be kUndefined");
-  const KernelDescriptor* best = nullptr;
-  if (auto it = buckets_.find(static_cast<uint16_t>(op_type)); it != buckets_.end()) {
-    for (size_t idx : it->second) {
-      const KernelDescriptor& d = kernels_[idx];
-      if (!SelectorMatches(d.selector, selector)) continue;
-      if (best == nullptr || d.priority > best->priority) best = &d;
-    }
-  }
-  if (best == nullptr)
-    return Status::NotFound(std::string("No matching kernel registered for op_type=") + ToString(op_type) +
-                            ", selector=" + ToString(selector));
-  return best;
+    return Status::FailedPrecondition("kernel table must be frozen before resolving");
+  if (op_type == OpType::kUnknown) return Status::InvalidArgument("resolve: op type is unknown");
+  if (selector.device_type == DeviceType::kUndefined) return Status::InvalidArgument("resolve: device type is undefined");
+  const size_t op = static_cast<size_t>(op_type);
+  if (op < kOpSlots)
+    for (uint32_t i = ranges_[op].begin; i < ranges_[op].end; ++i)
+      if (SelectorMatches(table_[i].selector, selector)) return &table_[i];
+  return Status::NotFound(std::string("no kernel for ") + ToString(op_type) + " matches " + ToString(selector));
 }
 
 size_t KernelRegistry::size() const {
   std::lock_guard<std::mutex> lock(mutex_);
-  return kernels_.size();
+  return pending_.size();
 }
 
 StatusOr<std::vector<const KernelDescriptor*>> KernelRegistry::FindByOpType(OpType op_type) const {
   if (!frozen_.load(std::memory_order_acquire))
-    return Status::FailedPrecondition("Cannot find kernels by op_type before registry has been frozen");
+    return Status::FailedPrecondition("kernel table must be frozen before listing kernels");
   std::vector<const KernelDescriptor*> out;
-  if (auto it = buckets_.find(static_cast<uint16_t>(op_type)); it != buckets_.end())
-    for (size_t idx : it->second) out.push_back(&kernels_[idx]);
+  const size_t op = static_cast<size_t>(op_type);
+  if (op < kOpSlots)
+    for (uint32_t i = ranges_[op].begin; i < ranges_[op].end; ++i) out.push_back(&table_[i]);
   return out;
 }
 
 std::string KernelRegistry::DebugDump() const {
   std::lock_guard<std::mutex> lock(mutex_);
   std::string out;
-  for (size_t i = 0; i < kernels_.size(); ++i) {
-    if (i) out += '\n';
-    out += std::string(ToString(kernels_[i].op_type)) + " | " + kernels_[i].name + " | " +
-           ToString(kernels_[i].selector) + " | priority=" + std::to_string(kernels_[i].priority);
+  for (const KernelDescriptor& d : pending_) {
+    if (!out.empty()) out += '\n';
+    out += std::string(ToString(d.op_type)) + " | " + d.name + " | " + ToString(d.selector) +
+           " | priority=" + std::to_string(d.priority);
   }
   return out;
 }
@@ -274,89 +270,93 @@ Status LayerRunner::RunStep(size_t index, const ExecutionStep& step, RuntimeBind
 }
 
 // ---------------------------------------------------------------- KV cache
+// Layout arithmetic and checks follow the reference contract (kv_cache_view.cpp:17-75):
+// the same strides, the same error codes for a dimension or index out of range and
+// for size_t overflow.
 Status KVCacheLayout::Validate() const noexcept {
   if (num_layers == 0 || num_kv_heads == 0 || max_tokens == 0 || head_dim == 0)
-    return Status::InvalidArgument("KV layout dimensions must be non-zero");
+    return Status::InvalidArgument("KV layout: every dimension must be positive");
   if (alignment == 0 || (alignment & (alignment - 1)) != 0)
-    return Status::InvalidArgument("KV layout alignment must be a non-zero power of two");
-  if (kv_dtype.bits == 0 || kv_dtype.lanes == 0) return Status::InvalidArgument("KV layout dtype must be initialized");
-  if (head_dim_stride < head_dim) return Status::InvalidArgument("KV head_dim_stride must be >= head_dim");
+    return Status::InvalidArgument("KV layout: alignment must be a power of two");
+  if (kv_dtype.bits == 0 || kv_dtype.lanes == 0) return Status::InvalidArgument("KV layout: element type not set");
+  if (head_dim_stride < head_dim) return Status::InvalidArgument("KV layout: head_dim_stride below head_dim");
   return Status::Ok();
 }
 
 StatusOr<size_t> KVCacheLayout::Offset(size_t layer, size_t head, size_t pos, size_t dim) const noexcept {
   AM_RETURN_IF_ERROR(Validate());
-  if (layer >= num_layers) return Status::OutOfRange("layer index out of range");
-  if (head >= num_kv_heads) return Status::OutOfRange("kv_head index out of range");
-  if (pos >= max_tokens) return Status::OutOfRange("seq_pos index out of range");
-  if (dim >= head_dim) return Status::OutOfRange("dim index out of range");
-  size_t off = 0, t = 0;
-  if (CheckOverflowMul(layer, layer_stride, &off)) return Status::Overflow("KV layer offset overflowed size_t");
-  if (CheckOverflowMul(head, head_stride, &t) || CheckOverflowAdd(off, t, &off))
-    return Status::Overflow("KV head offset overflowed size_t");
-  if (CheckOverflowMul(pos, token_stride, &t) || CheckOverflowAdd(off, t, &off))
-    return Status::Overflow("KV token offset overflowed size_t");
-  if (CheckOverflowMul(dim, ElementBytes(), &t) || CheckOverflowAdd(off, t, &off))
-    return Status::Overflow("KV dim offset overflowed size_t");
+  const size_t index[4] = {layer, head, pos, dim};
+  const size_t limit[4] = {num_layers, num_kv_heads, max_tokens, head_dim};
+  const size_t stride[4] = {layer_stride, head_stride, token_stride, ElementBytes()};
+  static const char* const what[4] = {"layer", "kv head", "position", "dim"};
+  size_t off = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (index[i] >= limit[i]) return Status::OutOfRange(std::string("KV offset: ") + what[i] + " index out of range");
+    size_t term = 0;
+    if (CheckOverflowMul(index[i], stride[i], &term) || CheckOverflowAdd(off, term, &off))
+      return Status::Overflow(std::string("KV offset: ") + what[i] + " term overflows size_t");
+  }
   return off;
 }
 
 StatusOr<size_t> KVCacheLayout::BytesPerPlane() const noexcept {
   AM_RETURN_IF_ERROR(Validate());
   size_t b = 0;
-  if (CheckOverflowMul(num_layers, layer_stride, &b)) return Status::Overflow("KV bytes-per-plane overflowed size_t");
+  if (CheckOverflowMul(num_layers, layer_stride, &b)) return Status::Overflow("KV plane size overflows size_t");
   return b;
 }
 
-bool KVCacheView::valid() const noexcept {
-  return layout_ && storage_ && storage_->is_initialized() && slot_ && slot_->in_use && slot_->generation == generation_;
-}
+bool KVCacheView::valid() const noexcept { return CheckLive().ok(); }
 
-Status KVCacheView::ValidateBase() const noexcept {
-  if (!layout_ || !storage_ || !slot_) return Status::FailedPrecondition("KVCacheView is not bound to manager-owned state");
-  if (!storage_->is_initialized()) return Status::FailedPrecondition("KVCacheView storage is not initialized");
-  if (!(slot_->in_use && slot_->generation == generation_))
-    return Status::FailedPrecondition("KVCacheView is stale or released");
-  return layout_->Validate();
+Status KVCacheView::CheckLive() const noexcept {
+  if (layout_ == nullptr || storage_ == nullptr || slot_ == nullptr)
+    return Status::FailedPrecondition("KV view is not bound to a reservation");
+  if (!storage_->is_initialized()) return Status::FailedPrecondition("KV view: the pool has no storage");
+  if (!slot_->in_use || slot_->generation != generation_)
+    return Status::FailedPrecondition("KV view belongs to a released reservation");
+  return Status::Ok();
 }
 
 Status KVCacheView::ValidateWrite(size_t layer, size_t head, size_t pos, size_t count) const noexcept {
-  AM_RETURN_IF_ERROR(ValidateBase());
-  if (layer >= layout_->num_layers) return Status::OutOfRange("layer index out of range");
-  if (head >= layout_->num_kv_heads) return Status::OutOfRange("kv_head index out of range");
-  if (count == 0) return Status::InvalidArgument("KV write token_count must be non-zero");
+  AM_RETURN_IF_ERROR(CheckLive());
+  AM_RETURN_IF_ERROR(layout_->Validate());
+  if (layer >= layout_->num_layers || head >= layout_->num_kv_heads)
+    return Status::OutOfRange("KV write: layer or kv head out of range");
+  if (count == 0) return Status::InvalidArgument("KV write: no tokens");
   size_t end = 0;
-  if (CheckOverflowAdd(pos, count, &end)) return Status::Overflow("KV write range overflowed size_t");
-  if (end > slot_->capacity_tokens) return Status::OutOfRange("KV write exceeds reserved session token capacity");
-  if (end > layout_->max_tokens) return Status::OutOfRange("KV write exceeds physical KV capacity");
+  if (CheckOverflowAdd(pos, count, &end)) return Status::Overflow("KV write: end position overflows size_t");
+  if (end > slot_->capacity_tokens || end > layout_->max_tokens)
+    return Status::OutOfRange("KV write: rows " + std::to_string(pos) + ".." + std::to_string(end) +
+                              " fall outside the reservation");
   return Status::Ok();
 }
 
 Status KVCacheView::ValidateRead(size_t layer, size_t head, size_t begin, size_t end) const noexcept {
-  AM_RETURN_IF_ERROR(ValidateBase());
-  if (layer >= layout_->num_layers) return Status::OutOfRange("layer index out of range");
-  if (head >= layout_->num_kv_heads) return Status::OutOfRange("kv_head index out of range");
-  if (begin > end) return Status::InvalidArgument("KV read seq_begin must be <= seq_end");
-  if (end > slot_->current_pos) return Status::OutOfRange("KV read exceeds committed token range");
+  AM_RETURN_IF_ERROR(CheckLive());
+  AM_RETURN_IF_ERROR(layout_->Validate());
+  if (layer >= layout_->num_layers || head >= layout_->num_kv_heads)
+    return Status::OutOfRange("KV read: layer or kv head out of range");
+  if (begin > end) return Status::InvalidArgument("KV read: begin after end");
+  if (end > slot_->current_pos)
+    return Status::OutOfRange("KV read: position " + std::to_string(end) + " is past the committed " +
+                              std::to_string(slot_->current_pos));
   return Status::Ok();
 }
 
-StatusOr<void*> KVCacheView::KeyPlane(size_t layer) const noexcept {
-  AM_RETURN_IF_ERROR(ValidateBase());
-  if (layer >= layout_->num_layers) return Status::OutOfRange("layer index out of range");
-  return static_cast<void*>(static_cast<std::byte*>(storage_->key) + layer * layout_->layer_stride);
+StatusOr<void*> KVCacheView::Plane(bool value, size_t layer) const noexcept {
+  AM_RETURN_IF_ERROR(CheckLive());
+  if (layer >= layout_->num_layers) return Status::OutOfRange("KV plane: layer out of range");
+  void* base = value ? storage_->value(slot_->index) : storage_->key(slot_->index);
+  return static_cast<void*>(static_cast<std::byte*>(base) + layer * layout_->layer_stride);
 }
 
-StatusOr<void*> KVCacheView::ValuePlane(size_t layer) const noexcept {
-  AM_RETURN_IF_ERROR(ValidateBase());
-  if (layer >= layout_->num_layers) return Status::OutOfRange("layer index out of range");
-  return static_cast<void*>(static_cast<std::byte*>(storage_->value) + layer * layout_->layer_stride);
-}
+StatusOr<void*> KVCacheView::KeyPlane(size_t layer) const noexcept { return Plane(false, layer); }
+StatusOr<void*> KVCacheView::ValuePlane(size_t layer) const noexcept { return Plane(true, layer); }
 
 Status KVCacheView::CommitUntil(size_t new_pos) noexcept {
-  AM_RETURN_IF_ERROR(ValidateBase());
-  if (new_pos < slot_->current_pos) return Status::InvalidArgument("KV commit position cannot move backwards");
-  if (new_pos > slot_->capacity_tokens) return Status::OutOfRange("KV commit exceeds reserved session token capacity");
+  AM_RETURN_IF_ERROR(CheckLive());
+  if (new_pos < slot_->current_pos) return Status::InvalidArgument("KV commit: position would move backwards");
+  if (new_pos > slot_->capacity_tokens) return Status::OutOfRange("KV commit: position past the reservation");
   slot_->current_pos = new_pos;
   return Status::Ok();
 }
@@ -379,77 +379,106 @@ void HostFree(void* p, void*) { std::free(p); }
 DeviceAllocator HipDeviceAllocator() { return {&HipAlloc, &HipFree, nullptr}; }
 DeviceAllocator HostTestAllocator() { return {&HostAlloc, &HostFree, nullptr}; }
 
-KVCacheManager::~KVCacheManager() { FreeStorage(); }
+KVCacheManager::~KVCacheManager() { Release(); }
 
-void KVCacheManager::FreeStorage() noexcept {
-  if (storage_.key) alloc_.free(storage_.key, alloc_.user);
-  if (storage_.value) alloc_.free(storage_.value, alloc_.user);
+void KVCacheManager::Release() noexcept {
+  if (storage_.base != nullptr) alloc_.free(storage_.base, alloc_.user);
   storage_ = {};
+  slots_.clear();
+  layout_ = {};
+  initialized_ = false;
+}
+
+size_t KVCacheManager::free_slots() const noexcept {
+  size_t n = 0;
+  for (const SessionKVSlot& s : slots_) n += s.in_use ? 0 : 1;
+  return n;
 }
 
 Status KVCacheManager::Init(size_t num_layers, size_t num_kv_heads, size_t max_tokens, size_t head_dim,
-                            DataType kv_dtype, size_t alignment) {
-  FreeStorage();
-  layout_ = {};
-  slot_ = {};
-  total_bytes_ = 0;
-  initialized_ = false;
-  layout_.num_layers = num_layers;
-  layout_.num_kv_heads = num_kv_heads;
-  layout_.max_tokens = max_tokens;
-  layout_.head_dim = head_dim;
-  layout_.head_dim_stride = head_dim;
-  layout_.kv_dtype = kv_dtype;
-  layout_.alignment = alignment;
-  const size_t eb = layout_.ElementBytes();
-  if (eb == 0) return Status::InvalidArgument("KV dtype must have non-zero element bytes");
-  if (CheckOverflowMul(layout_.head_dim_stride, eb, &layout_.token_stride) ||
-      CheckOverflowMul(layout_.max_tokens, layout_.token_stride, &layout_.head_stride) ||
-      CheckOverflowMul(layout_.num_kv_heads, layout_.head_stride, &layout_.layer_stride))
-    return Status::Overflow("KV layout stride computation overflowed size_t");
-  AM_RETURN_IF_ERROR(layout_.Validate());
-  auto bpp = layout_.BytesPerPlane();
-  if (!bpp.ok()) return bpp.status();
-  size_t total = 0;
-  if (CheckOverflowMul(bpp.value(), size_t{2}, &total)) return Status::Overflow("KV total bytes overflowed size_t");
-  storage_.key = alloc_.alloc(bpp.value(), alloc_.user);
-  storage_.value = alloc_.alloc(bpp.value(), alloc_.user);
-  if (!storage_.key || !storage_.value) {
-    FreeStorage();
-    return Status::ResourceExhausted("Failed to allocate KV cache planes");
-  }
-  storage_.bytes_per_plane = bpp.value();
-  total_bytes_ = total;
+                            DataType kv_dtype, size_t alignment, size_t num_slots) {
+  for (const SessionKVSlot& s : slots_)
+    if (s.in_use) return Status::FailedPrecondition("KV pool: cannot rebuild while a reservation is active");
+  Release();
+  if (num_slots == 0) return Status::InvalidArgument("KV pool: at least one slot");
+  KVCacheLayout l;
+  l.num_layers = num_layers;
+  l.num_kv_heads = num_kv_heads;
+  l.max_tokens = max_tokens;
+  l.head_dim = head_dim;
+  l.head_dim_stride = head_dim;
+  l.kv_dtype = kv_dtype;
+  l.alignment = alignment;
+  if (l.ElementBytes() == 0) return Status::InvalidArgument("KV pool: element type has no size");
+  // strides inside a plane set: dim, then position, then kv head, then layer
+  if (CheckOverflowMul(l.head_dim_stride, l.ElementBytes(), &l.token_stride) ||
+      CheckOverflowMul(l.max_tokens, l.token_stride, &l.head_stride) ||
+      CheckOverflowMul(l.num_kv_heads, l.head_stride, &l.layer_stride))
+    return Status::Overflow("KV pool: stride overflows size_t");
+  AM_RETURN_IF_ERROR(l.Validate());
+  auto plane = l.BytesPerPlane();
+  if (!plane.ok()) return plane.status();
+  // each plane set starts on an alignment boundary; a slot holds K then V
+  size_t padded = 0, slot = 0, total = 0;
+  if (CheckOverflowAdd(plane.value(), alignment - 1, &padded)) return Status::Overflow("KV pool: size overflows size_t");
+  padded &= ~(alignment - 1);
+  if (CheckOverflowMul(padded, size_t{2}, &slot) || CheckOverflowMul(slot, num_slots, &total))
+    return Status::Overflow("KV pool: size overflows size_t");
+  void* base = alloc_.alloc(total, alloc_.user);
+  if (base == nullptr)
+    return Status::ResourceExhausted("KV pool: could not allocate " + std::to_string(total) + " bytes");
+  layout_ = l;
+  storage_ = KVCacheStorage{base, plane.value(), padded, slot, num_slots};
+  slots_.assign(num_slots, SessionKVSlot{});
+  for (size_t i = 0; i < num_slots; ++i) slots_[i].index = i;
   initialized_ = true;
   return Status::Ok();
 }
 
+StatusOr<KVCacheView> KVCacheManager::Take(SessionKVSlot& s, size_t prompt_len, size_t max_new_tokens) noexcept {
+  size_t want = 0;
+  if (CheckOverflowAdd(prompt_len, max_new_tokens, &want)) return Status::Overflow("KV reserve: size overflows size_t");
+  if (want == 0) return Status::InvalidArgument("KV reserve: no tokens requested");
+  if (want > layout_.max_tokens)
+    return Status::OutOfRange("KV reserve: " + std::to_string(want) + " tokens exceed the " +
+                              std::to_string(layout_.max_tokens) + "-token cache");
+  ++s.generation;
+  s.in_use = true;
+  s.capacity_tokens = want;
+  s.prompt_len = prompt_len;
+  s.current_pos = prompt_len;
+  return KVCacheView(&layout_, &storage_, &s);
+}
+
 StatusOr<KVCacheView> KVCacheManager::ReserveForSession(size_t prompt_len, size_t max_new_tokens) noexcept {
-  if (!initialized_) return Status::FailedPrecondition("KVCacheManager is not initialized");
-  if (slot_.in_use) return Status::FailedPrecondition("KVCacheManager already has an active session reservation");
-  size_t req = 0;
-  if (CheckOverflowAdd(prompt_len, max_new_tokens, &req)) return Status::Overflow("KV session reservation overflowed size_t");
-  if (req == 0) return Status::InvalidArgument("KV session reservation must request at least one token");
-  if (req > layout_.max_tokens) return Status::OutOfRange("KV session reservation exceeds physical KV capacity");
-  ++slot_.generation;
-  slot_.in_use = true;
-  slot_.capacity_tokens = req;
-  slot_.prompt_len = prompt_len;
-  slot_.current_pos = prompt_len;
-  return KVCacheView(&layout_, &storage_, &slot_);
+  if (!initialized_) return Status::FailedPrecondition("KV pool is not initialized");
+  for (SessionKVSlot& s : slots_)
+    if (!s.in_use) return Take(s, prompt_len, max_new_tokens);
+  return Status::FailedPrecondition("KV pool: every slot holds an active reservation");
+}
+
+StatusOr<KVCacheView> KVCacheManager::ReserveSlot(size_t slot, size_t prompt_len, size_t max_new_tokens) noexcept {
+  if (!initialized_) return Status::FailedPrecondition("KV pool is not initialized");
+  if (slot >= slots_.size()) return Status::OutOfRange("KV pool: slot index out of range");
+  if (slots_[slot].in_use) return Status::FailedPrecondition("KV pool: the slot already holds a reservation");
+  return Take(slots_[slot], prompt_len, max_new_tokens);
 }
 
 Status KVCacheManager::ResetSession(KVCacheView& view) noexcept {
-  if (!initialized_) return Status::FailedPrecondition("KVCacheManager is not initialized");
-  if (!view.valid()) return Status::FailedPrecondition("Cannot reset an invalid or stale KVCacheView");
-  slot_.current_pos = slot_.prompt_len;
+  if (!initialized_) return Status::FailedPrecondition("KV pool is not initialized");
+  if (!view.valid()) return Status::FailedPrecondition("KV reset: the view is stale or unbound");
+  SessionKVSlot& s = slots_[view.slot()];
+  s.current_pos = s.prompt_len;
   return Status::Ok();
 }
 
 Status KVCacheManager::ReleaseSession(KVCacheView& view) noexcept {
-  if (!initialized_) return Status::FailedPrecondition("KVCacheManager is not initialized");
-  if (!view.valid()) return Status::FailedPrecondition("Cannot release an invalid or stale KVCacheView");
-  slot_ = SessionKVSlot{slot_.generation + 1, false, 0, 0, 0};
+  if (!initialized_) return Status::FailedPrecondition("KV pool is not initialized");
+  if (!view.valid()) return Status::FailedPrecondition("KV release: the view is stale or unbound");
+  SessionKVSlot& s = slots_[view.slot()];
+  ++s.generation;
+  s.in_use = false;
+  s.capacity_tokens = s.prompt_len = s.current_pos = 0;
   view.Invalidate();
   return Status::Ok();
 }

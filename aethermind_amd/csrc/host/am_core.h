@@ -13,7 +13,7 @@
 //                             include/aethermind/backend/kernel_types.h:21-51
 //   KernelContext             include/aethermind/backend/kernel_context.h:14-22
 //   KernelDescriptor          include/aethermind/backend/kernel_descriptor.h:12-57
-//   KernelRegistry            src/backend/kernel_registry.cpp:30-142
+//   KernelRegistry            src/backend/kernel_registry.cpp:30-142 (contract; flat sorted table here)
 //   AM_REGISTER_KERNEL        include/aethermind/backend/kernel_static_registration.h:15-22
 //   Backend/BackendFactory    include/aethermind/backend/backend.h:14-28, backend_factory.h:12-17
 //   ResolvedKernel            include/aethermind/backend/resolved_kernel.h:11-28
@@ -22,7 +22,8 @@
 //   LayerRunner/Executor      src/execution/layer_runner.cpp:9-93, executor.cpp:8-11
 //   RuntimeBindingContext     include/aethermind/execution/runtime_binding_context.h:49-104
 //   KVCacheLayout/View/Manager include/aethermind/execution/kv_cache_view.h,
-//                             src/execution/kv_cache_{view,manager}.cpp (device storage)
+//                             src/execution/kv_cache_{view,manager}.cpp (contract; here a
+//                             device slot pool: one HBM allocation, one slot per sequence)
 #pragma once
 
 #include <atomic>
@@ -286,6 +287,14 @@ struct KernelDescriptor {
 };
 Status ValidateKernelDescriptor(const KernelDescriptor& d) noexcept;
 
+// Kernel table.  Registration appends descriptors under a mutex until the first
+// Freeze(); freezing sorts a flat copy by (op type, priority high to low, registration
+// order) and records each op type's range, so Resolve is a lock-free scan of one
+// contiguous range that returns the first matching entry.  Contract of the reference
+// (kernel_registry.cpp:30-112): no registration after freeze (kFailedPrecondition),
+// one descriptor per (op type, selector) (kAlreadyExists), no resolve before freeze,
+// the highest priority wins and the earlier registration wins a tie (kNotFound when
+// nothing matches).
 class KernelRegistry {
  public:
   static KernelRegistry& Global() noexcept;
@@ -298,19 +307,15 @@ class KernelRegistry {
   std::string DebugDump() const;
 
  private:
-  struct Key {
-    OpType op;
-    KernelSelector sel;
-    friend bool operator==(const Key& a, const Key& b) { return a.op == b.op && a.sel == b.sel; }
-  };
-  struct KeyHash {
-    size_t operator()(const Key& k) const noexcept;
+  static constexpr size_t kOpSlots = 64;  // OpType values are small integers
+  struct Range {
+    uint32_t begin = 0, end = 0;
   };
   mutable std::mutex mutex_;
   std::atomic<bool> frozen_{false};
-  std::vector<KernelDescriptor> kernels_;
-  std::unordered_map<uint16_t, std::vector<size_t>> buckets_;
-  std::unordered_set<Key, KeyHash> keys_;
+  std::vector<KernelDescriptor> pending_;  // registration order
+  std::vector<KernelDescriptor> table_;    // frozen, sorted
+  Range ranges_[kOpSlots]{};
 };
 
 namespace kernel_registration_detail {
@@ -463,44 +468,56 @@ struct KVCacheLayout {
   StatusOr<size_t> BytesPerPlane() const noexcept;
 };
 
-// Device-resident storage: one HBM slab per plane (allocated by the manager).
+// Device KV slot pool.  One allocation holds num_slots slots; a slot is one sequence's
+// key planes followed by its value planes, each [layers][kv heads][max_tokens][head_dim]
+// with the KVCacheLayout strides above.  Slot s starts s * slot_bytes after slot 0, so
+// a batched kernel reaches sequence r's planes at a fixed stride from sequence 0's.
 struct KVCacheStorage {
-  void* key = nullptr;
-  void* value = nullptr;
-  size_t bytes_per_plane = 0;
-  bool is_initialized() const noexcept { return key != nullptr && value != nullptr; }
+  void* base = nullptr;
+  size_t bytes_per_plane = 0;  // one K (or V) plane set, unpadded
+  size_t value_offset = 0;     // bytes from a slot's key planes to its value planes
+  size_t slot_bytes = 0;       // bytes between consecutive slots
+  size_t num_slots = 0;
+  bool is_initialized() const noexcept { return base != nullptr; }
+  void* key(size_t slot) const noexcept { return static_cast<std::byte*>(base) + slot * slot_bytes; }
+  void* value(size_t slot) const noexcept { return static_cast<std::byte*>(key(slot)) + value_offset; }
 };
 
+// One sequence's reservation: its token capacity, prompt length and committed position.
+// The generation changes on every release, so views of an earlier reservation go stale.
 struct SessionKVSlot {
   uint64_t generation = 0;
   bool in_use = false;
   size_t capacity_tokens = 0, prompt_len = 0, current_pos = 0;
+  size_t index = 0;  // slot number inside the pool
 };
 
 class KVCacheView {
  public:
   KVCacheView() = default;
-  KVCacheView(const KVCacheLayout* l, KVCacheStorage* s, SessionKVSlot* slot) noexcept
+  KVCacheView(const KVCacheLayout* l, const KVCacheStorage* s, SessionKVSlot* slot) noexcept
       : layout_(l), storage_(s), slot_(slot), generation_(slot ? slot->generation : 0) {}
   bool valid() const noexcept;
   size_t current_pos() const noexcept { return valid() ? slot_->current_pos : 0; }
   size_t token_capacity() const noexcept { return valid() ? slot_->capacity_tokens : 0; }
+  size_t slot() const noexcept { return valid() ? slot_->index : 0; }
   size_t max_tokens() const noexcept { return layout_ ? layout_->max_tokens : 0; }
   size_t num_layers() const noexcept { return layout_ ? layout_->num_layers : 0; }
   size_t num_kv_heads() const noexcept { return layout_ ? layout_->num_kv_heads : 0; }
   size_t head_dim() const noexcept { return layout_ ? layout_->head_dim : 0; }
   Status ValidateWrite(size_t layer, size_t head, size_t pos, size_t count) const noexcept;
   Status ValidateRead(size_t layer, size_t head, size_t begin, size_t end) const noexcept;
-  // Device address of the [head][pos][dim] plane of `layer` (K or V).
+  // Device address of the [head][pos][dim] plane of `layer` (K or V) in this slot.
   StatusOr<void*> KeyPlane(size_t layer) const noexcept;
   StatusOr<void*> ValuePlane(size_t layer) const noexcept;
   Status CommitUntil(size_t new_pos) noexcept;
   void Invalidate() noexcept { *this = KVCacheView(); }
 
  private:
-  Status ValidateBase() const noexcept;
+  Status CheckLive() const noexcept;
+  StatusOr<void*> Plane(bool value, size_t layer) const noexcept;
   const KVCacheLayout* layout_ = nullptr;
-  KVCacheStorage* storage_ = nullptr;
+  const KVCacheStorage* storage_ = nullptr;
   SessionKVSlot* slot_ = nullptr;
   uint64_t generation_ = 0;
 };
@@ -514,6 +531,10 @@ struct DeviceAllocator {
 DeviceAllocator HipDeviceAllocator();
 DeviceAllocator HostTestAllocator();
 
+// Static KV cache manager over a slot pool (the reference's KVCacheManager contract,
+// kv_cache_manager.cpp:49-150, with one reservation per slot instead of one per
+// manager).  With num_slots = 1 it behaves as the reference's: a second active
+// reservation is refused.
 class KVCacheManager {
  public:
   KVCacheManager() = default;
@@ -521,24 +542,30 @@ class KVCacheManager {
   ~KVCacheManager();
   KVCacheManager(const KVCacheManager&) = delete;
   KVCacheManager& operator=(const KVCacheManager&) = delete;
+  // (Re)builds the pool; refused while a reservation is active.
   Status Init(size_t num_layers, size_t num_kv_heads, size_t max_tokens, size_t head_dim, DataType kv_dtype,
-              size_t alignment = 256);
+              size_t alignment = 256, size_t num_slots = 1);
+  // Reserves the lowest free slot (kFailedPrecondition when every slot is taken).
   StatusOr<KVCacheView> ReserveForSession(size_t prompt_len, size_t max_new_tokens) noexcept;
+  // Reserves slot `slot` (a batched session keeps sequence r in slot r).
+  StatusOr<KVCacheView> ReserveSlot(size_t slot, size_t prompt_len, size_t max_new_tokens) noexcept;
   Status ResetSession(KVCacheView& view) noexcept;
   Status ReleaseSession(KVCacheView& view) noexcept;
   const KVCacheLayout& layout() const noexcept { return layout_; }
   size_t capacity_tokens() const noexcept { return layout_.max_tokens; }
-  size_t total_bytes() const noexcept { return total_bytes_; }
+  size_t total_bytes() const noexcept { return initialized_ ? storage_.slot_bytes * storage_.num_slots : 0; }
   bool is_initialized() const noexcept { return initialized_; }
   const KVCacheStorage& storage() const noexcept { return storage_; }
+  size_t num_slots() const noexcept { return slots_.size(); }
+  size_t free_slots() const noexcept;
 
  private:
-  void FreeStorage() noexcept;
+  void Release() noexcept;
+  StatusOr<KVCacheView> Take(SessionKVSlot& s, size_t prompt_len, size_t max_new_tokens) noexcept;
   DeviceAllocator alloc_ = HipDeviceAllocator();
   KVCacheLayout layout_{};
   KVCacheStorage storage_{};
-  SessionKVSlot slot_{};
-  size_t total_bytes_ = 0;
+  std::vector<SessionKVSlot> slots_;
   bool initialized_ = false;
 };
 

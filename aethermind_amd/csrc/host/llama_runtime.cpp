@@ -355,24 +355,6 @@ class LlamaModel {
 };
 
 // ------------------------------------------------------------------ session
-// KV planes of the session's sequences come from one allocation: the reference
-// KVCacheManager (one reservation each, kv_cache_manager.cpp:49-126) allocates its key
-// then value plane through this allocator, which hands sequence r the r-th slot of a
-// key region and of a value region, so every sequence's planes sit a fixed stride
-// apart (the batch stride of the batched decode kernels).
-struct KvSlotAllocator {
-  char* key = nullptr;
-  char* value = nullptr;
-  size_t slot_bytes = 0;
-  int next = 0;
-  static void* Alloc(size_t bytes, void* user) {
-    auto* a = static_cast<KvSlotAllocator*>(user);
-    if (bytes > a->slot_bytes || a->next > 1) return nullptr;
-    return a->next++ == 0 ? a->key : a->value;
-  }
-  static void Free(void*, void*) {}
-};
-
 class LlamaSession {
  public:
   LlamaModel* m = nullptr;
@@ -383,11 +365,10 @@ class LlamaSession {
   am_session_options opt{1, 1, 1, 0};
   int64_t B = 1;  // sequences decoded together
 
-  // KV: one reference KVCacheManager per sequence, planes in kv_slab
-  void* kv_slab = nullptr;
-  int64_t kv_row_elems = 0;  // elements between sequence r and r+1's planes
-  std::vector<std::unique_ptr<KvSlotAllocator>> kv_alloc;
-  std::vector<std::unique_ptr<KVCacheManager>> kvs;
+  // KV: one device slot pool, sequence r in slot r (its planes kv_row_elems elements
+  // after sequence r-1's, the batch stride of the batched decode kernels)
+  std::unique_ptr<KVCacheManager> kv;
+  int64_t kv_row_elems = 0;
   std::vector<KVCacheView> views;
 
   // device buffers
@@ -426,8 +407,7 @@ class LlamaSession {
     if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
     if (graph) (void)hipGraphDestroy(graph);
     views.clear();
-    kvs.clear();
-    if (kv_slab) (void)hipFree(kv_slab);
+    kv.reset();
     if (act_slab) (void)hipFree(act_slab);
     if (dl_table) (void)hipFree(dl_table);
     if (dl_ws) (void)hipFree(dl_ws);
@@ -456,24 +436,15 @@ class LlamaSession {
     backend = b.value();
     (void)am::DeviceCUs();
 
-    // KV: B reservations of max_tokens positions, planes a fixed stride apart
-    const size_t eb = ActBytes(c.act_dtype);
-    const size_t plane = static_cast<size_t>(c.num_layers) * c.num_kv_heads * c.max_tokens * c.head_dim * eb;
-    const size_t slot = (plane + 255) & ~size_t{255};
-    AM_HIP_OK(hipMalloc(&kv_slab, 2 * slot * static_cast<size_t>(B)));
-    kv_row_elems = static_cast<int64_t>(slot / eb);
+    // KV: a pool of B slots of max_tokens positions, sequence r in slot r
+    kv = std::make_unique<KVCacheManager>(HipDeviceAllocator());
+    AM_RETURN_IF_ERROR(kv->Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype), 256,
+                                static_cast<size_t>(B)));
+    kv_row_elems = static_cast<int64_t>(kv->storage().slot_bytes / ActBytes(c.act_dtype));
     for (int64_t r = 0; r < B; ++r) {
-      auto a = std::make_unique<KvSlotAllocator>();
-      a->key = static_cast<char*>(kv_slab) + static_cast<size_t>(r) * slot;
-      a->value = static_cast<char*>(kv_slab) + static_cast<size_t>(B + r) * slot;
-      a->slot_bytes = slot;
-      auto mgr = std::make_unique<KVCacheManager>(DeviceAllocator{&KvSlotAllocator::Alloc, &KvSlotAllocator::Free, a.get()});
-      AM_RETURN_IF_ERROR(mgr->Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype)));
-      auto vw = mgr->ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+      auto vw = kv->ReserveSlot(static_cast<size_t>(r), 0, static_cast<size_t>(c.max_tokens));
       if (!vw.ok()) return vw.status();
       views.push_back(vw.value());
-      kvs.push_back(std::move(mgr));
-      kv_alloc.push_back(std::move(a));
     }
     row_pos.assign(static_cast<size_t>(B), 0);
     row_ready.assign(static_cast<size_t>(B), 0);
@@ -839,8 +810,8 @@ class LlamaSession {
     for (int64_t i = 0; i < n; ++i)
       if (prompt[i] < 0 || prompt[i] >= c.vocab) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
     const size_t ri = static_cast<size_t>(row);
-    AM_RETURN_IF_ERROR(kvs[ri]->ReleaseSession(views[ri]));
-    auto vw = kvs[ri]->ReserveForSession(0, static_cast<size_t>(c.max_tokens));
+    AM_RETURN_IF_ERROR(kv->ReleaseSession(views[ri]));
+    auto vw = kv->ReserveSlot(ri, 0, static_cast<size_t>(c.max_tokens));
     if (!vw.ok()) return vw.status();
     views[ri] = vw.value();  // same slot planes: the decode plan and graph stay valid
     row_ready[ri] = 0;

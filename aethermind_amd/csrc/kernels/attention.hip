@@ -26,8 +26,11 @@
 //     writeback or invalidate, and no second launch.
 
 #include <cmath>
+#include <cstdio>
+#include <mutex>
 
 #include "am_kernel_common.h"
+#include "am_launch_timing.h"
 
 namespace am {
 namespace {
@@ -838,8 +841,11 @@ __global__ __launch_bounds__(kPreWaves * 64) void attention_prefill_kernel(AttnA
   }
 }
 
+int64_t GridBlocks(dim3 g) { return static_cast<int64_t>(g.x) * g.y * g.z; }
+
 template <int D>
 am_status_code LaunchPrefill(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  RecordLaunch(GridBlocks(grid), kPreWaves * 64, 0, "attention_prefill<d=%d,g=%d>", D, static_cast<int>(G));
   switch (G) {
     case 1: hipLaunchKernelGGL((attention_prefill_kernel<D, 1>), grid, dim3(kPreWaves * 64), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attention_prefill_kernel<D, 2>), grid, dim3(kPreWaves * 64), 0, s, a); break;
@@ -862,6 +868,8 @@ int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
 
 template <int D>
 am_status_code LaunchDecode(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  RecordLaunch(GridBlocks(grid), kDecWaves * 64, 0, "attention_decode<d=%d,g=%d,splits=%u>", D, static_cast<int>(G),
+               grid.x);
   switch (G) {
     case 1: hipLaunchKernelGGL((attention_decode_kernel<D, 1>), grid, dim3(kDecWaves * 64), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attention_decode_kernel<D, 2>), grid, dim3(kDecWaves * 64), 0, s, a); break;
@@ -875,6 +883,8 @@ am_status_code LaunchDecode(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t
 
 template <class A, int D>
 am_status_code LaunchD(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
+  RecordLaunch(GridBlocks(grid), kWaves * 64, 0, "attention_valu<%s,d=%d,g=%d,splits=%u>",
+               A::kDtype == AM_DT_BF16 ? "bf16" : "f32", D, static_cast<int>(G), grid.x);
   switch (G) {
     case 1: hipLaunchKernelGGL((attention_kernel<A, D, 1>), grid, dim3(kWaves * 64), 0, s, a); break;
     case 2: hipLaunchKernelGGL((attention_kernel<A, D, 2>), grid, dim3(kWaves * 64), 0, s, a); break;

@@ -22,6 +22,7 @@
 //     keeps each XCD's L2 working on neighbouring weight columns.
 
 #include "am_kernel_common.h"
+#include "am_launch_timing.h"
 
 namespace am {
 am_status_code GemvLinearRow(const void* x, int32_t act, const am_gfx950_weight& w, void* out, int32_t out_dtype,
@@ -374,6 +375,9 @@ extern "C" am_status_code am_gfx950_linear(const am_gfx950_linear_args* a, void*
       return true;
     }();
     if (!lds_ok) return SetLastError(AM_STATUS_INTERNAL, "gemm: could not raise the dynamic LDS limit");
+    RecordLaunch(tiles, 256, static_cast<int32_t>(kGemmLds), "gemm<%s,%dx%dx%d>",
+                 w.format == AM_WF_BF16 ? "bf16" : w.format == AM_WF_INT8 ? "int8" : "int4", static_cast<int>(BM),
+                 static_cast<int>(BN), static_cast<int>(BK));
     switch (w.format) {
       case AM_WF_BF16: hipLaunchKernelGGL((gemm_kernel<AM_WF_BF16, false>), grid, dim3(256), kGemmLds, s, g); break;
       case AM_WF_INT8: hipLaunchKernelGGL((gemm_kernel<AM_WF_INT8, false>), grid, dim3(256), kGemmLds, s, g); break;

@@ -21,6 +21,9 @@
 //     applies the reference op-boundary roundings of the nodes that were fused.
 
 #include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
 #include <cmath>
 
 #include "am_gemv_common.h"
@@ -866,9 +869,30 @@ __global__ __launch_bounds__(kSkWaves * 64) void gemv_ksplit_kernel(GemvArgs p) 
   }
 }
 
+const char* EpiName(int epi) {
+  switch (epi) {
+    case kEpiStore: return "store";
+    case kEpiResidual: return "residual";
+    case kEpiQkv: return "qkv";
+    case kEpiGateUp: return "gate_up";
+    default: return "lm_head";
+  }
+}
+
+const char* WfName(int wf) {
+  switch (wf) {
+    case AM_WF_F32: return "f32";
+    case AM_WF_BF16: return "bf16";
+    case AM_WF_INT8: return "int8";
+    default: return "int4";
+  }
+}
+
 template <class A, int WF, int EPI>
 am_status_code LaunchKsplit(const GemvArgs& g, hipStream_t s) {
   const int64_t blocks = CeilDiv(g.n, kSkRows);
+  RecordLaunch(blocks, kSkWaves * 64, 0, "gemv_ksplit<%s,%s,%s>", A::kDtype == AM_DT_BF16 ? "bf16" : "f32",
+               WfName(WF), EpiName(EPI));
   LaunchTiming& lt = ThreadLaunchTiming();
   if (lt.start != nullptr) {
     hipExtLaunchKernelGGL((gemv_ksplit_kernel<A, WF, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kSkWaves * 64),
@@ -884,6 +908,9 @@ am_status_code LaunchKsplit(const GemvArgs& g, hipStream_t s) {
 
 template <class A, int WF, bool NORM, int EPI, int JM, int P, int NW, bool ONE>
 am_status_code LaunchGrid(const GemvArgs& g, int64_t blocks, int64_t lds, hipStream_t s) {
+  RecordLaunch(blocks, NW * 64, static_cast<int32_t>(lds), "gemv<%s,%s,%s,norm=%d,jm=%d,p=%d,nw=%d,one=%d>",
+               A::kDtype == AM_DT_BF16 ? "bf16" : "f32", WfName(WF), EpiName(EPI), NORM ? 1 : 0, JM, P, NW,
+               ONE ? 1 : 0);
   LaunchTiming& lt = ThreadLaunchTiming();
   if (lt.start != nullptr) {
     hipExtLaunchKernelGGL((gemv_kernel<A, WF, NORM, EPI, JM, P, NW, ONE>), dim3(static_cast<unsigned>(blocks)),
@@ -1024,6 +1051,17 @@ LaunchTiming& ThreadLaunchTiming() noexcept {
   return t;
 }
 
+void RecordLaunch(int64_t grid, int32_t block_threads, int32_t lds_bytes, const char* fmt, ...) noexcept {
+  LaunchTiming& t = ThreadLaunchTiming();
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(t.kernel, sizeof(t.kernel), fmt, ap);
+  va_end(ap);
+  t.grid = grid;
+  t.block_threads = block_threads;
+  t.lds_bytes = lds_bytes;
+}
+
 // Linear rows for am_gfx950_linear (decode GEMV; also the row loop of small m).
 am_status_code GemvLinearRow(const void* x, int32_t act, const am_gfx950_weight& w, void* out, int32_t out_dtype,
                              const void* residual, hipStream_t s) {
@@ -1104,6 +1142,17 @@ extern "C" am_status_code am_gfx950_fused_gate_up(const am_gfx950_fused_gate_up_
   g.eps = a->eps;
   g.out = a->act_out;
   return Dispatch<true, kEpiGateUp>(a->dtype, a->w_gate_up.format, g, AsStream(stream));
+}
+
+extern "C" am_status_code am_gfx950_last_launch(am_gfx950_launch_info* out) {
+  AM_CHECK_ARG(out != nullptr, "last_launch: null out");
+  const LaunchTiming& t = ThreadLaunchTiming();
+  std::memcpy(out->kernel, t.kernel, sizeof(out->kernel));
+  out->kernel[sizeof(out->kernel) - 1] = 0;
+  out->grid = t.grid;
+  out->block_threads = t.block_threads;
+  out->lds_bytes = t.lds_bytes;
+  return AM_STATUS_OK;
 }
 
 extern "C" int64_t am_gfx950_lm_head_workspace_bytes(void) {

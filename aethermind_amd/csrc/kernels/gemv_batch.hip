@@ -458,6 +458,8 @@ am_status_code LaunchBatch(const BatchArgs& a, size_t lds, hipStream_t s) {
     cached_lds = lds;
   }
   const int64_t blocks = std::min<int64_t>(a.units, static_cast<int64_t>(DeviceCUs()) * cached_blocks);
+  RecordLaunch(blocks, kBWaves * 64, static_cast<int32_t>(lds), "gemv_batch<wf=%d,epi=%d,norm=%d,tpb=%d,r=%d>", WF, EPI,
+               NORM ? 1 : 0, TPB, R);
   LaunchTiming& lt = ThreadLaunchTiming();
   if (lt.start != nullptr) {
     hipExtLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kBWaves * 64), lds, s, lt.start, lt.stop, 0,

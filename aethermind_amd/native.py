@@ -112,6 +112,10 @@ class FusedLmHeadArgs(C.Structure):
                 ("workspace_bytes", i64), ("rows", i64), ("hist_stride", i64)]
 
 
+class LaunchInfo(C.Structure):
+    _fields_ = [("kernel", C.c_char * 96), ("grid", i64), ("block_threads", i32), ("lds_bytes", i32)]
+
+
 class DecodeLayer(C.Structure):
     _fields_ = [("w_qkv", Weight), ("w_o", Weight), ("w_gate_up", Weight), ("w_down", Weight), ("in_norm", vp),
                 ("post_norm", vp), ("k_cache", vp), ("v_cache", vp)]
@@ -147,6 +151,7 @@ _SIGS = {
     "am_gfx950_error_code": (i32, [vp]),
     "am_gfx950_error_message": (C.c_char_p, [vp]),
     "am_gfx950_device_count": (i32, []),
+    "am_gfx950_last_launch": (i32, [C.POINTER(LaunchInfo)]),
     "am_gfx950_version": (C.c_char_p, []),
     "am_gfx950_embedding": (i32, [C.POINTER(EmbeddingArgs), vp]),
     "am_gfx950_embed_token": (i32, [vp, vp, i32, i64, i64, vp, vp, vp]),
@@ -253,6 +258,13 @@ def lib() -> Lib:
     if _LIB is None:
         _LIB = Lib()
     return _LIB
+
+
+def last_launch() -> LaunchInfo:
+    """The last kernel an entry point launched on this thread (name and launch shape)."""
+    info = LaunchInfo()
+    lib().call("am_gfx950_last_launch", C.byref(info))
+    return info
 
 
 def header_functions(include_dir: str) -> list[str]:

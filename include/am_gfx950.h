@@ -186,6 +186,7 @@ am_status_code am_gfx950_attention(const am_gfx950_attention_args* args, void* h
 int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
                                             int64_t head_dim, int64_t capacity, int32_t num_splits);
 
+
 /* OpType::kSiluMul (silu_mul_op.cpp:32-61; formula const_eval_silu_mul.cpp:18-31). */
 typedef struct am_gfx950_silu_mul_args {
   const void* gate;
@@ -435,6 +436,20 @@ am_status_code am_gfx950_decode_layers_validate(const am_gfx950_decode_layers_ar
  * timed out (the grid was not resident at once); the workspace must then be
  * zero-filled again.  Synchronous. */
 am_status_code am_gfx950_decode_layers_aborted(const void* workspace, int32_t* out);
+
+/* Host-side record of the last kernel an entry point of this library launched on the
+ * calling thread: kernel family and template variant (e.g.
+ * "gemv<bf16,int4,gate_up,norm=1,jm=2,p=1,nw=8,one=0>"), grid size in blocks,
+ * threads per block and dynamic LDS bytes.  No counterpart in the reference (its
+ * kernels are plain CPU functions): it lets a caller or a test confirm which kernel
+ * variant a shape reached. */
+typedef struct am_gfx950_launch_info {
+  char kernel[96];
+  int64_t grid;
+  int32_t block_threads;
+  int32_t lds_bytes;
+} am_gfx950_launch_info;
+am_status_code am_gfx950_last_launch(am_gfx950_launch_info* out);
 
 /* Library / device information. */
 int32_t am_gfx950_device_count(void);

@@ -218,6 +218,51 @@ void TestKV() {
     auto v = m.ReserveForSession(6, 4);
     CHECK(!v.ok() && v.status().code() == StatusCode::kOutOfRange);
   }
+  {  // slot pool: one allocation, slot r's planes a fixed stride after slot 0's
+    KVCacheManager m(HostTestAllocator());
+    CHECK(m.Init(2, 2, 40, 8, KVType(), 256, 4).ok());
+    CHECK(m.num_slots() == 4 && m.free_slots() == 4);
+    const size_t plane = 2u * 2 * 40 * 8 * 2;           // 2560 bytes, padded to 2560
+    CHECK(m.storage().slot_bytes == 2 * plane && m.total_bytes() == 4 * 2 * plane);
+    std::vector<KVCacheView> vs;
+    for (int r = 0; r < 4; ++r) {
+      auto v = m.ReserveForSession(3, 5);
+      CHECK(v.ok() && v->slot() == static_cast<size_t>(r));
+      if (v.ok()) vs.push_back(v.value());
+    }
+    CHECK(m.free_slots() == 0);
+    auto full = m.ReserveForSession(1, 1);
+    CHECK(!full.ok() && full.status().code() == StatusCode::kFailedPrecondition);
+    CHECK(vs.size() == 4);
+    if (vs.size() == 4) {
+      const auto base_k = static_cast<char*>(vs[0].KeyPlane(0).value());
+      for (int r = 0; r < 4; ++r) {
+        CHECK(static_cast<char*>(vs[r].KeyPlane(1).value()) - base_k ==
+              static_cast<std::ptrdiff_t>(r * m.storage().slot_bytes + m.layout().layer_stride));
+        CHECK(static_cast<char*>(vs[r].ValuePlane(0).value()) - static_cast<char*>(vs[r].KeyPlane(0).value()) ==
+              static_cast<std::ptrdiff_t>(plane));
+      }
+      // slots are independent: commits and releases touch only their own slot
+      CHECK(vs[2].CommitUntil(7).ok() && vs[1].current_pos() == 3 && vs[2].current_pos() == 7);
+      CHECK(m.ReleaseSession(vs[1]).ok());
+      CHECK(!vs[1].valid() && vs[0].valid() && vs[2].valid() && m.free_slots() == 1);
+      auto again = m.ReserveSlot(1, 0, 40);
+      CHECK(again.ok() && again->slot() == 1 && again->current_pos() == 0);
+      auto taken = m.ReserveSlot(2, 0, 1);
+      CHECK(!taken.ok() && taken.status().code() == StatusCode::kFailedPrecondition);
+      auto bad = m.ReserveSlot(4, 0, 1);
+      CHECK(!bad.ok() && bad.status().code() == StatusCode::kOutOfRange);
+      // the pool is not rebuilt under active reservations
+      CHECK(m.Init(1, 1, 8, 8, KVType(), 64).code() == StatusCode::kFailedPrecondition);
+    }
+  }
+  {  // zero slots, zero dimensions, bad alignment
+    KVCacheManager m(HostTestAllocator());
+    CHECK(m.Init(1, 1, 8, 8, KVType(), 64, 0).code() == StatusCode::kInvalidArgument);
+    CHECK(m.Init(1, 0, 8, 8, KVType(), 64).code() == StatusCode::kInvalidArgument);
+    CHECK(m.Init(1, 1, 8, 8, KVType(), 48).code() == StatusCode::kInvalidArgument);
+    CHECK(!m.ReserveForSession(1, 1).ok());
+  }
 }
 
 // ---------------------------------------------------------------- executor
