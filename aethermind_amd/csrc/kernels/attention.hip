@@ -909,6 +909,80 @@ extern "C" int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t se
   return tickets + batch * seq * hq * splits * (head_dim + 2) * 4;
 }
 
+// ---- zero-allocation variant -----------------------------------------------------
+// The split tickets and records live in this file-scope device array instead of a
+// caller workspace.  Its name is only a host-side handle: host code uses the address
+// hipGetSymbolAddress returns for the current device (each device holds its own copy).
+constexpr int64_t kNoAllocScratchBytes = int64_t{8} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+__global__ void scratch_zero_kernel(uint32_t* p, int64_t words) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+am_status_code ScratchAddress(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return SetLastError(AM_STATUS_INTERNAL, "attention_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return SetLastError(AM_STATUS_INTERNAL, "attention_noalloc: hipGetSymbolAddress(scratch) failed");
+    g_scratch_dev[dev] = ptr;
+  }
+  *out = g_scratch_dev[dev];
+  return AM_STATUS_OK;
+}
+}  // namespace
+
+extern "C" int64_t am_gfx950_attention_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" am_status_code am_gfx950_attention_noalloc(const am_gfx950_attention_args* a, void* stream) {
+  AM_CHECK_ARG(a != nullptr, "attention_noalloc: null args");
+  AM_CHECK_ARG(a->workspace == nullptr && a->workspace_bytes == 0,
+               "attention_noalloc: pass no workspace (the split records use the library's device scratch)");
+  AM_CHECK_ARG(a->hq > 0 && a->hkv > 0 && a->seq > 0 && a->capacity > 0 && a->head_dim > 0,
+               "attention_noalloc: bad shape");
+  const int64_t batch = a->batch > 0 ? a->batch : 1;
+  AM_CHECK_ARG(batch * a->seq <= 65535, "attention: too many query rows");
+  const int64_t need = am_gfx950_attention_workspace_bytes(batch, a->seq, a->hq, a->hkv, a->head_dim, a->capacity,
+                                                           a->num_splits);
+  if (need > kNoAllocScratchBytes) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg), "attention_noalloc: needs %lld bytes of split scratch, the maximum is %lld",
+                  static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+    return SetLastError(AM_STATUS_RESOURCE_EXHAUSTED, msg);
+  }
+  hipStream_t s = AsStream(stream);
+  if (s != nullptr) {
+    int cur = -1, sdev = -1;
+    if (hipGetDevice(&cur) != hipSuccess || hipStreamGetDevice(s, &sdev) != hipSuccess || cur != sdev)
+      return SetLastError(AM_STATUS_INVALID_ARGUMENT, "attention_noalloc: the stream's device is not the current device");
+  }
+  am_gfx950_attention_args b = *a;
+  if (need > 0) {
+    void* ptr = nullptr;
+    if (auto st = ScratchAddress(&ptr); st != AM_STATUS_OK) return st;
+    // the tickets must start at zero: clear them with a kernel (capturable, no memset)
+    const int64_t ticket_words = 64 * CeilDiv(batch * a->seq * a->hkv * 4, 256);
+    hipLaunchKernelGGL(scratch_zero_kernel, dim3(static_cast<unsigned>(CeilDiv(ticket_words, 256))), dim3(256), 0, s,
+                       static_cast<uint32_t*>(ptr), ticket_words);
+    AM_RETURN_IF_LAUNCH_FAILED("attention_noalloc");
+    b.workspace = ptr;
+    b.workspace_bytes = kNoAllocScratchBytes;
+  }
+  return am_gfx950_attention(&b, stream);
+}
+
 extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a, void* stream) {
   AM_CHECK_ARG(a != nullptr, "attention: null args");
   AM_CHECK_ARG(a->dtype == AM_DT_F32 || a->dtype == AM_DT_BF16, "attention: dtype must be f32 or bf16");

@@ -162,6 +162,8 @@ _SIGS = {
     "am_gfx950_kv_update": (i32, [C.POINTER(KvUpdateArgs), vp]),
     "am_gfx950_attention": (i32, [C.POINTER(AttentionArgs), vp]),
     "am_gfx950_attention_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64, i32]),
+    "am_gfx950_attention_noalloc": (i32, [C.POINTER(AttentionArgs), vp]),
+    "am_gfx950_attention_noalloc_max_bytes": (i64, []),
     "am_gfx950_silu_mul": (i32, [C.POINTER(SiluMulArgs), vp]),
     "am_gfx950_add": (i32, [C.POINTER(AddArgs), vp]),
     "am_gfx950_argmax": (i32, [C.POINTER(ArgmaxArgs), vp]),

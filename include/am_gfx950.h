@@ -186,6 +186,19 @@ am_status_code am_gfx950_attention(const am_gfx950_attention_args* args, void* h
 int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
                                             int64_t head_dim, int64_t capacity, int32_t num_splits);
 
+/* am_gfx950_attention without a caller workspace and without any allocation: the
+ * split tickets and records live in a file-scope device array of
+ * am_gfx950_attention_noalloc_max_bytes() bytes (8 MiB) that each device holds until
+ * the process ends.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * args->workspace must be NULL and args->workspace_bytes 0; a shape whose
+ * am_gfx950_attention_workspace_bytes exceeds the maximum is rejected with
+ * AM_STATUS_RESOURCE_EXHAUSTED.  Each call clears its tickets with a kernel on
+ * hip_stream (no memset), then launches the same kernels as am_gfx950_attention.
+ * Every call on one device shares that device's array: calls that overlap on one
+ * device (different streams, concurrently) race and must not be issued. */
+am_status_code am_gfx950_attention_noalloc(const am_gfx950_attention_args* args, void* hip_stream);
+int64_t am_gfx950_attention_noalloc_max_bytes(void);
 
 /* OpType::kSiluMul (silu_mul_op.cpp:32-61; formula const_eval_silu_mul.cpp:18-31). */
 typedef struct am_gfx950_silu_mul_args {
