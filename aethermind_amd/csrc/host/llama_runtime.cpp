@@ -992,6 +992,7 @@ using aethermind::llama::LlamaSession;
 struct am_runtime {
   int device = 0;
   hipStream_t stream = nullptr;
+  am_config_t config{};  // load options of am_model_load
 };
 struct am_model {
   am_runtime* rt = nullptr;
@@ -999,6 +1000,8 @@ struct am_model {
 };
 struct am_session {
   std::unique_ptr<LlamaSession> impl;
+  uint32_t max_tokens = 0;  // am_session_config_t generation limits (PRD interface)
+  int64_t eos = -1;
 };
 
 namespace {
@@ -1010,7 +1013,19 @@ am_status_code Ret(const Status& s) {
 
 extern "C" {
 
-am_status_code am_runtime_create(int32_t device, am_runtime** out) {
+static am_config_t DefaultConfig(int32_t device) {
+  am_config_t c{};
+  c.struct_size = sizeof(am_config_t);
+  c.device = device;
+  c.act_dtype = AM_DT_BF16;
+  c.weight_format = AM_WF_INT4;
+  c.group_size = 128;
+  c.max_tokens = 4096;
+  c.max_prefill_chunk = 512;
+  return c;
+}
+
+am_status_code am_runtime_open(int32_t device, am_runtime** out) {
   if (out == nullptr) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "runtime: null out");
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
@@ -1019,6 +1034,7 @@ am_status_code am_runtime_create(int32_t device, am_runtime** out) {
   if (hipSetDevice(device) != hipSuccess) return am::SetLastError(AM_STATUS_INTERNAL, "hipSetDevice failed");
   auto* rt = new am_runtime();
   rt->device = device;
+  rt->config = DefaultConfig(device);
   if (hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking) != hipSuccess) {
     delete rt;
     return am::SetLastError(AM_STATUS_INTERNAL, "hipStreamCreate failed");
@@ -1174,7 +1190,7 @@ am_status_code am_model_buffer(am_model* m, int32_t kind, int32_t layer, void** 
   return AM_STATUS_OK;
 }
 
-am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out) {
+am_status_code am_session_open(am_model* m, const am_session_options* opt, am_session** out) {
   if (!m || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "session: null argument");
   auto s = std::make_unique<am_session>();
   s->impl = std::make_unique<LlamaSession>();
@@ -1216,7 +1232,7 @@ am_status_code am_session_decode_async(am_session* s, int64_t n) {
   return Ret(st);
 }
 
-am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new, int64_t eos,
+am_status_code am_session_generate_ids(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new, int64_t eos,
                                    int64_t* tokens_out, int64_t* n_out) {
   if (!s || !prompt || !tokens_out || max_new <= 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "generate: bad argument");
   if (s->impl->B != 1) return am::SetLastError(AM_STATUS_UNIMPLEMENTED, "generate: single-sequence sessions only");
@@ -1271,5 +1287,94 @@ am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by
   if (!s || !ms_by_op || !count_by_op || n <= 0) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "profile: bad argument");
   return Ret(s->impl->Profile(n, ms_by_op, count_by_op));
 }
+
+// ---- the PRD's Phase-1 interface (aethermind_prd.md:298-320) over the calls above ----
+
+am_runtime_t am_runtime_create(const am_config_t* config) {
+  am_config_t c = DefaultConfig(0);
+  if (config != nullptr) {
+    if (config->struct_size < sizeof(am_config_t)) {
+      (void)am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "am_config_t: struct_size too small");
+      return nullptr;
+    }
+    c = *config;
+    c.struct_size = sizeof(am_config_t);
+  }
+  am_runtime* rt = nullptr;
+  if (am_runtime_open(c.device, &rt) != AM_STATUS_OK) return nullptr;
+  rt->config = c;
+  return rt;
+}
+
+static void SetError(am_error_t* error, am_status_code code) {
+  if (error != nullptr)
+    *error = code == AM_STATUS_OK ? nullptr : am_gfx950_error_create(code, am_last_error_message());
+}
+
+am_model_t am_model_load(am_runtime_t runtime, const char* path, am_error_t* error) {
+  if (error != nullptr) *error = nullptr;
+  if (runtime == nullptr || path == nullptr) {
+    SetError(error, am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_load: null runtime or path"));
+    return nullptr;
+  }
+  const am_config_t& c = runtime->config;
+  const am_model_load_options opt{c.act_dtype, c.weight_format, c.group_size, c.max_tokens, c.max_prefill_chunk};
+  am_model* m = nullptr;
+  const am_status_code rc = am_model_load_hf(runtime, path, &opt, &m);
+  SetError(error, rc);
+  return rc == AM_STATUS_OK ? m : nullptr;
+}
+
+void am_model_unload(am_model_t model) { am_model_destroy(model); }
+
+am_session_t am_session_create(am_model_t model, const am_session_config_t* config) {
+  if (config != nullptr && config->struct_size < sizeof(am_session_config_t)) {
+    (void)am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "am_session_config_t: struct_size too small");
+    return nullptr;
+  }
+  const am_session_options opt{1, config != nullptr ? config->use_graph : 1, 1, 0};
+  am_session* s = nullptr;
+  if (am_session_open(model, &opt, &s) != AM_STATUS_OK) return nullptr;
+  if (config != nullptr) {
+    s->max_tokens = config->max_tokens;
+    s->eos = config->eos_token_id;
+  }
+  return s;
+}
+
+int am_session_generate(am_session_t session, const uint32_t* input_tokens, size_t input_len,
+                        uint32_t* output_tokens, size_t output_capacity, size_t* output_len,
+                        am_error_t* error) {
+  if (error != nullptr) *error = nullptr;
+  if (output_len != nullptr) *output_len = 0;
+  auto fail = [&](am_status_code code, const char* msg) {
+    SetError(error, am::SetLastError(code, msg));
+    return static_cast<int>(code);
+  };
+  if (session == nullptr || input_tokens == nullptr || output_tokens == nullptr || output_len == nullptr)
+    return fail(AM_STATUS_INVALID_ARGUMENT, "generate: null argument");
+  if (input_len == 0 || output_capacity == 0) return fail(AM_STATUS_INVALID_ARGUMENT, "generate: empty prompt or output");
+  const int64_t cap = session->impl->m->cfg.max_tokens;
+  if (input_len >= static_cast<size_t>(cap))
+    return fail(AM_STATUS_OUT_OF_RANGE, "generate: the prompt leaves no KV capacity for a new token");
+  // new tokens: the output capacity, the session's limit and the KV positions left
+  // (the last generated token is never written to the cache)
+  int64_t max_new = static_cast<int64_t>(std::min<size_t>(output_capacity, static_cast<size_t>(cap) - input_len));
+  if (session->max_tokens > 0) max_new = std::min<int64_t>(max_new, session->max_tokens);
+  std::vector<int64_t> prompt(input_tokens, input_tokens + input_len);
+  std::vector<int64_t> out(static_cast<size_t>(max_new));
+  int64_t n = 0;
+  const am_status_code rc = am_session_generate_ids(session, prompt.data(), static_cast<int64_t>(input_len), max_new,
+                                                    session->eos, out.data(), &n);
+  if (rc != AM_STATUS_OK) {
+    SetError(error, rc);
+    return static_cast<int>(rc);
+  }
+  for (int64_t i = 0; i < n; ++i) output_tokens[i] = static_cast<uint32_t>(out[static_cast<size_t>(i)]);
+  *output_len = static_cast<size_t>(n);
+  return AM_STATUS_OK;
+}
+
+void am_error_free(am_error_t error) { am_gfx950_error_destroy(error); }
 
 }  // extern "C"

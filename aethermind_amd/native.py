@@ -139,6 +139,15 @@ class ModelLoadOptions(C.Structure):
                 ("max_prefill_chunk", i32)]
 
 
+class Config(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("device", i32), ("act_dtype", i32), ("weight_format", i32),
+                ("group_size", i32), ("max_tokens", i32), ("max_prefill_chunk", i32)]
+
+
+class SessionConfig(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("max_tokens", C.c_uint32), ("eos_token_id", i64), ("use_graph", i32)]
+
+
 class SessionOptions(C.Structure):
     _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32)]
 
@@ -187,7 +196,7 @@ _SIGS = {
     "am_gfx950_decode_layers_aborted": (i32, [vp, C.POINTER(i32)]),
     "am_gfx950_decode_advance": (i32, [vp, vp, vp, vp, vp]),
     "am_gfx950_decode_advance_rows": (i32, [vp, i64, vp, i64, vp, vp, vp]),
-    "am_runtime_create": (i32, [i32, C.POINTER(vp)]),
+    "am_runtime_open": (i32, [i32, C.POINTER(vp)]),
     "am_runtime_destroy": (None, [vp]),
     "am_runtime_stream": (vp, [vp]),
     "am_runtime_synchronize": (i32, [vp]),
@@ -199,7 +208,7 @@ _SIGS = {
     "am_hf_inspect": (i32, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(i64), C.POINTER(i64)]),
     "am_model_buffer": (i32, [vp, i32, i32, C.POINTER(vp), C.POINTER(i64)]),
     "am_model_weight_bytes_total": (i64, [vp]),
-    "am_session_create": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
+    "am_session_open": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
     "am_session_destroy": (None, [vp]),
     "am_session_prefill": (i32, [vp, vp, i64, C.POINTER(i64)]),
     "am_session_prefill_row": (i32, [vp, i64, vp, i64, C.POINTER(i64)]),
@@ -207,7 +216,13 @@ _SIGS = {
     "am_session_row_position": (i64, [vp, i64]),
     "am_session_decode": (i32, [vp, i64, vp]),
     "am_session_decode_async": (i32, [vp, i64]),
-    "am_session_generate": (i32, [vp, vp, i64, i64, i64, vp, C.POINTER(i64)]),
+    "am_session_generate_ids": (i32, [vp, vp, i64, i64, i64, vp, C.POINTER(i64)]),
+    "am_runtime_create": (vp, [C.POINTER(Config)]),
+    "am_model_load": (vp, [vp, C.c_char_p, C.POINTER(vp)]),
+    "am_model_unload": (None, [vp]),
+    "am_session_create": (vp, [vp, C.POINTER(SessionConfig)]),
+    "am_session_generate": (i32, [vp, vp, C.c_size_t, vp, C.c_size_t, C.POINTER(C.c_size_t), C.POINTER(vp)]),
+    "am_error_free": (None, [vp]),
     "am_session_logits": (i32, [vp, vp]),
     "am_session_position": (i64, [vp]),
     "am_session_decode_plan_size": (i64, [vp]),

@@ -140,14 +140,14 @@ def run_long(args, N, L):
     if P + args.warmup + steps + args.profile_steps + 2 > CAP:
         raise SystemExit("prompt + warmup + steps + profile exceed the 32768-token KV cache")
     rt = N.vp()
-    L.call("am_runtime_create", 0, C.byref(rt))
+    L.call("am_runtime_open", 0, C.byref(rt))
     mc = N.ModelConfig(SHAPE["num_layers"], SHAPE["hidden"], SHAPE["num_q_heads"], SHAPE["num_kv_heads"],
                        SHAPE["head_dim"], SHAPE["ffn"], SHAPE["vocab"], SHAPE["rms_eps"], SHAPE["rope_theta"],
                        N.AM_DT_BF16, 3, 128, CAP, CHUNK)
     m = N.vp()
     L.call("am_model_create_synthetic", rt, C.byref(mc), 1, C.byref(m))
     s = N.vp()
-    L.call("am_session_create", m, C.byref(N.SessionOptions(1, 1, B)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, B)), C.byref(s))
     prompts = []
     for r in range(B):
         pr = np.empty(P, np.int64)
@@ -261,7 +261,7 @@ def main():
         raise SystemExit("prompt + warmup + steps + profile exceed the 4096-token KV cache")
 
     rt = N.vp()
-    L.call("am_runtime_create", 0, C.byref(rt))
+    L.call("am_runtime_open", 0, C.byref(rt))
     mc = N.ModelConfig(SHAPE["num_layers"], SHAPE["hidden"], SHAPE["num_q_heads"], SHAPE["num_kv_heads"],
                        SHAPE["head_dim"], SHAPE["ffn"], SHAPE["vocab"], SHAPE["rms_eps"], SHAPE["rope_theta"],
                        N.AM_DT_BF16, cfgd["weight_format"], 128, max_tokens, 512)
@@ -271,7 +271,7 @@ def main():
     log(f"model {cfgd['name']} created in {time.perf_counter() - t0:.1f}s; linear weight bytes/token "
         f"{L.am_model_weight_bytes_total(m)}")
     s = N.vp()
-    L.call("am_session_create", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
 
     import numpy as np
     prompt = np.empty(args.prompt, np.int64)

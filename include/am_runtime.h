@@ -8,11 +8,18 @@
  * design on one GPU: one HIP stream per runtime, weights repacked into HBM at model
  * creation, a device-resident static KV cache, and a frozen decode plan replayed as a
  * HIP graph with device-resident position/token state (no host sync per token).
- * Token ids are int64 (the graph input dtype, model_graph_builder.cpp:339-342).
+ *
+ * Two layers: the PRD's own Phase-1 interface (am_runtime_create(config),
+ * am_model_load, am_session_create(config), am_session_generate with uint32 token ids,
+ * am_error_t) at the end of this file, and the extended interface it is built on
+ * (am_runtime_open, am_model_create_synthetic / am_model_load_hf, am_session_open,
+ * prefill / decode / batched rows / profiling; int64 token ids, the graph input dtype of
+ * model_graph_builder.cpp:339-342).
  */
 #ifndef AM_RUNTIME_H
 #define AM_RUNTIME_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "am_c_api.h"
@@ -60,7 +67,7 @@ typedef enum am_model_buffer_kind {
   AM_BUF_ROPE_SIN = 5
 } am_model_buffer_kind;
 
-am_status_code am_runtime_create(int32_t device, am_runtime** out);
+am_status_code am_runtime_open(int32_t device, am_runtime** out);
 void am_runtime_destroy(am_runtime* rt);
 void* am_runtime_stream(am_runtime* rt); /* hipStream_t */
 /* Blocks until all work enqueued on the runtime's stream has finished; reports an
@@ -111,7 +118,7 @@ typedef struct am_session_options {
                                 per-op fused plan (default) */
 } am_session_options;
 
-am_status_code am_session_create(am_model* m, const am_session_options* opt, am_session** out);
+am_status_code am_session_open(am_model* m, const am_session_options* opt, am_session** out);
 void am_session_destroy(am_session* s);
 /* Prefill the prompt (host ids) from position 0; returns the first generated token.
  * In a batched session this prefills sequence 0. */
@@ -130,7 +137,7 @@ am_status_code am_session_decode(am_session* s, int64_t n, int64_t* tokens_out);
 am_status_code am_session_decode_async(am_session* s, int64_t n);
 /* Prefill + greedy decode up to max_new tokens (stops after eos if eos >= 0).
  * Single-sequence sessions only. */
-am_status_code am_session_generate(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
+am_status_code am_session_generate_ids(am_session* s, const int64_t* prompt, int64_t n_prompt, int64_t max_new,
                                    int64_t eos, int64_t* tokens_out, int64_t* n_out);
 /* fp32 logits [batch][vocab] of the most recent step (host copy). */
 am_status_code am_session_logits(am_session* s, float* out);
@@ -149,6 +156,54 @@ int32_t am_session_persistent_decode(am_session* s);
  * (array of at least 64 doubles, indexed by OpType) and launch counts into
  * count_by_op. */
 am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by_op, int64_t* count_by_op);
+
+/* ---------------- the PRD's Phase-1 C ABI (aethermind_prd.md:298-320) ----------------
+ * Token ids are the only data boundary and are uint32 (prd.md:158-185).  Config structs
+ * start with struct_size and only grow at the end (the PRD's ABI v1.x rules,
+ * prd.md:322-327).  Errors: am_runtime_create / am_session_create return NULL (the text
+ * is in am_last_error_message()); am_model_load and am_session_generate also fill
+ * *error (when error != NULL) with an error object of this library, read with
+ * am_gfx950_error_code / am_gfx950_error_message and released with am_error_free.  (The
+ * PRD's am_error_message reads the reference library's own error objects, c_api.h:88.) */
+typedef am_runtime* am_runtime_t;
+typedef am_model* am_model_t;
+typedef am_session* am_session_t;
+typedef am_error_handle am_error_t;
+
+typedef struct am_config {
+  uint32_t struct_size;      /* sizeof(am_config_t) */
+  int32_t device;            /* HIP device index */
+  int32_t act_dtype;         /* activations of loaded models: AM_DT_BF16 or AM_DT_F32 */
+  int32_t weight_format;     /* am_weight_format the loader converts / quantizes to */
+  int32_t group_size;        /* INT4 group along k (128) */
+  int32_t max_tokens;        /* static KV capacity per sequence (positions) */
+  int32_t max_prefill_chunk; /* rows per prefill pass */
+} am_config_t;
+
+typedef struct am_session_config {
+  uint32_t struct_size;  /* sizeof(am_session_config_t) */
+  uint32_t max_tokens;   /* GenerationConfig.max_tokens: tokens per generate call, 0 = no limit */
+  int64_t eos_token_id;  /* GenerationConfig.eos_token_id, -1 = none */
+  int32_t use_graph;     /* 1: decode steps replayed as a HIP graph (default) */
+} am_session_config_t;
+
+/* Runtime on config->device (NULL config: device 0, bf16 activations, INT4 g128
+ * weights, 4096 positions, 512-row prefill chunks). */
+am_runtime_t am_runtime_create(const am_config_t* config);
+/* A Hugging Face checkpoint directory (see am_model_load_hf), converted to the
+ * runtime's activation dtype and weight format. */
+am_model_t am_model_load(am_runtime_t runtime, const char* path, am_error_t* error);
+void am_model_unload(am_model_t model);
+/* Single-sequence session with the fused decode plan (NULL config: graph on, no token
+ * limit, no eos). */
+am_session_t am_session_create(am_model_t model, const am_session_config_t* config);
+/* Prefill input_tokens from position 0 and decode greedily: up to output_capacity
+ * tokens, the session's max_tokens and the KV capacity left after the prompt,
+ * stopping after eos_token_id.  Writes *output_len; returns an am_status_code. */
+int am_session_generate(am_session_t session, const uint32_t* input_tokens, size_t input_len,
+                        uint32_t* output_tokens, size_t output_capacity, size_t* output_len,
+                        am_error_t* error);
+void am_error_free(am_error_t error);
 
 #ifdef __cplusplus
 }

@@ -11,7 +11,13 @@ decode steps (33 tokens).  Stored per step: the greedy token, the top-16 (index,
 logits, the gap between the two largest logits (a near-tie tells the test where a
 divergence is admissible) and the logits at every 257th vocabulary index.
 
-CPU only, all host cores; about 3-6 minutes per format:
+The same steps are then recomputed on the oracle's fp64-accumulation path, fed the same
+tokens: the per-step error between the two paths (same metric as the GPU test) and
+the steps where their greedy tokens differ measure how far two valid summation orders
+of the same bf16 composition drift apart over 32 layers.  That spread sets the GPU
+test's logit bar.
+
+CPU only, all host cores; about 15 minutes per format:
     python tests/golden/make_8b_golden.py int4 [int8 bf16]
 """
 import os
@@ -55,11 +61,27 @@ def main(fmts):
             gap.append(logits[order[0]] - logits[order[1]])
             sample.append(logits[::SAMPLE_STRIDE].copy())
             print(f"[{fmt}] step {step}: token {t} gap {gap[-1]:.4g} ({time.time() - t0:.0f} s)", flush=True)
+        # the fp64 path over the same tokens (it rewrites every cache row it reads)
+        m.set_fast(False)
+        self_err, self_flip = [], []
+        for step in range(STEPS):
+            if step == 0:
+                lg = m.forward(prompt, 0)
+            else:
+                lg = m.forward(np.array([toks[step - 1]], np.int64), PROMPT + step - 1)
+            scale = float(np.max(np.abs(top_val[step])))
+            e = max(float(np.max(np.abs(lg[top_idx[step]] - top_val[step]))),
+                    float(np.max(np.abs(lg[::SAMPLE_STRIDE] - sample[step])))) / scale
+            self_err.append(e)
+            self_flip.append(int(O.argmax(lg) != toks[step]))
+            print(f"[{fmt}] fp64 step {step}: error {e:.4g} token {'differs' if self_flip[-1] else 'same'} "
+                  f"({time.time() - t0:.0f} s)", flush=True)
         m.close()
         np.savez(os.path.join(HERE, f"llama8b_{fmt}_seed1.npz"), prompt=prompt, tokens=np.array(toks, np.int64),
                  top_idx=np.array(top_idx, np.int64), top_val=np.array(top_val, np.float32),
                  top2_gap=np.array(gap, np.float32), sample=np.array(sample, np.float32),
-                 sample_stride=np.int64(SAMPLE_STRIDE))
+                 sample_stride=np.int64(SAMPLE_STRIDE), self_err=np.array(self_err, np.float32),
+                 self_flip=np.array(self_flip, np.int64))
         print(f"[{fmt}] tokens {toks}", flush=True)
 
 

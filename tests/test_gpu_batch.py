@@ -236,7 +236,7 @@ def test_attention_decode_long_context_batch4():
 class _Rt:
     def __init__(self):
         self.rt = N.vp()
-        L.call("am_runtime_create", 0, C.byref(self.rt))
+        L.call("am_runtime_open", 0, C.byref(self.rt))
 
     def close(self):
         L.am_runtime_destroy(self.rt)
@@ -258,7 +258,7 @@ def test_batched_session_matches_oracle_per_sequence(fmt, graph):
     m = N.vp()
     L.call("am_model_create_synthetic", rt.rt, C.byref(mc), seed, C.byref(m))
     s = N.vp()
-    L.call("am_session_create", m, C.byref(N.SessionOptions(1, graph, B)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, graph, B)), C.byref(s))
     assert L.am_session_batch(s) == B
     prompts = [O.token_ids(seed, 10 + r, cfg["vocab"], n) for r, n in enumerate((12, 5, 19))]
     orcs = [O.OracleModel(cfg, seed) for _ in range(B)]
@@ -308,7 +308,7 @@ def test_batched_session_needs_every_sequence_prefilled():
     m = N.vp()
     L.call("am_model_create_synthetic", rt.rt, C.byref(mc), 1, C.byref(m))
     s = N.vp()
-    L.call("am_session_create", m, C.byref(N.SessionOptions(1, 1, 2)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, 2)), C.byref(s))
     pr = O.token_ids(1, 0, cfg["vocab"], 4)
     first = N.i64()
     L.call("am_session_prefill_row", s, 0, pr.ctypes.data, pr.size, C.byref(first))

@@ -38,7 +38,7 @@ def test_layer0_node_by_node(act, fmt, S):
     seed = 3
 
     rt = N.vp()
-    L.call("am_runtime_create", 0, C.byref(rt))
+    L.call("am_runtime_open", 0, C.byref(rt))
     mc = N.ModelConfig(1, H, hq, hkv, d, F, cfg["vocab"], 1e-5, 10000.0, dt, fmt, 128, cap, 16)
     m = N.vp()
     L.call("am_model_create_synthetic", rt, C.byref(mc), seed, C.byref(m))

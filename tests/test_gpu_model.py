@@ -25,7 +25,7 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "tiny_fp32_seed0.npz"
 class Runtime:
     def __init__(self):
         self.rt = N.vp()
-        L.call("am_runtime_create", 0, C.byref(self.rt))
+        L.call("am_runtime_open", 0, C.byref(self.rt))
 
     def model(self, cfg: dict, seed: int):
         mc = N.ModelConfig(cfg["num_layers"], cfg["hidden"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"],
@@ -38,7 +38,7 @@ class Runtime:
 
     def session(self, m, fused=1, graph=1):
         s = N.vp()
-        L.call("am_session_create", m, C.byref(N.SessionOptions(fused, graph)), C.byref(s))
+        L.call("am_session_open", m, C.byref(N.SessionOptions(fused, graph)), C.byref(s))
         return s
 
 
@@ -46,7 +46,7 @@ def gpu_generate(rt, m, prompt, n_new, fused=1, graph=1):
     s = rt.session(m, fused, graph)
     toks = np.zeros(n_new, np.int64)
     nout = N.i64()
-    L.call("am_session_generate", s, prompt.ctypes.data, prompt.size, n_new, -1, toks.ctypes.data, C.byref(nout))
+    L.call("am_session_generate_ids", s, prompt.ctypes.data, prompt.size, n_new, -1, toks.ctypes.data, C.byref(nout))
     logits = np.zeros(m_vocab(rt, m), np.float32)
     L.call("am_session_logits", s, logits.ctypes.data)
     L.am_session_destroy(s)

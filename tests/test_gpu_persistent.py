@@ -49,7 +49,7 @@ B8_2L = dict(num_layers=2, hidden=4096, num_q_heads=32, num_kv_heads=8, head_dim
 class Runtime:
     def __init__(self):
         self.rt = N.vp()
-        L.call("am_runtime_create", 0, C.byref(self.rt))
+        L.call("am_runtime_open", 0, C.byref(self.rt))
         self.models = []
 
     def model(self, cfg, seed):
@@ -64,7 +64,7 @@ class Runtime:
     def session(self, m, persistent, graph=1):
         s = N.vp()
         try:
-            L.call("am_session_create", m, C.byref(N.SessionOptions(1, graph, 1, persistent)), C.byref(s))
+            L.call("am_session_open", m, C.byref(N.SessionOptions(1, graph, 1, persistent)), C.byref(s))
         except N.NativeError as e:  # pragma: no cover - other CU counts
             if "256-CU" in str(e):
                 pytest.skip("persistent decode needs a 256-CU device")

@@ -334,16 +334,16 @@ def _model_tensors(L, m, c, torch):
 def _runtime():
     L = N.lib()
     rt = N.vp()
-    L.call("am_runtime_create", 0, C.byref(rt))
+    L.call("am_runtime_open", 0, C.byref(rt))
     return L, rt
 
 
 def _generate(L, m, prompt, n_new):
     s = N.vp()
-    L.call("am_session_create", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
     toks = np.zeros(n_new, np.int64)
     nout = N.i64()
-    L.call("am_session_generate", s, prompt.ctypes.data, prompt.size, n_new, -1, toks.ctypes.data, C.byref(nout))
+    L.call("am_session_generate_ids", s, prompt.ctypes.data, prompt.size, n_new, -1, toks.ctypes.data, C.byref(nout))
     L.am_session_destroy(s)
     return toks
 
@@ -452,3 +452,68 @@ def test_f16_linear_with_mixed_norm_dtypes_loads_exactly(tmp_path):
         assert np.array_equal(got[n], a), n
     L.am_model_destroy(m)
     L.am_runtime_destroy(rt)
+
+
+@pytest.mark.gpu
+def test_prd_session_abi_generates_golden_tokens(tmp_path):
+    """The PRD's Phase-1 C ABI (aethermind_prd.md:298-320): am_runtime_create(config),
+    am_model_load(runtime, path, &error), am_session_create(model, config) and
+    am_session_generate with uint32 token ids, output capacity and an error object.
+    The tiny fp32 checkpoint generates the golden tokens (prefill token + 32 decode
+    steps); the generation limits and the error path behave as specified."""
+    torch = _gpu()
+    import oracle_lib as O
+    L, rt0 = _runtime()
+    c = dict(O.TINY)
+    mc = N.ModelConfig(c["num_layers"], c["hidden"], c["num_q_heads"], c["num_kv_heads"], c["head_dim"], c["ffn"],
+                       c["vocab"], c["rms_eps"], c["rope_theta"], N.AM_DT_F32, N.AM_WF_F32, 128, c["max_tokens"], 16)
+    ms = N.vp()
+    L.call("am_model_create_synthetic", rt0, C.byref(mc), 0, C.byref(ms))
+    tensors = _model_tensors(L, ms, c, torch)
+    L.am_model_destroy(ms)
+    L.am_runtime_destroy(rt0)
+    d = str(tmp_path / "tiny")
+    make_dir(d, c, tensors=tensors, cfg_kw={"rms_norm_eps": c["rms_eps"], "rope_theta": c["rope_theta"]})
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "tiny_fp32_seed0.npz"))
+
+    dll = L.dll
+    cfg = N.Config(C.sizeof(N.Config), 0, N.AM_DT_F32, N.AM_WF_F32, 128, c["max_tokens"], 16)
+    rt = dll.am_runtime_create(C.byref(cfg))
+    assert rt, dll.am_last_error_message()
+    err = N.vp()
+    bad = dll.am_model_load(rt, str(tmp_path / "missing").encode(), C.byref(err))
+    assert not bad and err.value, "a missing directory must fail with an error object"
+    assert dll.am_gfx950_error_code(err) == N.STATUS_NAMES.index("NOT_FOUND")
+    assert b"missing" in dll.am_gfx950_error_message(err)
+    dll.am_error_free(err)
+    m = dll.am_model_load(rt, d.encode(), C.byref(err))
+    assert m and not err.value, dll.am_last_error_message()
+    prompt = np.ascontiguousarray(g["prompt"].astype(np.uint32))
+    out = np.zeros(64, np.uint32)
+    n = C.c_size_t()
+    # no session limit: the output capacity (33) bounds the generation
+    s = dll.am_session_create(m, C.byref(N.SessionConfig(C.sizeof(N.SessionConfig), 0, -1, 1)))
+    assert s, dll.am_last_error_message()
+    rc = dll.am_session_generate(s, prompt.ctypes.data, prompt.size, out.ctypes.data, 33, C.byref(n), C.byref(err))
+    assert rc == 0 and not err.value and n.value == 33
+    assert np.array_equal(out[:33].astype(np.int64), g["tokens"]), (out[:33], g["tokens"])
+    dll.am_session_destroy(s)
+    # the session's max_tokens bounds it, and generation stops after eos
+    eos = int(g["tokens"][4])
+    s = dll.am_session_create(m, C.byref(N.SessionConfig(C.sizeof(N.SessionConfig), 3, -1, 0)))
+    rc = dll.am_session_generate(s, prompt.ctypes.data, prompt.size, out.ctypes.data, 64, C.byref(n), C.byref(err))
+    assert rc == 0 and n.value == 3 and np.array_equal(out[:3].astype(np.int64), g["tokens"][:3])
+    dll.am_session_destroy(s)
+    s = dll.am_session_create(m, C.byref(N.SessionConfig(C.sizeof(N.SessionConfig), 0, eos, 1)))
+    rc = dll.am_session_generate(s, prompt.ctypes.data, prompt.size, out.ctypes.data, 64, C.byref(n), C.byref(err))
+    first = int(np.flatnonzero(g["tokens"] == eos)[0])
+    assert rc == 0 and n.value == first + 1 and int(out[first]) == eos
+    # an out-of-vocabulary id is an error with an error object
+    badp = prompt.copy()
+    badp[3] = c["vocab"]
+    rc = dll.am_session_generate(s, badp.ctypes.data, badp.size, out.ctypes.data, 64, C.byref(n), C.byref(err))
+    assert rc == N.STATUS_NAMES.index("OUT_OF_RANGE") and err.value and n.value == 0
+    dll.am_error_free(err)
+    dll.am_session_destroy(s)
+    dll.am_model_unload(m)
+    dll.am_runtime_destroy(rt)
