@@ -103,6 +103,8 @@ const char* ToString(OpType op) noexcept {
     case OpType::kFusedDecodeLayers: return "FusedDecodeLayers";
     case OpType::kFusedRmsNormLmHeadArgmax: return "FusedRmsNormLmHeadArgmax";
     case OpType::kEmbedToken: return "EmbedToken";
+    case OpType::kFusedLinearSplit: return "FusedLinearSplit";
+    case OpType::kFusedLinearSiluMul: return "FusedLinearSiluMul";
     default: return "Unknown";
   }
 }

@@ -208,6 +208,8 @@ enum class OpType : uint16_t {
   kFusedRmsNormLmHeadArgmax,
   kEmbedToken,
   kFusedDecodeLayers,  // every layer of one decode token in one persistent launch
+  kFusedLinearSplit,   // prefill: one weight whose row ranges are several Linears (q|k|v)
+  kFusedLinearSiluMul, // prefill: Linear gate|up -> SiluMul
 };
 const char* ToString(OpType op) noexcept;
 

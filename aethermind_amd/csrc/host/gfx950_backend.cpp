@@ -248,6 +248,62 @@ Status FusedLinearAddKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_fused_linear_residual(&a, StreamOf(ctx)));
 }
 
+// Prefill Linear -> Add on the MFMA GEMM: in: x; out: h (in/out residual)
+Status PrefillLinearAddKernel(const KernelContext& ctx) noexcept {
+  const GfxParams* p = P(ctx);
+  AM_RETURN_IF_ERROR(NeedArgs(p, 1, 1, "PrefillLinearAdd"));
+  if (W(ctx) == nullptr) return Status::InvalidArgument("PrefillLinearAdd requires packed weights");
+  am_gfx950_linear_args a{};
+  a.x = p->in[0].p;
+  a.x_dtype = p->in[0].dt;
+  a.m = p->in[0].d[0];
+  a.w = *W(ctx);
+  a.out = p->out[0].p;
+  a.out_dtype = p->out[0].dt;
+  a.residual = p->out[0].p;
+  a.mode = 2;
+  if (p->out[0].d[1] != a.w.n || p->in[0].d[1] != a.w.k)
+    return Status::InvalidArgument("PrefillLinearAdd: tensor shapes do not match the packed weight");
+  return FromC(am_gfx950_linear(&a, StreamOf(ctx)));
+}
+
+// Prefill q|k|v: in: x; out: the row ranges of the weight, in order (2 or 3 outputs)
+Status FusedLinearSplitKernel(const KernelContext& ctx) noexcept {
+  const GfxParams* p = P(ctx);
+  if (p->nin < 1 || p->nout < 2 || p->nout > 3) return Status::InvalidArgument("FusedLinearSplit: needs 1 input, 2-3 outputs");
+  if (W(ctx) == nullptr) return Status::InvalidArgument("FusedLinearSplit requires packed weights");
+  am_gfx950_prefill_linear_args a{};
+  a.x = p->in[0].p;
+  a.m = p->in[0].d[0];
+  a.w = *W(ctx);
+  a.epilogue = AM_PREFILL_SPLIT;
+  int64_t col = 0;
+  for (int i = 0; i < p->nout; ++i) {
+    a.out[i] = p->out[i].p;
+    col += p->out[i].d[1];
+    if (i < 2) a.split[i] = col;
+  }
+  if (p->nout == 2) a.split[1] = col;
+  if (col != a.w.n || p->in[0].d[1] != a.w.k) return Status::InvalidArgument("FusedLinearSplit: outputs do not tile the weight rows");
+  return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));
+}
+
+// Prefill gate|up -> SiluMul: in: x; out: act [m][n/2]
+Status FusedLinearSiluMulKernel(const KernelContext& ctx) noexcept {
+  const GfxParams* p = P(ctx);
+  AM_RETURN_IF_ERROR(NeedArgs(p, 1, 1, "FusedLinearSiluMul"));
+  if (W(ctx) == nullptr) return Status::InvalidArgument("FusedLinearSiluMul requires packed weights");
+  am_gfx950_prefill_linear_args a{};
+  a.x = p->in[0].p;
+  a.m = p->in[0].d[0];
+  a.w = *W(ctx);
+  a.epilogue = AM_PREFILL_SILU_MUL;
+  a.out[0] = p->out[0].p;
+  if (2 * p->out[0].d[1] != a.w.n || p->in[0].d[1] != a.w.k)
+    return Status::InvalidArgument("FusedLinearSiluMul: tensor shapes do not match the packed weight");
+  return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));
+}
+
 // in: h, pos, cos, sin, layer table (device am_gfx950_decode_layer[layers]),
 // workspace; out: h (the embedding in, the last layer's output out)
 Status FusedDecodeLayersKernel(const KernelContext& ctx) noexcept {
@@ -472,6 +528,12 @@ AM_FUSED_REGS(f32_int4, kF32, kI4, WF::kQuantizedInt4)
 AM_FUSED_REGS(bf16_bf16, kBF16, kBF16, WF::kPlain)
 AM_FUSED_REGS(bf16_int8, kBF16, kI8, WF::kQuantizedInt8)
 AM_FUSED_REGS(bf16_int4, kBF16, kI4, WF::kQuantizedInt4)
+AM_REGISTER_KERNEL(HipPreLinAddBF16I4, Desc(OpType::kFusedLinearAdd, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
+                                            &PrefillLinearAddKernel, "gfx950::gemm_add_bf16_int4"))
+AM_REGISTER_KERNEL(HipPreSplitBF16I4, Desc(OpType::kFusedLinearSplit, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
+                                           &FusedLinearSplitKernel, "gfx950::gemm_split_bf16_int4"))
+AM_REGISTER_KERNEL(HipPreSiluBF16I4, Desc(OpType::kFusedLinearSiluMul, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
+                                          &FusedLinearSiluMulKernel, "gfx950::gemm_silu_mul_bf16_int4"))
 }  // namespace
 
 }  // namespace aethermind::gfx950

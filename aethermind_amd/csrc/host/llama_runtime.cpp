@@ -630,11 +630,22 @@ class LlamaSession {
     const gfx950::NormAttrs na{c.rms_eps};
     auto& W = s_views[static_cast<size_t>(l)];
     const TensorView hv(h, A, {S, H}), xnv(xn, A, {S, H});
+    // Prefill with INT4 weights on the MFMA GEMM fuses each Linear with its neighbour:
+    // q|k|v as one GEMM over the concatenated weight, o and down with their residual
+    // Add, gate|up with the SiluMul (the same op-boundary roundings).
+    const bool fuse = ph == ExecPhase::kPrefill && c.act_dtype == AM_DT_BF16 && c.weight_format == AM_WF_INT4 &&
+                      c.group_size % 64 == 0 && c.ffn % 64 == 0;
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
                              {hv, TensorView(m->in_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
-    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.q, {xnv}, {MutableTensorView(q, A, {S, Q})}));
-    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.k, {xnv}, {MutableTensorView(k, A, {S, KV})}));
-    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.v, {xnv}, {MutableTensorView(v, A, {S, KV})}));
+    if (fuse) {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSplit, {}, Sel(true, ph), &m->qkv[l], {xnv},
+                               {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV}),
+                                MutableTensorView(v, A, {S, KV})}));
+    } else {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.q, {xnv}, {MutableTensorView(q, A, {S, Q})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.k, {xnv}, {MutableTensorView(k, A, {S, KV})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.v, {xnv}, {MutableTensorView(v, A, {S, KV})}));
+    }
     const gfx950::RopeAttrs ra{c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
     AM_RETURN_IF_ERROR(b.Add(OpType::kRoPE, PackAttrs(ra), Sel(false, ph), nullptr,
                              {TensorView(q, A, {S, Q}), TensorView(k, A, {S, KV}),
@@ -653,12 +664,24 @@ class LlamaSession {
     AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
                              {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},
                              {MutableTensorView(attn, A, {S, Q})}, attn_ws_bytes));
-    AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
-                             {MutableTensorView(tmp, A, {S, H})}));
-    AM_RETURN_IF_ERROR(b.Add(OpType::kAdd, {}, Sel(false, ph), nullptr, {hv, TensorView(tmp, A, {S, H})},
-                             {MutableTensorView(h, A, {S, H})}));
+    if (fuse) {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
+                               {MutableTensorView(h, A, {S, H})}));
+    } else {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
+                               {MutableTensorView(tmp, A, {S, H})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kAdd, {}, Sel(false, ph), nullptr, {hv, TensorView(tmp, A, {S, H})},
+                               {MutableTensorView(h, A, {S, H})}));
+    }
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
                              {hv, TensorView(m->post_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
+    if (fuse) {
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSiluMul, {}, Sel(true, ph), &m->gate_up[l], {xnv},
+                               {MutableTensorView(act, A, {S, F})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {S, F})},
+                               {MutableTensorView(h, A, {S, H})}));
+      return Status::Ok();
+    }
     AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.gate, {xnv}, {MutableTensorView(gate, A, {S, F})}));
     AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.up, {xnv}, {MutableTensorView(up, A, {S, F})}));
     AM_RETURN_IF_ERROR(b.Add(OpType::kSiluMul, {}, Sel(false, ph), nullptr,

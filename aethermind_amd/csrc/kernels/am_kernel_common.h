@@ -37,6 +37,12 @@ am_status_code BatchLinearResidual(const am_gfx950_fused_linear_residual_args* a
 am_status_code BatchGateUp(const am_gfx950_fused_gate_up_args* a, hipStream_t s);
 am_status_code BatchNormLogits(const am_gfx950_fused_lm_head_args* a, hipStream_t s);
 
+// Prefill INT4 GEMM (gemm_i4.hip): epilogue 0 store, 1 residual, 2 column split into
+// out0|out1|out2 at columns c1, c2, 3 SiLU-Mul of the gate|up halves into out0.
+bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x);
+am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
+                      void* out2, int64_t c1, int64_t c2, const void* residual, hipStream_t s);
+
 // ---- device: numeric helpers ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

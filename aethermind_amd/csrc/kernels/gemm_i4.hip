@@ -1,0 +1,391 @@
+// Prefill GEMM for INT4 weights on gfx950: out[M,N] = X[M,K] (bf16) @ W[N,K]^T on
+// bf16 MFMA (v_mfma_f32_16x16x32_bf16), with the prefill plan's fused epilogues.
+//
+//   * Block tile 128 x 128 (M x N), k step 64, 256 threads = 2 x 2 waves of 64 x 64
+//     (4 x 4 MFMA tiles each); two blocks per CU.
+//   * Operands move global -> LDS by DMA (global_load_lds_dwordx4): no registers and no
+//     LDS store instructions, so three k steps are in flight while one is computed (a
+//     step's 20 KB arrive ~1-2 us after issue; one step of MFMAs takes ~0.4 us).  The
+//     ring holds three stages of X (128 rows x 128 B) and W (128 rows x 32 B raw INT4),
+//     plus a four-slot ring of the fp16 group scales.
+//   * DMA writes a wave's 64 lanes to 1 KB of consecutive LDS, so the bank layout is
+//     set by which global chunk each lane fetches: 16-byte chunk c of X row r sits at
+//     slot c ^ ((r >> 1) & 7) of the row, and chunk c of W row n at slot c ^ ((n >> 3)
+//     & 1).  The 16 rows read by one MFMA operand fetch then fall into distinct banks.
+//   * The weight stays INT4 in LDS: a lane's B operand (8 k values) is one 32-bit LDS
+//     read, unpacked in registers right before the MFMA with one shift and one AND-OR
+//     per bf16 pair (nibble q+8 in the low mantissa bits of bf16 128.0 reads 136+q).
+//   * The 136 * sum(x) that 136+q adds is taken out on the MFMA: the A operand times an
+//     all -136 B operand gives -136 * (row sum) in exactly the accumulator layout of the
+//     output tiles.  Each group's sum is scaled by its fp16 scale when the group (two k
+//     steps) completes.  Products are exact and accumulation is fp32.
+//   * Rows past the M or N edge read row 0 and are never stored.
+//   * Epilogues (the op boundaries of the reference graph, model_graph_builder.cpp:
+//     133-290): store; residual (out = round(res + round(acc)), Linear then Add);
+//     column split (one q|k|v weight, three outputs); SiLU-Mul (the block's waves
+//     wn = 0 hold gate columns u, its waves wn = 1 the up columns F + u of the same u;
+//     act = round(silu(round(gate)) * round(up)), exchanged through LDS).
+
+#include "am_gemv_common.h"
+#include "am_launch_timing.h"
+
+namespace am {
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
+
+constexpr int QBM = 128, QBK = 64;
+constexpr int XST = QBM * QBK * 2;  // 16 KB of X per stage
+
+// Block shapes: NWN waves along N (64 columns each) by 2 along M.
+//   NWN = 2: 256 threads, 128 x 128 tile, 3 stages (62 KB of LDS, two blocks per CU)
+//   NWN = 4: 512 threads, 128 x 256 tile, 4 stages (100 KB, one block per CU): half
+//            the X bytes per MFMA, which moves most of the traffic.
+template <int NWN>
+struct Shape {
+  static constexpr int kWaves = 2 * NWN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBN = 64 * NWN;
+  static constexpr int kStages = NWN == 2 ? 3 : 4;
+  static constexpr int kWSt = kBN * QBK / 2;       // W bytes per stage
+  static constexpr int kStg = XST + kWSt;
+  static constexpr int kScSlot = kBN * 4;          // one dword per weight row
+  static constexpr int kLds = kStages * kStg + 4 * kScSlot;
+  static constexpr int kXi = 16 / kWaves;          // X DMA instructions per wave per step
+  static constexpr int kLoads = kXi + 2;           // + W + scales
+};
+
+// X row r's 16-byte chunk c sits at slot c ^ xsw(r) of the row: 8 consecutive rows, and
+// 16 rows taken as two parity classes, land in distinct LDS banks.
+__device__ __forceinline__ int xsw(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+enum I4Epi { kI4Store = 0, kI4Residual = 1, kI4Split = 2, kI4SiluMul = 3 };
+
+struct I4Args {
+  const uint16_t* x;  // bf16 [M][K]
+  const uint8_t* w;   // INT4 device tile order, [N][K/2]
+  const uint16_t* s;  // fp16 scales [N][K/group]
+  int32_t M, N, K, group;
+  int32_t ffn;  // SiLU-Mul: rows [0, ffn) gate, [ffn, 2 ffn) up
+  uint16_t* out0;
+  uint16_t* out1;
+  uint16_t* out2;
+  int32_t c1, c2;             // split: columns [0,c1) -> out0, [c1,c2) -> out1, [c2,N) -> out2
+  const uint16_t* residual;   // [M][N] bf16, may alias out0
+};
+
+__device__ __forceinline__ bf16x8_t unpack8(uint32_t word, uint32_t mask, uint32_t magic) {
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = ((word >> (4 * i)) & mask) | magic;
+  return __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+}
+
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((const gvoid*)(g), (lvoid*)(l), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((const gvoid*)(g), (lvoid*)(l), 4, 0, 0);
+}
+
+// Weight row of local tile row r.
+template <int EPI, int BN>
+__device__ __forceinline__ int32_t wrow(const I4Args& p, int32_t tn, int32_t r) {
+  if constexpr (EPI == kI4SiluMul) return r < BN / 2 ? tn * (BN / 2) + r : p.ffn + tn * (BN / 2) + (r - BN / 2);
+  const int32_t g = tn * BN + r;
+  return g < p.N ? g : 0;
+}
+
+// Wait until at most AHEAD steps of this wave's DMA are in flight, then a plain
+// s_barrier, as one asm statement (no memory access moves across it; a fenced barrier
+// would also wait for the younger steps' DMA).
+template <int LOADS>
+__device__ __forceinline__ void wait_barrier(int ahead) {
+  if (ahead >= 2)
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * LOADS) : "memory");
+  else if (ahead == 1)
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(LOADS) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int EPI, int NWN>
+__global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i4_kernel(I4Args p) {
+  using S = Shape<NWN>;
+  constexpr int BN = S::kBN, NST = S::kStages, STG = S::kStg;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / NWN, wn = wave % NWN;
+
+  // tile mapping: bands of 8 M-tiles, N fastest inside a band
+  const int32_t tiles_m = (p.M + QBM - 1) / QBM;
+  const int32_t tiles_n = EPI == kI4SiluMul ? p.ffn / (BN / 2) : (p.N + BN - 1) / BN;
+  const int32_t bid = blockIdx.x;
+  const int32_t per_band = 8 * tiles_n;
+  const int32_t b0 = bid / per_band, rem = bid - b0 * per_band;
+  const int32_t bands_m = min(tiles_m - b0 * 8, 8);
+  const int32_t tm = b0 * 8 + rem % bands_m, tn = rem / bands_m;
+  const int32_t m0 = tm * QBM;
+
+  const int32_t ng = p.K / p.group;
+  const int32_t nk = p.K / QBK;
+  const int32_t spg = p.group / QBK;  // k steps per group
+
+  // ---- DMA sources of this lane ----
+  // X: wave w moves rows [8 kXi w, 8 kXi (w + 1)), 8 rows per instruction
+  const uint8_t* xsrc[S::kXi];
+#pragma unroll
+  for (int i = 0; i < S::kXi; ++i) {
+    const int r = (wave * S::kXi + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ xsw(r);
+    const int32_t gr = m0 + r < p.M ? m0 + r : 0;
+    xsrc[i] = reinterpret_cast<const uint8_t*>(p.x) + (static_cast<int64_t>(gr) * p.K + 8 * c) * 2;
+  }
+  // W: wave w moves rows 32w .. 32w+31, two 16-byte chunks per row
+  const int wr = wave * 32 + (lane >> 1);
+  const uint8_t* wsrc =
+      p.w + static_cast<int64_t>(wrow<EPI, BN>(p, tn, wr)) * (p.K / 2) + 16 * ((lane & 1) ^ ((wr >> 3) & 1));
+  // scales: lane -> weight row (wave % NWN) * 64 + lane (waves past NWN repeat the
+  // same rows); the dword holding its fp16
+  const int sr = (wave % NWN) * 64 + lane;
+  const int64_t sbase = static_cast<int64_t>(wrow<EPI, BN>(p, tn, sr)) * ng;
+
+  auto issue = [&](int32_t ks) {
+    uint8_t* st = lds + (ks % NST) * STG;
+#pragma unroll
+    for (int i = 0; i < S::kXi; ++i) dma16(xsrc[i] + ks * (QBK * 2), st + (wave * S::kXi + i) * 1024);
+    dma16(wsrc + ks * (QBK / 2), st + XST + wave * 1024);
+    const int32_t g = ks / spg;
+    const int64_t se = sbase + g;  // fp16 element; its dword, aligned down
+    dma4(reinterpret_cast<const uint8_t*>(p.s) + ((se * 2) & ~int64_t{3}),
+         lds + NST * STG + (g & 3) * S::kScSlot + (wave % NWN) * 256);
+  };
+
+  f32x4_t acc[4][4], part[4][4], corr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    corr[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      part[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  uint32_t mask = 0x000F000Fu, magic = 0x43004300u;
+  asm volatile("" : "+v"(mask), "+v"(magic));
+  const bf16x8_t bneg = __builtin_bit_cast(bf16x8_t, make_uint4(0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u));
+
+  // LDS read offsets of this lane (within a stage)
+  int aoff[4][2], boff[4][2];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int r = wm * 64 + mt * 16 + (lane & 15);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) aoff[mt][kk] = r * 128 + 16 * ((kk * 4 + (lane >> 4)) ^ xsw(r));
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int n = wn * 64 + nt * 16 + (lane & 15);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) boff[nt][kk] = XST + n * 32 + 16 * (kk ^ ((n >> 3) & 1)) + 4 * (lane >> 4);
+  }
+  // scale of this lane's column of tile nt in group g: the half of the slot dword that
+  // holds element (row * ng + g)
+  int soff[4], shalf_base[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int n = wn * 64 + nt * 16 + (lane & 15);
+    soff[nt] = NST * STG + n * 4;
+    shalf_base[nt] = static_cast<int>(static_cast<int64_t>(wrow<EPI, BN>(p, tn, n)) * ng & 1);
+  }
+
+  // prologue: steps 0 .. NST-2 in flight
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < nk) issue(i);
+
+  for (int32_t ks = 0; ks < nk; ++ks) {
+    // this wave's DMA for step ks has landed (younger steps may still be in flight);
+    // after the barrier every wave's has, and step ks-1 is no longer read
+    static_assert(NST <= 4, "wait_barrier keeps at most two younger steps in flight");
+    wait_barrier<S::kLoads>(min(nk - 1 - ks, NST - 2));
+    if (ks + NST - 1 < nk) issue(ks + NST - 1);
+    const uint8_t* st = lds + (ks % NST) * STG;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8_t af[4], bfr[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) af[mt] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + aoff[mt][kk]));
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        bfr[nt] = unpack8(*reinterpret_cast<const uint32_t*>(st + boff[nt][kk]), mask, magic);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        corr[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bneg, corr[mt], 0, 0, 0);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          part[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], part[mt][nt], 0, 0, 0);
+      }
+    }
+    if ((ks + 1) % spg == 0) {  // the group closes: scale and fold into acc
+      const int32_t g = ks / spg;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + soff[nt] + (g & 3) * S::kScSlot);
+        const uint32_t bits = ((shalf_base[nt] + g) & 1) ? (sw >> 16) : (sw & 0xFFFFu);
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(sc, part[mt][nt][r] + corr[mt][r], acc[mt][nt][r]);
+          part[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) corr[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue: lane holds D[4*(lane/16)+r][lane%16] of each 16x16 tile ----
+  if constexpr (EPI == kI4SiluMul) {
+    // the up waves (wn >= NWN/2) hand round(up) to the gate waves wn - NWN/2 through LDS
+    constexpr int HN = NWN / 2;
+    float* ex = reinterpret_cast<float*>(lds) + (wm * HN + wn % HN) * 64 * 64;
+    if (wn >= HN) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            ex[(mt * 16 + 4 * (lane >> 4) + r) * 64 + nt * 16 + (lane & 15)] =
+                bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][nt][r]));
+    }
+    __syncthreads();
+    if (wn < HN) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t gm = m0 + wm * 64 + mt * 16 + 4 * (lane >> 4) + r;
+          if (gm >= p.M) continue;
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            const int col = nt * 16 + (lane & 15);
+            const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][nt][r]));
+            const float u = ex[(mt * 16 + 4 * (lane >> 4) + r) * 64 + col];
+            p.out0[static_cast<int64_t>(gm) * p.ffn + tn * (BN / 2) + wn * 64 + col] = f32_to_bf16_bits(silu_ref(g) * u);
+          }
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int32_t gn = tn * BN + wn * 64 + nt * 16 + (lane & 15);
+    if (gn >= p.N) continue;
+    uint16_t* o = p.out0;
+    int32_t col = gn, ld = p.N;
+    if constexpr (EPI == kI4Split) {
+      if (gn < p.c1) {
+        ld = p.c1;
+      } else if (gn < p.c2) {
+        o = p.out1;
+        col = gn - p.c1;
+        ld = p.c2 - p.c1;
+      } else {
+        o = p.out2;
+        col = gn - p.c2;
+        ld = p.N - p.c2;
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t gm = m0 + wm * 64 + mt * 16 + 4 * (lane >> 4) + r;
+        if (gm >= p.M) continue;
+        const int64_t idx = static_cast<int64_t>(gm) * ld + col;
+        float v = acc[mt][nt][r];
+        if constexpr (EPI == kI4Residual) v = bf16_bits_to_f32(p.residual[idx]) + bf16_bits_to_f32(f32_to_bf16_bits(v));
+        o[idx] = f32_to_bf16_bits(v);
+      }
+  }
+}
+
+template <int EPI, int NWN>
+am_status_code LaunchI4(const I4Args& p, hipStream_t s) {
+  using S = Shape<NWN>;
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i4_kernel<EPI, NWN>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds) == hipSuccess;
+  if (!lds_ok) return SetLastError(AM_STATUS_INTERNAL, "gemm_i4: could not set the dynamic LDS size");
+  const int64_t tiles_m = CeilDiv(p.M, QBM);
+  const int64_t tiles_n = EPI == kI4SiluMul ? p.ffn / (S::kBN / 2) : CeilDiv(p.N, S::kBN);
+  const int64_t blocks = tiles_m * tiles_n;
+  static const char* const names[] = {"store", "residual", "split", "silu_mul"};
+  RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_i4<%s,bn=%d>", names[EPI], S::kBN);
+  hipLaunchKernelGGL((gemm_i4_kernel<EPI, NWN>), dim3(static_cast<unsigned>(blocks)), dim3(S::kThreads), S::kLds, s, p);
+  AM_RETURN_IF_LAUNCH_FAILED("gemm_i4");
+  return AM_STATUS_OK;
+}
+
+// Tile width per shape: the 256-wide tile when it still gives every CU a block.
+template <int EPI>
+am_status_code LaunchI4Any(const I4Args& p, hipStream_t s) {
+  const int64_t tiles_m = CeilDiv(p.M, QBM);
+  const int64_t cols = EPI == kI4SiluMul ? 2 * static_cast<int64_t>(p.ffn) : p.N;
+  const bool wide = (EPI != kI4SiluMul || p.ffn % 128 == 0) && tiles_m * CeilDiv(cols, 256) >= DeviceCUs();
+  return wide ? LaunchI4<EPI, 4>(p, s) : LaunchI4<EPI, 2>(p, s);
+}
+
+}  // namespace
+
+// INT4 weights with group % 64 == 0 and K % group == 0, bf16 activations.
+bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x) {
+  return w.format == AM_WF_INT4 && w.scales != nullptr && w.group_size > 0 && w.group_size % QBK == 0 &&
+         w.k % w.group_size == 0 && m > 0 && m * w.k < (int64_t{1} << 31) && w.n * (w.k / 2) < (int64_t{1} << 31) &&
+         m * w.n < (int64_t{1} << 31) && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
+                      void* out2, int64_t c1, int64_t c2, const void* residual, hipStream_t s) {
+  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unsupported shape or weight");
+  I4Args p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.w = static_cast<const uint8_t*>(w.data);
+  p.s = static_cast<const uint16_t*>(w.scales);
+  p.M = static_cast<int32_t>(m);
+  p.N = static_cast<int32_t>(w.n);
+  p.K = static_cast<int32_t>(w.k);
+  p.group = w.group_size;
+  p.out0 = static_cast<uint16_t*>(out0);
+  p.out1 = static_cast<uint16_t*>(out1);
+  p.out2 = static_cast<uint16_t*>(out2);
+  p.c1 = static_cast<int32_t>(c1);
+  p.c2 = static_cast<int32_t>(c2);
+  p.residual = static_cast<const uint16_t*>(residual);
+  switch (epi) {
+    case kI4Store: return LaunchI4Any<kI4Store>(p, s);
+    case kI4Residual:
+      AM_CHECK_ARG(residual != nullptr, "gemm_i4: residual epilogue without a residual");
+      return LaunchI4Any<kI4Residual>(p, s);
+    case kI4Split:
+      AM_CHECK_ARG(0 < c1 && c1 <= c2 && c2 <= w.n && out0 && (c2 == c1 || out1) && (c2 == w.n || out2),
+                   "gemm_i4: bad column split");
+      return LaunchI4Any<kI4Split>(p, s);
+    case kI4SiluMul:
+      AM_CHECK_ARG(w.n % 128 == 0, "gemm_i4: SiLU-Mul needs 2*ffn rows with ffn a multiple of 64");
+      p.ffn = static_cast<int32_t>(w.n / 2);
+      return LaunchI4Any<kI4SiluMul>(p, s);
+    default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unknown epilogue");
+  }
+}
+
+}  // namespace am

@@ -11,6 +11,7 @@ import os
 
 AM_DT_F32, AM_DT_BF16, AM_DT_F16, AM_DT_I8, AM_DT_I4, AM_DT_I32, AM_DT_I64, AM_DT_U32, AM_DT_U8 = range(9)
 AM_WF_F32, AM_WF_BF16, AM_WF_INT8, AM_WF_INT4 = range(4)
+AM_PREFILL_SPLIT, AM_PREFILL_SILU_MUL = 0, 1
 (AM_ROLE_QKV, AM_ROLE_O, AM_ROLE_GATE_UP, AM_ROLE_DOWN, AM_ROLE_LM_HEAD, AM_ROLE_Q, AM_ROLE_K, AM_ROLE_V,
  AM_ROLE_GATE, AM_ROLE_UP) = range(10)
 AM_BUF_EMBED, AM_BUF_IN_NORM, AM_BUF_POST_NORM, AM_BUF_FINAL_NORM, AM_BUF_ROPE_COS, AM_BUF_ROPE_SIN = range(6)
@@ -40,6 +41,10 @@ class RmsNormArgs(C.Structure):
 class LinearArgs(C.Structure):
     _fields_ = [("x", vp), ("x_dtype", i32), ("m", i64), ("w", Weight), ("out", vp), ("out_dtype", i32),
                 ("residual", vp), ("mode", i32)]
+
+
+class PrefillLinearArgs(C.Structure):
+    _fields_ = [("x", vp), ("m", i64), ("w", Weight), ("epilogue", i32), ("out", vp * 3), ("split", i64 * 2)]
 
 
 class RopeArgs(C.Structure):
@@ -166,6 +171,7 @@ _SIGS = {
     "am_gfx950_embed_token": (i32, [vp, vp, i32, i64, i64, vp, vp, vp]),
     "am_gfx950_rmsnorm": (i32, [C.POINTER(RmsNormArgs), vp]),
     "am_gfx950_linear": (i32, [C.POINTER(LinearArgs), vp]),
+    "am_gfx950_prefill_linear": (i32, [C.POINTER(PrefillLinearArgs), vp]),
     "am_gfx950_rope": (i32, [C.POINTER(RopeArgs), vp]),
     "am_gfx950_rope_table": (i32, [i64, i64, f64, vp, vp]),
     "am_gfx950_kv_update": (i32, [C.POINTER(KvUpdateArgs), vp]),

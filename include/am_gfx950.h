@@ -117,6 +117,30 @@ typedef struct am_gfx950_linear_args {
 } am_gfx950_linear_args;
 am_status_code am_gfx950_linear(const am_gfx950_linear_args* args, void* hip_stream);
 
+/* Prefill fusions of Linear with the next reference node, on the MFMA GEMM (m rows of
+ * bf16 activations, INT4 weights with group a multiple of 64; other formats return
+ * AM_STATUS_UNIMPLEMENTED and take am_gfx950_linear per node):
+ *   AM_PREFILL_SPLIT     one weight whose row ranges are several Linears (q|k|v):
+ *                        columns [0, split[0]) -> out[0] [m][split[0]], [split[0],
+ *                        split[1]) -> out[1], [split[1], n) -> out[2]; each rounded
+ *                        to bf16 as its own Linear's output
+ *   AM_PREFILL_SILU_MUL  Linear gate|up (rows [0, n/2) gate, [n/2, n) up) -> SiluMul:
+ *                        out[0] [m][n/2] = round(silu(round(gate)) * round(up))
+ * (model_graph_builder.cpp:133-290 node order; SiluMul formula const_eval_silu_mul.cpp:18-31) */
+typedef enum am_gfx950_prefill_epilogue {
+  AM_PREFILL_SPLIT = 0,
+  AM_PREFILL_SILU_MUL = 1
+} am_gfx950_prefill_epilogue;
+typedef struct am_gfx950_prefill_linear_args {
+  const void* x;
+  int64_t m;
+  am_gfx950_weight w;
+  int32_t epilogue;
+  void* out[3];
+  int64_t split[2];
+} am_gfx950_prefill_linear_args;
+am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* args, void* hip_stream);
+
 /* OpType::kRoPE (rope_op.cpp:202-223; RoPEOp design :588-622): split-half rotation of
  * q [seq][hq*d] and k [seq][hkv*d] at positions pos[seq] (I64, device) using the
  * fp32 tables cos_tab/sin_tab [max_pos][d/2] built by am_gfx950_rope_table.

@@ -1,0 +1,121 @@
+"""The prefill GEMM for INT4 weights (gemm_i4.hip) and its fused epilogues, through
+the C ABI, against the CPU oracle: am_gfx950_linear (store, residual) and
+am_gfx950_prefill_linear (q|k|v column split, gate|up SiLU-Mul) at the 8B prefill
+shapes (512 rows; q|k|v 6144x4096, gate|up 28672x4096, down 4096x14336) and at ragged
+shapes (rows and columns that are not tile multiples, a k of one group, groups of 256).
+
+Bar: bf16 outputs within 2e-2 of the largest reference magnitude per row (north-star
+tolerance); the oracle computes a sample of rows in full, covering every 128-row tile.
+The roundings are the reference op boundaries: each Linear output rounded to bf16,
+the residual sum rounded again, SiLU-Mul from the rounded gate and up."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+import aethermind_amd.native as N  # noqa: E402
+import oracle_lib as O  # noqa: E402
+from gpu_util import bf16_dev, bits_host, empty, p, pack_weight, stream  # noqa: E402
+from test_gpu_decode_shapes import act_rows, bf16_rne_bits, bits_f32, close, launched, rbf  # noqa: E402
+
+L = N.lib()
+TOL = 2e-2
+
+
+def int4_weight(n, k, seed, group=128):
+    rng = np.random.default_rng(seed)
+    bits = bf16_rne_bits(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    w = bits_f32(bits)
+    dw, keep = pack_weight(w, N.AM_WF_INT4, group, src_bf16_bits=bits)
+    pk, sc = O.quant_int4(w, group)
+    return O.dequant_int4(pk, sc, k, group), dw, keep[:2]
+
+
+def sample_rows(m):
+    rows = sorted({0, 1, m - 1, m // 2, min(m - 1, 127), min(m - 1, 128), min(m - 1, 255), min(m - 1, 300)})
+    return [r for r in rows if 0 <= r < m]
+
+
+def rd(t):
+    return O.bf16_to_f32(bits_host(t))
+
+
+@pytest.mark.parametrize("m", [512, 200, 17])
+def test_split_qkv(m):
+    n_q, n_kv, k = 4096, 1024, 4096
+    w, dw, keep = int4_weight(n_q + 2 * n_kv, k, seed=201)
+    x = act_rows(202, m, k)
+    xd = bf16_dev(bf16_rne_bits(x))
+    outs = [empty((m, n), torch.int16) for n in (n_q, n_kv, n_kv)]
+    a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SPLIT, (N.vp * 3)(*[p(o) for o in outs]),
+                            (N.i64 * 2)(n_q, n_q + n_kv))
+    L.call("am_gfx950_prefill_linear", a, stream())
+    assert launched().startswith("gemm_i4<split,"), launched()
+    rows = sample_rows(m)
+    ref = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
+    got = np.concatenate([rd(o) for o in outs], axis=1)
+    for i, r in enumerate(rows):
+        close(got[r], ref[i], TOL, f"q|k|v row {r} (m={m})")
+        for c0, c1 in ((0, n_q), (n_q, n_q + n_kv), (n_q + n_kv, n_q + 2 * n_kv)):
+            close(got[r, c0:c1], ref[i, c0:c1], TOL, f"row {r} cols {c0}:{c1}")
+
+
+@pytest.mark.parametrize("m", [512, 77])
+def test_silu_mul_gate_up(m):
+    F, k = 14336, 4096
+    w, dw, keep = int4_weight(2 * F, k, seed=211)
+    x = act_rows(212, m, k)
+    xd = bf16_dev(bf16_rne_bits(x))
+    out = empty((m, F), torch.int16)
+    a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0))
+    L.call("am_gfx950_prefill_linear", a, stream())
+    assert launched() == ("gemm_i4<silu_mul,bn=256>" if m >= 256 else "gemm_i4<silu_mul,bn=128>"), launched()
+    rows = sample_rows(m)
+    gu = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
+    ref = rbf(O.silu_mul(gu[:, :F], gu[:, F:]))
+    got = rd(out)
+    for i, r in enumerate(rows):
+        close(got[r], ref[i], TOL, f"silu row {r} (m={m})")
+        for seg in range(0, F, 2048):
+            close(got[r, seg:seg + 2048], ref[i, seg:seg + 2048], 3 * TOL, f"row {r} features {seg}+")
+
+
+@pytest.mark.parametrize("shape", [(512, 4096, 14336, 128), (200, 4096, 4096, 128), (130, 260, 512, 256),
+                                   (33, 130, 128, 128), (512, 16384, 512, 64)])
+def test_linear_store_and_residual(shape):
+    m, n, k, group = shape
+    w, dw, keep = int4_weight(n, k, seed=221 + n, group=group)
+    x = act_rows(222, m, k)
+    res = act_rows(223, m, n)
+    xd, rdv = bf16_dev(bf16_rne_bits(x)), bf16_dev(bf16_rne_bits(res))
+    out = empty((m, n), torch.int16)
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2), stream())
+    assert launched().startswith("gemm_i4<store,"), launched()
+    rows = sample_rows(m)
+    ref = O.linear(np.ascontiguousarray(x[rows]), w)
+    got = rd(out)
+    for i, r in enumerate(rows):
+        close(got[r], rbf(ref[i]), TOL, f"store row {r} {shape}")
+    # Linear then Add, in place on the residual (out aliases residual)
+    L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(rdv), N.AM_DT_BF16, p(rdv), 2), stream())
+    assert launched().startswith("gemm_i4<residual,"), launched()
+    got = rd(rdv)
+    for i, r in enumerate(rows):
+        close(got[r], rbf(res[r] + rbf(ref[i])), TOL, f"residual row {r} {shape}")
+
+
+def test_prefill_linear_rejects_other_formats():
+    rng = np.random.default_rng(3)
+    bits = bf16_rne_bits(rng.standard_normal((256, 512), dtype=np.float32))
+    dw, keep = pack_weight(bits_f32(bits), N.AM_WF_BF16, 128, src_bf16_bits=bits)
+    x = bf16_dev(bf16_rne_bits(act_rows(4, 64, 512)))
+    out = empty((64, 128), torch.int16)
+    a = N.PrefillLinearArgs(p(x), 64, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0))
+    with pytest.raises(N.NativeError) as e:
+        L.call("am_gfx950_prefill_linear", a, stream())
+    assert e.value.status == "UNIMPLEMENTED"
