@@ -44,11 +44,15 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(weight_format: int, seconds_budget: float = 20.0):
+def cpu_baseline(weight_format: int, seconds_budget: float = 20.0, pos: int = 512, sequences: int = 1):
     """Oracle restatement of the reference CPU path (AVX2 dot product inner loop,
     dequantize-on-the-fly rows), 1 thread, on a bounded sample of the same decode
     workload: one 8B-shape layer + the full lm_head, timed per decode token at
-    position ~512, then scaled to the 32-layer token (t_token = t_rest + 32 * t_layer)."""
+    position ~pos, then scaled to the 32-layer token (t_token = t_rest + 32 * t_layer).
+    The cache rows before pos are left as the model allocated them (zeros): a decode
+    step's cost does not depend on their values.  With sequences > 1 the reference's
+    CPU path decodes each sequence on its own, so the aggregate rate equals the
+    single-sequence rate (reported as such)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import numpy as np
 
@@ -57,22 +61,23 @@ def cpu_baseline(weight_format: int, seconds_budget: float = 20.0):
     L = O.lib()
     res = {}
     for layers in (1, 2):
-        cfg = dict(SHAPE, num_layers=layers, act="bf16", weight_format=weight_format, group_size=128, max_tokens=600)
+        cfg = dict(SHAPE, num_layers=layers, act="bf16", weight_format=weight_format, group_size=128,
+                   max_tokens=pos + 88)
         L.orc_set_threads(min(16, os.cpu_count() or 1))     # weight generation only (untimed)
         m = O.OracleModel(cfg, 1)
         m.set_fast(True)
         L.orc_set_threads(1)
         prompt = O.token_ids(1, 0, SHAPE["vocab"], 4)
-        m.forward(prompt, 508)                                # fill a few cache rows near position 512
+        m.forward(prompt, pos - 4)                            # fill a few cache rows before pos
         times = []
         t_start = time.perf_counter()
         tok = np.array([int(prompt[-1])], np.int64)
-        pos = 512
+        p = pos
         while len(times) < 3 and time.perf_counter() - t_start < seconds_budget / 2:
             t0 = time.perf_counter()
-            m.forward(tok, pos)
+            m.forward(tok, p)
             times.append(time.perf_counter() - t0)
-            pos += 1
+            p += 1
         res[layers] = min(times)
         m.close()
     t_layer = max(res[2] - res[1], 1e-9)
@@ -92,9 +97,11 @@ def cpu_baseline(weight_format: int, seconds_budget: float = 20.0):
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"oracle AVX2 path, 1 thread on {cpu} (nproc={os.cpu_count()}): decode tokens at pos 512 of "
+        "sample": (f"oracle AVX2 path, 1 thread on {cpu} (nproc={os.cpu_count()}): decode tokens at pos {pos} of "
                    f"1-layer and 2-layer 8B-shape models with the full lm_head; t_layer={t_layer*1e3:.1f} ms, "
-                   f"t_rest={t_rest*1e3:.1f} ms, scaled to 32 layers = {t_token*1e3:.0f} ms/token"),
+                   f"t_rest={t_rest*1e3:.1f} ms, scaled to 32 layers = {t_token*1e3:.0f} ms/token" +
+                   (f"; {sequences} sequences decode one after another, so the aggregate rate is the same"
+                    if sequences > 1 else "")),
     }
 
 
@@ -118,15 +125,34 @@ def calibrate_copy(mib: int) -> None:
     print(json.dumps({"calibrate_copy_bytes": n}), flush=True)
 
 
-def measured_traffic(config: str):
-    """HBM bytes per decode token of the GEMV launches, from the committed rocprofv3 PMC
-    summary of this workload (None when there is none)."""
-    path = os.path.join(ROOT, "profiles", f"gemv_{config}_decode_traffic.json")
+def measured_traffic(name: str):
+    """The committed rocprofv3 PMC summary profiles/<name>.json of this workload, as
+    (summary dict or None, provenance).  Provenance names the commit the counters were
+    taken at and whether the native library's sources have changed since (the summary
+    records their digest), in which case the byte counts describe older code."""
+    path = os.path.join(ROOT, "profiles", f"{name}.json")
     try:
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_token")
+            d = json.load(f)
     except (OSError, ValueError):
+        return None, {"source": None}
+    from aethermind_amd.profiling import source_digest
+    return d, {"source": f"profiles/{name}.json", "commit": d.get("commit"),
+               "stale": d.get("source_digest") != source_digest()}
+
+
+def attention_pmc(summary):
+    """PMC bytes and measured GB/s of the decode attention kernel from a traffic summary"""
+    if not summary:
         return None
+    for name, k in summary.get("per_kernel", {}).items():
+        if name.startswith("attention_decode_kernel"):
+            out = {"kernel": name, "pmc_bytes_per_launch": round(k["fetch_bytes_avg"] + k["write_bytes_avg"])}
+            if "duration_ns_avg" in k:
+                out["trace_us_per_launch"] = round(k["duration_ns_avg"] / 1e3, 2)
+                out["measured_gbs"] = round(k["achieved_gbs"], 1)
+            return out
+    return None
 
 
 def run_long(args, N, L):
@@ -195,6 +221,15 @@ def run_long(args, N, L):
     L.am_model_destroy(m)
     L.am_runtime_destroy(rt)
     step_bytes = weight_bytes + kv_bytes
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(3, pos=P + 64, sequences=B)
+            log(f"cpu baseline: {cpu['value']} tok/s ({cpu['sample']})")
+        except Exception as e:  # the GPU figures stand without it
+            log(f"cpu baseline failed: {e}")
+    pmc, prov = measured_traffic("attention_long_decode_traffic")
+    att = attention_pmc(pmc)
     out = {
         "metric": "batch-4 long-context decode tokens/sec (aggregate), Llama-3-8B-shape INT4, KV 32768",
         "value": round(tok_s, 2),
@@ -215,12 +250,16 @@ def run_long(args, N, L):
                    "prefill_tokens_per_s": round(B * P / prefill_s, 1)},
         "roofline": {"bound": "hbm", "achieved": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": (att["pmc_bytes_per_launch"] * SHAPE["num_layers"]) if att else None,
+                     "traffic_unit": "HBM bytes per step of the decode attention launches (rocprofv3 PMC, "
+                                     "copy-scaled, one launch per layer)",
+                     "traffic_provenance": prov, "attention_pmc": att,
                      "bytes_per_step": int(step_bytes), "attention_ms_per_step": round(attn_ms, 4),
                      "attention_kv_gbs": round(attn_gbs, 1), "gemv_ms_per_step": round(gemv_ms, 4),
                      "gemv_weight_gbs": round(gemv_gbs, 1)},
         "breakdown": breakdown,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
         "host": platform.node(),
     }
     print(json.dumps(out), flush=True)
@@ -337,6 +376,7 @@ def main():
         except Exception as e:  # the GPU figures stand without it
             log(f"cpu baseline failed: {e}")
 
+    pmc, prov = measured_traffic(f"gemv_{args.config}_decode_traffic")
     out = {
         "metric": "batch-1 decode tokens/sec, Llama-3-8B-shape INT4; GEMV HBM GB/s vs peak",
         "value": round(tok_s, 2),
@@ -356,8 +396,10 @@ def main():
                    "model": cfgd["name"], "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
                    "prefill_ms": round(prefill_s * 1e3, 2), "kernels_per_token": plan_size},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": pmc.get("hbm_bytes_per_token") if pmc else None,
                      "traffic_unit": "HBM bytes per token over the GEMV launches (rocprofv3 PMC, copy-scaled)",
+                     "traffic_provenance": prov, "attention_pmc": attention_pmc(pmc),
                      "kernel": "gemv_kernel (weight-only INT4 dequant GEMV, all 4 fused epilogues)",
                      "bytes_per_token": weight_bytes, "gemv_ms_per_token": round(gemv_ms, 4),
                      "launches_per_token": gemv_launches},
