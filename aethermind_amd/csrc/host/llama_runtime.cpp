@@ -943,8 +943,9 @@ class LlamaSession {
   }
 
   // Per-step device time of the decode plan, eager replay of the same steps on the
-  // session stream.  Weight-GEMV steps are timed with events bound to their single
-  // dispatch (hipExtLaunchKernelGGL start/stop), other steps with events around the step.
+  // session stream.  Weight-GEMV and attention steps are timed with events bound to
+  // their single dispatch (hipExtLaunchKernelGGL start/stop), other steps with events
+  // around the step.
   Status Profile(int64_t n, double* ms_by_op, int64_t* count_by_op) {
     AM_RETURN_IF_ERROR(CheckDecode(n));
     const auto& steps = decode_plan->steps();
@@ -957,16 +958,15 @@ class LlamaSession {
     for (int64_t it = 0; it < n && st.ok(); ++it) {
       for (size_t i = 0; i < steps.size() && st.ok(); ++i) {
         const OpType t = steps[i].op->Type();
-        const bool gemv = t == OpType::kFusedRmsNormQkvRoPEKVUpdate || t == OpType::kFusedLinearAdd ||
-                          t == OpType::kFusedDecodeLayers ||
-                          t == OpType::kFusedRmsNormGateUpSiluMul ||
-                          (t == OpType::kFusedRmsNormLmHeadArgmax && B == 1);
-        if (gemv) {
+        const bool timed = t == OpType::kFusedRmsNormQkvRoPEKVUpdate || t == OpType::kFusedLinearAdd ||
+                           t == OpType::kFusedDecodeLayers || t == OpType::kFusedRmsNormGateUpSiluMul ||
+                           (t == OpType::kFusedRmsNormLmHeadArgmax && B == 1) || t == OpType::kAttention;
+        if (timed) {
           lt = {e0[i], e1[i], false};
           st = LayerRunner::RunStep(i, steps[i], decode_bind);
           const bool used = lt.used;
           lt = {};
-          if (st.ok() && !used) st = Status::Internal("profile: GEMV step did not take the timed launch");
+          if (st.ok() && !used) st = Status::Internal("profile: a timed step did not take the timed launch");
         } else {
           (void)hipEventRecord(e0[i], stream);
           st = LayerRunner::RunStep(i, steps[i], decode_bind);
