@@ -81,6 +81,7 @@ class Status {
   static Status OutOfRange(std::string m) { return {StatusCode::kOutOfRange, std::move(m)}; }
   static Status ResourceExhausted(std::string m) { return {StatusCode::kResourceExhausted, std::move(m)}; }
   static Status Internal(std::string m) { return {StatusCode::kInternal, std::move(m)}; }
+  static Status DataLoss(std::string m) { return {StatusCode::kDataLoss, std::move(m)}; }
   static Status Unimplemented(std::string m) { return {StatusCode::kUnimplemented, std::move(m)}; }
   static Status Overflow(std::string m) { return {StatusCode::kOverflow, std::move(m)}; }
   static Status FromC(am_status_code c, const char* m) {

@@ -265,6 +265,7 @@ StDType ParseDType(const std::string& s, uint64_t* elem_bytes) {
   if (s == "F32") return StDType::kF32;
   if (s == "F16") return StDType::kF16;
   if (s == "BF16") return StDType::kBF16;
+  if (s == "I32") return StDType::kI32;
   return StDType::kOther;
 }
 
@@ -388,7 +389,43 @@ StatusOr<int64_t> PosInt(const Json& cfg, const char* key, bool required, int64_
 }
 }  // namespace
 
-StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view text) {
+namespace {
+// quantization_config -> GptqConfig (4-bit GPTQ only)
+Status ParseGptq(const Json& q, GptqConfig* g) {
+  if (q.kind != Json::kObject) return Status::InvalidArgument("config.json: quantization_config must be an object");
+  const Json* m = q.Get("quant_method");
+  if (m == nullptr || m->kind != Json::kString || m->str != "gptq")
+    return Status::Unimplemented("config.json: only quant_method \"gptq\" checkpoints can be ingested");
+  const Json* bits = q.Get("bits");
+  if (bits == nullptr || !bits->is_uint || bits->uint != 4)
+    return Status::Unimplemented("config.json: only 4-bit GPTQ checkpoints can be ingested");
+  const Json* gs = q.Get("group_size");
+  if (gs == nullptr || gs->kind != Json::kNumber) return Status::InvalidArgument("config.json: GPTQ group_size missing");
+  if (gs->number == -1.0) {
+    g->group_size = -1;
+  } else if (gs->is_uint && gs->uint > 0 && gs->uint % 8 == 0 && gs->uint <= static_cast<uint64_t>(INT32_MAX)) {
+    g->group_size = static_cast<int64_t>(gs->uint);
+  } else {
+    return Status::InvalidArgument("config.json: GPTQ group_size must be -1 or a positive multiple of 8");
+  }
+  for (const char* k : {"desc_act", "sym"}) {
+    const Json* b = q.Get(k);
+    if (b == nullptr || b->kind == Json::kNull) continue;
+    if (b->kind != Json::kBool) return Status::InvalidArgument(std::string("config.json: GPTQ ") + k + " must be a bool");
+    (std::string(k) == "desc_act" ? g->desc_act : g->sym) = b->boolean;
+  }
+  g->zero_offset = 1;
+  if (const Json* f = q.Get("checkpoint_format"); f != nullptr && f->kind != Json::kNull) {
+    if (f->kind != Json::kString || (f->str != "gptq" && f->str != "gptq_v2"))
+      return Status::Unimplemented("config.json: GPTQ checkpoint_format must be \"gptq\" or \"gptq_v2\"");
+    g->zero_offset = f->str == "gptq" ? 1 : 0;
+  }
+  g->present = true;
+  return Status::Ok();
+}
+}  // namespace
+
+StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view text, const LoadRules& rules) {
   auto doc = ParseJson(text);
   if (!doc.ok()) return doc.status();
   const Json& c = doc.value();
@@ -471,6 +508,12 @@ StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view text) {
   }
   if (const Json* a = c.Get("hidden_act"); a != nullptr && a->kind == Json::kString && a->str != "silu")
     return Status::InvalidArgument("config.json: hidden_act must be silu");
+  if (const Json* q = c.Get("quantization_config"); q != nullptr && q->kind != Json::kNull) {
+    if (!rules.allow_quantized_tensors)
+      return Status::InvalidArgument(
+          "config.json: quantization_config describes a quantized checkpoint; loading it needs allow_quantized_tensors");
+    AM_RETURN_IF_ERROR(ParseGptq(*q, &m.gptq));
+  }
   return m;
 }
 
@@ -513,7 +556,7 @@ Status ExpectTensor(const std::map<std::string, TensorView>& t, const std::strin
   const auto it = t.find(name);
   if (it == t.end()) return Status::InvalidArgument("checkpoint is missing required weight '" + name + "'");
   const TensorView& v = it->second;
-  if (v.dtype == StDType::kOther)
+  if (v.dtype != StDType::kF32 && v.dtype != StDType::kF16 && v.dtype != StDType::kBF16)
     return Status::InvalidArgument("tensor " + name + ": dtype " + v.dtype_text + " (expected F32, F16 or BF16)");
   if (v.shape != shape) {
     std::string want, got;
@@ -525,11 +568,99 @@ Status ExpectTensor(const std::map<std::string, TensorView>& t, const std::strin
 }
 }  // namespace
 
-StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir) {
+namespace {
+bool EndsWithComponent(const std::string& name, std::string_view comp) {
+  if (name.size() < comp.size() || name.compare(name.size() - comp.size(), comp.size(), comp) != 0) return false;
+  return name.size() == comp.size() || name[name.size() - comp.size() - 1] == '.';
+}
+
+// layer index of "model.layers.<i>.<rest>" (-1 for other names, -2 when malformed)
+int64_t LayerIndexOf(const std::string& name) {
+  static constexpr std::string_view kPre = "model.layers.";
+  if (name.compare(0, kPre.size(), kPre) != 0) return -1;
+  int64_t v = 0;
+  size_t i = kPre.size();
+  if (i >= name.size() || name[i] < '0' || name[i] > '9') return -2;
+  for (; i < name.size() && name[i] >= '0' && name[i] <= '9'; ++i) {
+    v = v * 10 + (name[i] - '0');
+    if (v > INT32_MAX) return -2;
+  }
+  return i < name.size() && name[i] == '.' ? v : -2;
+}
+
+// Tensors no Llama-dense kernel can run, whatever the rules (hf_model_validator.cpp:168-243):
+// mixture-of-experts, bias and LoRA/adapter weights; quantized components unless allowed.
+Status CheckSupported(const std::string& name, const LoadRules& rules) {
+  for (std::string_view p : {"experts", "router", "moe"})
+    if (name.find(p) != std::string::npos) return Status::InvalidArgument("tensor " + name + ": MoE weights are not supported");
+  for (std::string_view p : {".q_proj.bias", ".k_proj.bias", ".v_proj.bias", ".o_proj.bias", ".gate_proj.bias",
+                             ".up_proj.bias", ".down_proj.bias", "lm_head.bias"})
+    if (name.find(p) != std::string::npos) return Status::InvalidArgument("tensor " + name + ": bias weights are not supported");
+  for (std::string_view p : {"lora_A", "lora_B", "adapter", "peft"})
+    if (name.find(p) != std::string::npos)
+      return Status::InvalidArgument("tensor " + name + ": LoRA/adapter weights are not supported");
+  if (!rules.allow_quantized_tensors)
+    for (std::string_view p : {"qweight", "qzeros", "scales", "g_idx", "bits", "group_size"})
+      if (EndsWithComponent(name, p))
+        return Status::InvalidArgument("tensor " + name + ": quantized tensors need allow_quantized_tensors");
+  return Status::Ok();
+}
+
+std::string ShapeText(const std::vector<int64_t>& s) {
+  std::string t = "[";
+  for (size_t i = 0; i < s.size(); ++i) t += (i ? "," : "") + std::to_string(s[i]);
+  return t + "]";
+}
+
+// The GPTQ set of projection prefix [n][k] (all of qweight / qzeros / scales present).
+Status CheckGptq(const std::map<std::string, TensorView>& t, const std::string& prefix, int64_t n, int64_t k,
+                 const GptqConfig& g, GptqLinear* out) {
+  auto find = [&](const char* sfx) -> const TensorView* {
+    const auto it = t.find(prefix + sfx);
+    return it == t.end() ? nullptr : &it->second;
+  };
+  out->qweight = find(".qweight");
+  out->qzeros = find(".qzeros");
+  out->scales = find(".scales");
+  out->g_idx = find(".g_idx");
+  if (!out->qweight || !out->qzeros || !out->scales)
+    return Status::InvalidArgument("checkpoint is missing required weight '" + prefix + ".weight' (or its GPTQ "
+                                   "qweight / qzeros / scales)");
+  const int64_t group = g.group_size == -1 ? k : g.group_size;
+  if (k % 8 != 0 || n % 8 != 0 || k % group != 0)
+    return Status::InvalidArgument(prefix + ": GPTQ needs in/out features divisible by 8 and in_features by group_size");
+  out->n = n;
+  out->k = k;
+  out->group = group;
+  out->groups = k / group;
+  auto expect = [&](const TensorView* v, std::vector<int64_t> shape, bool int32) -> Status {
+    if (int32 ? v->dtype != StDType::kI32 : (v->dtype == StDType::kI32 || v->dtype == StDType::kOther))
+      return Status::InvalidArgument("tensor " + v->name + ": dtype " + v->dtype_text +
+                                     (int32 ? " (expected I32)" : " (expected F16, BF16 or F32)"));
+    if (v->shape != shape)
+      return Status::InvalidArgument("tensor " + v->name + ": shape " + ShapeText(v->shape) + " (expected " +
+                                     ShapeText(shape) + ")");
+    return Status::Ok();
+  };
+  AM_RETURN_IF_ERROR(expect(out->qweight, {k / 8, n}, true));
+  AM_RETURN_IF_ERROR(expect(out->qzeros, {out->groups, n / 8}, true));
+  AM_RETURN_IF_ERROR(expect(out->scales, {out->groups, n}, false));
+  if (out->g_idx) {
+    AM_RETURN_IF_ERROR(expect(out->g_idx, {k}, true));
+    const int32_t* gi = reinterpret_cast<const int32_t*>(out->g_idx->data);
+    for (int64_t i = 0; i < k; ++i)
+      if (gi[i] < 0 || gi[i] >= out->groups)
+        return Status::InvalidArgument("tensor " + out->g_idx->name + ": group index out of range at " + std::to_string(i));
+  }
+  return Status::Ok();
+}
+}  // namespace
+
+StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir, const LoadRules& rules) {
   std::unique_ptr<Checkpoint> ck(new Checkpoint());
   auto cfg_text = ReadFile(dir + "/config.json");
   if (!cfg_text.ok()) return cfg_text.status();
-  auto cfg = ParseLlamaConfig(cfg_text.value());
+  auto cfg = ParseLlamaConfig(cfg_text.value(), rules);
   if (!cfg.ok()) return cfg.status();
   ck->cfg_ = cfg.value();
   const std::string single = dir + "/model.safetensors", index = dir + "/model.safetensors.index.json";
@@ -562,13 +693,34 @@ StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir) {
   }
 
   // names, dtypes and shapes against the config (hf_weight_resolver.cpp:17-110,
-  // hf_model_validator.cpp:168-644); every other tensor is rejected
+  // hf_model_validator.cpp:168-644)
   const LlamaConfig& c = ck->cfg_;
+  for (const auto& [name, v] : ck->tensors_) {
+    AM_RETURN_IF_ERROR(CheckSupported(name, rules));
+    const int64_t li = LayerIndexOf(name);
+    if (li == -2) return Status::InvalidArgument("tensor " + name + ": malformed layer index");
+    if (li >= c.num_layers)
+      return Status::InvalidArgument("tensor " + name + " has layer index " + std::to_string(li) +
+                                     " but num_hidden_layers is " + std::to_string(c.num_layers));
+  }
   const int64_t H = c.hidden, Q = c.num_q_heads * c.head_dim, KV = c.num_kv_heads * c.head_dim;
   std::set<std::string> known;
+  // rotary inv_freq buffers some exporters save: ignored under every rule
+  // (hf_model_validator.cpp:340-355)
+  std::set<std::string> ignorable = {"model.rotary_emb.inv_freq"};
   auto need = [&](const std::string& n, std::vector<int64_t> shape) -> Status {
     known.insert(n);
     return ExpectTensor(ck->tensors_, n, std::move(shape));
+  };
+  // a projection [n][k]: dense .weight, or (quantized checkpoints) its GPTQ set
+  auto proj = [&](const std::string& prefix, int64_t n, int64_t k) -> Status {
+    if (ck->tensors_.count(prefix + ".weight") || !c.gptq.present) return need(prefix + ".weight", {n, k});
+    GptqLinear g;
+    AM_RETURN_IF_ERROR(CheckGptq(ck->tensors_, prefix, n, k, c.gptq, &g));
+    for (const TensorView* v : {g.qweight, g.qzeros, g.scales, g.g_idx})
+      if (v) known.insert(v->name);
+    ck->gptq_[prefix] = g;
+    return Status::Ok();
   };
   AM_RETURN_IF_ERROR(need("model.embed_tokens.weight", {c.vocab, H}));
   AM_RETURN_IF_ERROR(need("model.norm.weight", {H}));
@@ -578,40 +730,56 @@ StatusOr<std::unique_ptr<Checkpoint>> Checkpoint::Open(const std::string& dir) {
     return Status::InvalidArgument("required weight 'lm_head.weight' is missing and tie_word_embeddings is false");
   }
   for (int64_t l = 0; l < c.num_layers; ++l) {
+    ignorable.insert(LayerName(l, ".self_attn.rotary_emb.inv_freq"));
     AM_RETURN_IF_ERROR(need(LayerName(l, ".input_layernorm.weight"), {H}));
     AM_RETURN_IF_ERROR(need(LayerName(l, ".post_attention_layernorm.weight"), {H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.q_proj.weight"), {Q, H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.k_proj.weight"), {KV, H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.v_proj.weight"), {KV, H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".self_attn.o_proj.weight"), {H, Q}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.gate_proj.weight"), {c.ffn, H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.up_proj.weight"), {c.ffn, H}));
-    AM_RETURN_IF_ERROR(need(LayerName(l, ".mlp.down_proj.weight"), {H, c.ffn}));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".self_attn.q_proj"), Q, H));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".self_attn.k_proj"), KV, H));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".self_attn.v_proj"), KV, H));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".self_attn.o_proj"), H, Q));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".mlp.gate_proj"), c.ffn, H));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".mlp.up_proj"), c.ffn, H));
+    AM_RETURN_IF_ERROR(proj(LayerName(l, ".mlp.down_proj"), H, c.ffn));
   }
-  for (const auto& [name, v] : ck->tensors_)
-    if (!known.count(name)) return Status::InvalidArgument("unexpected tensor found: " + name);
-  // The embedding, the head and every projection share one dtype (the reference's
-  // default require_uniform_linear_dtype, hf_model_validator.cpp:433-500); a present
-  // head of a tied model has the embedding's dtype.  Norm gains may differ.
+  // tensors outside the model: ignored by default, errors under strict names or
+  // without allow_unknown_tensors (hf_model_validator.cpp:364-385); they are dropped
+  for (auto it = ck->tensors_.begin(); it != ck->tensors_.end();) {
+    if (known.count(it->first)) {
+      ++it;
+      continue;
+    }
+    if (!ignorable.count(it->first) && (rules.strict_tensor_names || !rules.allow_unknown_tensors))
+      return Status::InvalidArgument("unexpected tensor found: " + it->first);
+    it = ck->tensors_.erase(it);
+  }
+  // The embedding, the head and every dense projection share one dtype (the
+  // reference's default require_uniform_linear_dtype, hf_model_validator.cpp:433-500);
+  // a present head of a tied model has the embedding's dtype.  Norm gains may differ.
   const TensorView& embed = ck->Get("model.embed_tokens.weight");
   if (const TensorView* head = ck->Find("lm_head.weight"); head != nullptr && c.tie_word_embeddings &&
                                                              head->dtype != embed.dtype)
     return Status::InvalidArgument("tied embedding dtype mismatch: lm_head.weight is " + head->dtype_text +
                                    ", model.embed_tokens.weight is " + embed.dtype_text);
   auto same_as_embed = [&](const std::string& n) -> Status {
-    const TensorView& v = ck->Get(n);
-    if (v.dtype != embed.dtype)
-      return Status::InvalidArgument("mixed linear tensor dtype: " + n + " is " + v.dtype_text + ", expected " +
+    const TensorView* v = ck->Find(n);
+    if (v == nullptr) return Status::Ok();  // a GPTQ projection
+    if (v->dtype != embed.dtype)
+      return Status::InvalidArgument("mixed linear tensor dtype: " + n + " is " + v->dtype_text + ", expected " +
                                      embed.dtype_text);
     return Status::Ok();
   };
-  if (ck->Find("lm_head.weight") != nullptr) AM_RETURN_IF_ERROR(same_as_embed("lm_head.weight"));
+  AM_RETURN_IF_ERROR(same_as_embed("lm_head.weight"));
   for (int64_t l = 0; l < c.num_layers; ++l)
     for (const char* sfx : {".self_attn.q_proj.weight", ".self_attn.k_proj.weight", ".self_attn.v_proj.weight",
                             ".self_attn.o_proj.weight", ".mlp.gate_proj.weight", ".mlp.up_proj.weight",
                             ".mlp.down_proj.weight"})
       AM_RETURN_IF_ERROR(same_as_embed(LayerName(l, sfx)));
   return ck;
+}
+
+const GptqLinear* Checkpoint::Gptq(const std::string& prefix) const {
+  const auto it = gptq_.find(prefix);
+  return it == gptq_.end() ? nullptr : &it->second;
 }
 
 const TensorView* Checkpoint::Find(const std::string& name) const {

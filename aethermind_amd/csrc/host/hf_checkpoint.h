@@ -37,7 +37,7 @@ struct Json {
 StatusOr<Json> ParseJson(std::string_view text);
 
 // ---- safetensors ----
-enum class StDType { kF32, kF16, kBF16, kOther };
+enum class StDType { kF32, kF16, kBF16, kI32, kOther };
 struct TensorView {
   std::string name;
   StDType dtype = StDType::kOther;
@@ -67,27 +67,74 @@ class MappedFile {
 };
 
 // ---- model ----
+
+// The reference's ModelValidationOptions (model_validation_options.h:7-16) that this
+// reader honours, with the reference's defaults.  Bias, LoRA/adapter and MoE tensors
+// and RoPE scaling are always rejected (allow_bias / allow_lora_or_adapter /
+// allow_rope_scaling have no kernels behind them here).
+struct LoadRules {
+  bool strict_tensor_names = false;     // any tensor outside the model is an error
+  bool allow_unknown_tensors = true;    // otherwise unknown tensors are ignored
+  bool allow_quantized_tensors = false; // GPTQ checkpoints (see GptqConfig)
+};
+
+// quantization_config of a GPTQ checkpoint (AutoGPTQ / optimum layout, 4 bits), read
+// only under allow_quantized_tensors.  A quantized linear P is stored as
+//   P.qweight  I32 [k/8][n]   nibble t of word (i, j) = q[8i + t][j]       (0..15)
+//   P.qzeros   I32 [g][n/8]   nibble t of word (i, j) = stored zero of column 8j + t
+//   P.scales   F16/BF16/F32 [g][n]
+//   P.g_idx    I32 [k]        group of input feature k (optional: k / group_size)
+// and means w[j][k] = scales[g_idx[k]][j] * (q[k][j] - z), z = (stored + zero_offset) & 15.
+struct GptqConfig {
+  bool present = false;
+  int64_t group_size = 0;    // -1: one group over each linear's in_features
+  bool desc_act = false;
+  bool sym = true;
+  int32_t zero_offset = 1;   // checkpoint_format "gptq" stores z - 1; "gptq_v2" stores z
+};
+
 struct LlamaConfig {
   int64_t num_layers = 0, hidden = 0, num_q_heads = 0, num_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0;
   int64_t max_position_embeddings = 0;
   double rms_eps = 0.0, rope_theta = 10000.0;
   bool tie_word_embeddings = false;
+  GptqConfig gptq;
 };
 // config.json -> LlamaConfig with the reference's Phase-1 rules (model_type llama,
 // positive integer dimensions below 2^31, rms_norm_eps and max_position_embeddings
 // present, no bias, no RoPE scaling, head_dim = hidden / heads, heads divisible by kv
-// heads, intermediate_size >= hidden_size, a dense float dtype hint).
-StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view config_json);
+// heads, intermediate_size >= hidden_size, a dense float dtype hint).  A
+// quantization_config is refused unless rules.allow_quantized_tensors, and then must
+// describe 4-bit GPTQ.
+StatusOr<LlamaConfig> ParseLlamaConfig(std::string_view config_json, const LoadRules& rules = {});
+
+// The tensors of one GPTQ-quantized linear of shape [n][k] (views into the shards).
+struct GptqLinear {
+  const TensorView* qweight = nullptr;
+  const TensorView* qzeros = nullptr;
+  const TensorView* scales = nullptr;
+  const TensorView* g_idx = nullptr;  // may be null
+  int64_t n = 0, k = 0, group = 0, groups = 0;
+};
 
 class Checkpoint {
  public:
   // Reads model_dir/config.json and model.safetensors (or the shards named by
   // model.safetensors.index.json), then checks every tensor name, dtype (F32, F16,
   // BF16) and shape against the config; lm_head.weight may be absent only when
-  // tie_word_embeddings is true; the embedding, head and projections share a dtype.
-  static StatusOr<std::unique_ptr<Checkpoint>> Open(const std::string& model_dir);
+  // tie_word_embeddings is true; the embedding, head and dense projections share a
+  // dtype.  MoE, bias and LoRA/adapter tensors and layer indices past num_layers are
+  // errors; quantized tensors are errors unless rules.allow_quantized_tensors; other
+  // unknown tensors follow strict_tensor_names / allow_unknown_tensors
+  // (hf_model_validator.cpp:168-385).  Under allow_quantized_tensors a projection
+  // without a dense .weight must have a complete GPTQ set.
+  static StatusOr<std::unique_ptr<Checkpoint>> Open(const std::string& model_dir, const LoadRules& rules = {});
 
   const LlamaConfig& config() const { return cfg_; }
+  // The GPTQ tensors of projection `prefix` (e.g. "model.layers.0.self_attn.q_proj"),
+  // or null when it is stored dense (prefix + ".weight").
+  const GptqLinear* Gptq(const std::string& prefix) const;
+  bool has_gptq() const { return !gptq_.empty(); }
   const TensorView* Find(const std::string& name) const;
   const TensorView& Get(const std::string& name) const { return *Find(name); }
   // lm_head.weight, or the embedding when the head is tied
@@ -100,6 +147,7 @@ class Checkpoint {
   LlamaConfig cfg_{};
   std::vector<std::unique_ptr<MappedFile>> files_;
   std::map<std::string, TensorView> tensors_;
+  std::map<std::string, GptqLinear> gptq_;
 };
 
 std::string LayerName(int64_t layer, std::string_view suffix);

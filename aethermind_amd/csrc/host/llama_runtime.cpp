@@ -19,9 +19,13 @@
 //   token history) lives in device memory, and the decode plan is captured once as a
 //   HIP graph and replayed per token without host synchronisation.
 
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <cstddef>
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -32,6 +36,7 @@
 #include "gfx950_backend.h"
 #include "am_launch_timing.h"
 #include "hf_checkpoint.h"
+#include "packed_cache.h"
 
 namespace am {
 am_status_code SetLastError(am_status_code code, const char* msg);
@@ -281,27 +286,45 @@ class LlamaModel {
     const auto& c = cfg;
     const int64_t H = c.hidden, F = c.ffn, V = c.vocab, L = c.num_layers;
     const int32_t act_fmt = c.act_dtype == AM_DT_BF16 ? AM_WF_BF16 : AM_WF_F32;
-    // the staging area holds any one tensor of the checkpoint
-    const uint64_t max_bytes = ck.max_tensor_bytes();
+    auto align = [](uint64_t b) { return (b + 255) & ~uint64_t{255}; };
+    // The staging area holds any one tensor of the checkpoint, or the four tensors of
+    // a GPTQ projection back to back; GPTQ projections also need an unpack area
+    // (fp32 [n][k], or the logical INT4 bytes + fp16 scales).
+    const uint32_t zero_offset = static_cast<uint32_t>(ck.config().gptq.zero_offset);
+    uint64_t max_bytes = ck.max_tensor_bytes(), unpack_bytes = 0;
+    for (int64_t l = 0; l < L && ck.has_gptq(); ++l)
+      for (const char* p : {".self_attn.q_proj", ".self_attn.k_proj", ".self_attn.v_proj", ".self_attn.o_proj",
+                            ".mlp.gate_proj", ".mlp.up_proj", ".mlp.down_proj"})
+        if (const hf::GptqLinear* g = ck.Gptq(hf::LayerName(l, p))) {
+          uint64_t b = 0;
+          for (const hf::TensorView* v : {g->qweight, g->qzeros, g->scales, g->g_idx})
+            if (v) b += align(v->bytes);
+          max_bytes = std::max(max_bytes, b);
+          unpack_bytes = std::max<uint64_t>(unpack_bytes, static_cast<uint64_t>(g->n * g->k) * 4);
+        }
     constexpr size_t kRing = size_t{32} << 20;
     void* dsrc = nullptr;
+    void* dunpack = nullptr;
     void* pinned[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
     bool pending[2] = {false, false};
     Status st = [&]() -> Status {
       AM_HIP_OK(hipMalloc(&dsrc, static_cast<size_t>(max_bytes)));
+      if (unpack_bytes > 0) AM_HIP_OK(hipMalloc(&dunpack, static_cast<size_t>(unpack_bytes)));
       for (int i = 0; i < 2; ++i) {
         AM_HIP_OK(hipHostMalloc(&pinned[i], kRing, hipHostMallocDefault));
         AM_HIP_OK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
       }
       int slot = 0;
-      auto upload = [&](const hf::TensorView& t) -> Status {
-        if (t.bytes > max_bytes) return Status::Internal("tensor " + t.name + " exceeds the device staging area");
+      // tensor -> staging bytes [at, at + t.bytes)
+      auto upload = [&](const hf::TensorView& t, uint64_t at) -> Status {
+        if (at + t.bytes > max_bytes) return Status::Internal("tensor " + t.name + " exceeds the device staging area");
         for (uint64_t off = 0; off < t.bytes;) {
           const size_t n = static_cast<size_t>(std::min<uint64_t>(kRing, t.bytes - off));
           if (pending[slot]) AM_HIP_OK(hipEventSynchronize(ev[slot]));
           std::memcpy(pinned[slot], t.data + off, n);
-          AM_HIP_OK(hipMemcpyAsync(static_cast<char*>(dsrc) + off, pinned[slot], n, hipMemcpyHostToDevice, stream));
+          AM_HIP_OK(hipMemcpyAsync(static_cast<char*>(dsrc) + at + off, pinned[slot], n, hipMemcpyHostToDevice,
+                                   stream));
           AM_HIP_OK(hipEventRecord(ev[slot], stream));
           pending[slot] = true;
           off += n;
@@ -309,13 +332,15 @@ class LlamaModel {
         }
         return Status::Ok();
       };
-      // tensor -> rows [row_off, row_off + rows) of dst (the stream orders the next
-      // upload after the kernel that reads the staging area)
-      auto place = [&](const hf::TensorView& t, int64_t rows, const am_gfx950_weight& dst, int64_t row_off) -> Status {
-        AM_RETURN_IF_ERROR(upload(t));
+      auto src_dtype = [](hf::StDType d) {
+        return d == hf::StDType::kF32 ? AM_DT_F32 : d == hf::StDType::kF16 ? AM_DT_F16 : AM_DT_BF16;
+      };
+      // a float source matrix on the device -> rows [row_off, row_off + rows) of dst
+      auto convert = [&](const void* src, int32_t sdt, int64_t rows, const am_gfx950_weight& dst,
+                         int64_t row_off) -> Status {
         am_gfx950_quantize_args qa{};
-        qa.src = dsrc;
-        qa.src_dtype = t.dtype == hf::StDType::kF32 ? AM_DT_F32 : t.dtype == hf::StDType::kF16 ? AM_DT_F16 : AM_DT_BF16;
+        qa.src = src;
+        qa.src_dtype = sdt;
         qa.src_rows = rows;
         qa.dst = dst;
         qa.dst_row_offset = row_off;
@@ -326,19 +351,78 @@ class LlamaModel {
           AM_C_OK(am_gfx950_pack_plain(&qa, stream));
         return Status::Ok();
       };
+      // tensor -> rows [row_off, row_off + rows) of dst (the stream orders the next
+      // upload after the kernel that reads the staging area)
+      auto place = [&](const hf::TensorView& t, int64_t rows, const am_gfx950_weight& dst, int64_t row_off) -> Status {
+        AM_RETURN_IF_ERROR(upload(t, 0));
+        return convert(dsrc, src_dtype(t.dtype), rows, dst, row_off);
+      };
+      // A GPTQ projection -> rows [row_off, row_off + n) of dst.  When dst is INT4 with
+      // the checkpoint's group size, F16 scales, in-order groups and every zero 8, the
+      // GPTQ grid is this library's (q - 8 with the same fp16 scale), so the nibbles and
+      // scales are repacked as they are.  Otherwise the weight is dequantized exactly to
+      // fp32 (s * (q - z)) and converted like a dense fp32 tensor.
+      auto place_gptq = [&](const hf::GptqLinear& g, const am_gfx950_weight& dst, int64_t row_off) -> Status {
+        uint64_t at[4] = {0, 0, 0, 0}, cur = 0;
+        const hf::TensorView* parts[4] = {g.qweight, g.qzeros, g.scales, g.g_idx};
+        for (int i = 0; i < 4; ++i) {
+          if (!parts[i]) continue;
+          at[i] = cur;
+          AM_RETURN_IF_ERROR(upload(*parts[i], cur));
+          cur += align(parts[i]->bytes);
+        }
+        bool exact = dst.format == AM_WF_INT4 && dst.group_size == g.group && g.scales->dtype == hf::StDType::kF16;
+        if (exact && g.g_idx) {
+          const int32_t* gi = reinterpret_cast<const int32_t*>(g.g_idx->data);
+          for (int64_t i = 0; i < g.k && exact; ++i) exact = gi[i] == i / g.group;
+        }
+        if (exact) {
+          const uint32_t* zw = reinterpret_cast<const uint32_t*>(g.qzeros->data);
+          const int64_t words = g.groups * (g.n / 8);
+          for (int64_t i = 0; i < words && exact; ++i)
+            for (int t = 0; t < 8 && exact; ++t) exact = (((zw[i] >> (4 * t)) + zero_offset) & 15u) == 8u;
+        }
+        char* base = static_cast<char*>(dsrc);
+        am_gfx950_gptq_args a{};
+        a.qweight = reinterpret_cast<const int32_t*>(base + at[0]);
+        a.qzeros = reinterpret_cast<const int32_t*>(base + at[1]);
+        a.scales = base + at[2];
+        a.scales_dtype = src_dtype(g.scales->dtype);
+        a.zero_offset = static_cast<int32_t>(zero_offset);
+        a.g_idx = g.g_idx ? reinterpret_cast<const int32_t*>(base + at[3]) : nullptr;
+        a.n = g.n;
+        a.k = g.k;
+        a.group_size = g.group;
+        if (exact) {
+          a.out_logical = static_cast<uint8_t*>(dunpack);
+          a.out_scales = reinterpret_cast<uint16_t*>(static_cast<char*>(dunpack) + align(g.n * g.k / 2));
+          AM_C_OK(am_gfx950_gptq_unpack(&a, stream));
+          const am_gfx950_pack_int4_args pa{a.out_logical, a.out_scales, RowView(dst, row_off, g.n)};
+          AM_C_OK(am_gfx950_pack_int4(&pa, stream));
+          return Status::Ok();
+        }
+        a.out_f32 = static_cast<float*>(dunpack);
+        AM_C_OK(am_gfx950_gptq_unpack(&a, stream));
+        return convert(dunpack, AM_DT_F32, g.n, dst, row_off);
+      };
+      auto proj = [&](int64_t l, const char* name, int64_t rows, const am_gfx950_weight& dst, int64_t row_off) {
+        const std::string prefix = hf::LayerName(l, name);
+        if (const hf::GptqLinear* g = ck.Gptq(prefix)) return place_gptq(*g, dst, row_off);
+        return place(ck.Get(prefix + ".weight"), rows, dst, row_off);
+      };
       auto act = [&](void* p, int64_t rows) { return am_gfx950_weight{p, nullptr, rows, H, act_fmt, 0}; };
       auto get = [&](int64_t l, const char* sfx) -> const hf::TensorView& { return ck.Get(hf::LayerName(l, sfx)); };
       AM_RETURN_IF_ERROR(place(ck.Get("model.embed_tokens.weight"), V, act(embed, V), 0));
       for (int64_t l = 0; l < L; ++l) {
         AM_RETURN_IF_ERROR(place(get(l, ".input_layernorm.weight"), 1, act(in_norm[l], 1), 0));
         AM_RETURN_IF_ERROR(place(get(l, ".post_attention_layernorm.weight"), 1, act(post_norm[l], 1), 0));
-        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.q_proj.weight"), QRows(), qkv[l], 0));
-        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.k_proj.weight"), KvRows(), qkv[l], QRows()));
-        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.v_proj.weight"), KvRows(), qkv[l], QRows() + KvRows()));
-        AM_RETURN_IF_ERROR(place(get(l, ".self_attn.o_proj.weight"), H, o[l], 0));
-        AM_RETURN_IF_ERROR(place(get(l, ".mlp.gate_proj.weight"), F, gate_up[l], 0));
-        AM_RETURN_IF_ERROR(place(get(l, ".mlp.up_proj.weight"), F, gate_up[l], F));
-        AM_RETURN_IF_ERROR(place(get(l, ".mlp.down_proj.weight"), H, down[l], 0));
+        AM_RETURN_IF_ERROR(proj(l, ".self_attn.q_proj", QRows(), qkv[l], 0));
+        AM_RETURN_IF_ERROR(proj(l, ".self_attn.k_proj", KvRows(), qkv[l], QRows()));
+        AM_RETURN_IF_ERROR(proj(l, ".self_attn.v_proj", KvRows(), qkv[l], QRows() + KvRows()));
+        AM_RETURN_IF_ERROR(proj(l, ".self_attn.o_proj", H, o[l], 0));
+        AM_RETURN_IF_ERROR(proj(l, ".mlp.gate_proj", F, gate_up[l], 0));
+        AM_RETURN_IF_ERROR(proj(l, ".mlp.up_proj", F, gate_up[l], F));
+        AM_RETURN_IF_ERROR(proj(l, ".mlp.down_proj", H, down[l], 0));
       }
       AM_RETURN_IF_ERROR(place(ck.Get("model.norm.weight"), 1, act(final_norm, 1), 0));
       AM_RETURN_IF_ERROR(place(ck.LmHead(), V, lm_head, 0));
@@ -350,6 +434,121 @@ class LlamaModel {
       if (pinned[i]) (void)hipHostFree(pinned[i]);
     }
     if (dsrc) (void)hipFree(dsrc);
+    if (dunpack) (void)hipFree(dunpack);
+    return st;
+  }
+
+  // Slab bytes that hold weights: everything before the RoPE tables (which depend on
+  // max_tokens and are recomputed at load).
+  uint64_t WeightRegionBytes() const {
+    return static_cast<uint64_t>(reinterpret_cast<const char*>(cos_tab) - static_cast<const char*>(slab.base));
+  }
+
+  // Pinned two-buffer ring for the cache file: chunk i of the weight region goes
+  // through buffer i % 2, so the DMA of one buffer overlaps the file I/O of the other.
+  struct Ring {
+    static constexpr size_t kChunk = size_t{32} << 20;
+    void* buf[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    Status Init() {
+      for (int i = 0; i < 2; ++i) {
+        AM_HIP_OK(hipHostMalloc(&buf[i], kChunk, hipHostMallocDefault));
+        AM_HIP_OK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+      }
+      return Status::Ok();
+    }
+    ~Ring() {
+      for (int i = 0; i < 2; ++i) {
+        if (ev[i]) (void)hipEventSynchronize(ev[i]), (void)hipEventDestroy(ev[i]);
+        if (buf[i]) (void)hipHostFree(buf[i]);
+      }
+    }
+  };
+
+  // Writes the weight region to path (through path + ".tmp", renamed when complete).
+  Status SavePackedCache(const std::string& path) {
+    const uint64_t payload = WeightRegionBytes();
+    const std::string tmp = path + ".tmp";
+    const int fd = ::open(tmp.c_str(), O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+    if (fd < 0) return Status::InvalidArgument("packed cache: cannot create " + tmp + ": " + std::strerror(errno));
+    Ring ring;
+    packed::PayloadHasher hasher;
+    Status st = [&]() -> Status {
+      AM_RETURN_IF_ERROR(ring.Init());
+      AM_HIP_OK(hipStreamSynchronize(stream));
+      const uint64_t n_chunks = (payload + Ring::kChunk - 1) / Ring::kChunk;
+      auto issue = [&](uint64_t i) -> Status {
+        const uint64_t off = i * Ring::kChunk, n = std::min<uint64_t>(Ring::kChunk, payload - off);
+        AM_HIP_OK(hipMemcpyAsync(ring.buf[i & 1], static_cast<const char*>(slab.base) + off, n, hipMemcpyDeviceToHost,
+                                 stream));
+        AM_HIP_OK(hipEventRecord(ring.ev[i & 1], stream));
+        return Status::Ok();
+      };
+      AM_RETURN_IF_ERROR(issue(0));
+      for (uint64_t i = 0; i < n_chunks; ++i) {
+        if (i + 1 < n_chunks) AM_RETURN_IF_ERROR(issue(i + 1));
+        AM_HIP_OK(hipEventSynchronize(ring.ev[i & 1]));
+        const uint64_t off = i * Ring::kChunk, n = std::min<uint64_t>(Ring::kChunk, payload - off);
+        hasher.Update(ring.buf[i & 1], n);
+        for (uint64_t done = 0; done < n;) {
+          const ssize_t w = ::pwrite(fd, static_cast<const char*>(ring.buf[i & 1]) + done, n - done,
+                                     static_cast<off_t>(packed::kHeaderBytes + off + done));
+          if (w <= 0) return Status::Internal("packed cache: write failed: " + std::string(std::strerror(errno)));
+          done += static_cast<uint64_t>(w);
+        }
+      }
+      packed::Header h;
+      h.payload_bytes = payload;
+      h.payload_checksum = hasher.Finish();
+      h.cfg = cfg;
+      h.cfg.max_tokens = 0;
+      h.cfg.max_prefill_chunk = 0;
+      uint8_t hb[packed::kHeaderBytes];
+      packed::EncodeHeader(h, hb);
+      if (::pwrite(fd, hb, sizeof(hb), 0) != static_cast<ssize_t>(sizeof(hb)) || ::fsync(fd) != 0)
+        return Status::Internal("packed cache: write failed: " + std::string(std::strerror(errno)));
+      return Status::Ok();
+    }();
+    ::close(fd);
+    if (st.ok() && ::rename(tmp.c_str(), path.c_str()) != 0)
+      st = Status::Internal("packed cache: cannot rename " + tmp + " to " + path + ": " + std::strerror(errno));
+    if (!st.ok()) ::unlink(tmp.c_str());
+    return st;
+  }
+
+  // Allocates the model for cfg (shape and formats from the cache header) and streams
+  // the cache's weight region into the slab, checking the payload checksum.
+  Status LoadPackedCache(const std::string& path, const packed::Header& h) {
+    AM_RETURN_IF_ERROR(Allocate());
+    if (WeightRegionBytes() != h.payload_bytes)
+      return Status::FailedPrecondition("packed cache: payload size does not match this library's weight layout");
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return Status::NotFound("packed cache: cannot open " + path + ": " + std::strerror(errno));
+    Ring ring;
+    packed::PayloadHasher hasher;
+    Status st = [&]() -> Status {
+      AM_RETURN_IF_ERROR(ring.Init());
+      bool pending[2] = {false, false};
+      for (uint64_t off = 0, i = 0; off < h.payload_bytes; off += Ring::kChunk, ++i) {
+        const uint64_t n = std::min<uint64_t>(Ring::kChunk, h.payload_bytes - off);
+        if (pending[i & 1]) AM_HIP_OK(hipEventSynchronize(ring.ev[i & 1]));
+        for (uint64_t done = 0; done < n;) {
+          const ssize_t r = ::pread(fd, static_cast<char*>(ring.buf[i & 1]) + done, n - done,
+                                    static_cast<off_t>(packed::kHeaderBytes + off + done));
+          if (r <= 0) return Status::DataLoss("packed cache: " + path + " ends inside its payload");
+          done += static_cast<uint64_t>(r);
+        }
+        hasher.Update(ring.buf[i & 1], n);
+        AM_HIP_OK(hipMemcpyAsync(static_cast<char*>(slab.base) + off, ring.buf[i & 1], n, hipMemcpyHostToDevice,
+                                 stream));
+        AM_HIP_OK(hipEventRecord(ring.ev[i & 1], stream));
+        pending[i & 1] = true;
+      }
+      AM_HIP_OK(hipStreamSynchronize(stream));
+      if (hasher.Finish() != h.payload_checksum) return Status::DataLoss("packed cache: payload checksum mismatch");
+      return FillRope();
+    }();
+    ::close(fd);
     return st;
   }
 };
@@ -1110,12 +1309,15 @@ am_status_code am_model_create_synthetic(am_runtime* rt, const am_model_config* 
   return AM_STATUS_OK;
 }
 
-am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
-                                am_model** out) {
-  if (!rt || !model_dir || !opt || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_load_hf: null argument");
-  auto ck = aethermind::hf::Checkpoint::Open(model_dir);
-  if (!ck.ok()) return Ret(ck.status());
-  const auto& hc = ck.value()->config();
+namespace {
+aethermind::hf::LoadRules RulesOf(uint32_t flags) {
+  aethermind::hf::LoadRules r;
+  r.strict_tensor_names = (flags & AM_LOAD_STRICT_TENSOR_NAMES) != 0;
+  r.allow_unknown_tensors = (flags & AM_LOAD_REJECT_UNKNOWN_TENSORS) == 0;
+  r.allow_quantized_tensors = (flags & AM_LOAD_ALLOW_QUANTIZED_TENSORS) != 0;
+  return r;
+}
+am_model_config ShapeOf(const aethermind::hf::LlamaConfig& hc) {
   am_model_config mc{};
   mc.num_layers = static_cast<int32_t>(hc.num_layers);
   mc.hidden = static_cast<int32_t>(hc.hidden);
@@ -1126,6 +1328,19 @@ am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_
   mc.vocab = static_cast<int32_t>(hc.vocab);
   mc.rms_eps = static_cast<float>(hc.rms_eps);
   mc.rope_theta = hc.rope_theta;
+  return mc;
+}
+constexpr uint32_t kKnownLoadFlags =
+    AM_LOAD_STRICT_TENSOR_NAMES | AM_LOAD_REJECT_UNKNOWN_TENSORS | AM_LOAD_ALLOW_QUANTIZED_TENSORS;
+}  // namespace
+
+am_status_code am_model_load_hf_ex(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
+                                   uint32_t flags, am_model** out) {
+  if (!rt || !model_dir || !opt || !out) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_load_hf: null argument");
+  if (flags & ~kKnownLoadFlags) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "model_load_hf: unknown load flags");
+  auto ck = aethermind::hf::Checkpoint::Open(model_dir, RulesOf(flags));
+  if (!ck.ok()) return Ret(ck.status());
+  am_model_config mc = ShapeOf(ck.value()->config());
   mc.act_dtype = opt->act_dtype;
   mc.weight_format = opt->weight_format;
   mc.group_size = opt->group_size;
@@ -1142,23 +1357,67 @@ am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_
   return AM_STATUS_OK;
 }
 
-am_status_code am_hf_inspect(const char* model_dir, am_model_config* cfg, int64_t* n_tensors, int64_t* total_bytes) {
+am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
+                                am_model** out) {
+  return am_model_load_hf_ex(rt, model_dir, opt, 0, out);
+}
+
+am_status_code am_hf_inspect_ex(const char* model_dir, uint32_t flags, am_model_config* cfg, int64_t* n_tensors,
+                                int64_t* total_bytes) {
   if (!model_dir || !cfg) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "hf_inspect: null argument");
-  auto ck = aethermind::hf::Checkpoint::Open(model_dir);
+  if (flags & ~kKnownLoadFlags) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "hf_inspect: unknown load flags");
+  auto ck = aethermind::hf::Checkpoint::Open(model_dir, RulesOf(flags));
   if (!ck.ok()) return Ret(ck.status());
-  const auto& hc = ck.value()->config();
-  *cfg = am_model_config{};
-  cfg->num_layers = static_cast<int32_t>(hc.num_layers);
-  cfg->hidden = static_cast<int32_t>(hc.hidden);
-  cfg->num_q_heads = static_cast<int32_t>(hc.num_q_heads);
-  cfg->num_kv_heads = static_cast<int32_t>(hc.num_kv_heads);
-  cfg->head_dim = static_cast<int32_t>(hc.head_dim);
-  cfg->ffn = static_cast<int32_t>(hc.ffn);
-  cfg->vocab = static_cast<int32_t>(hc.vocab);
-  cfg->rms_eps = static_cast<float>(hc.rms_eps);
-  cfg->rope_theta = hc.rope_theta;
+  *cfg = ShapeOf(ck.value()->config());
   if (n_tensors) *n_tensors = static_cast<int64_t>(ck.value()->num_tensors());
   if (total_bytes) *total_bytes = static_cast<int64_t>(ck.value()->total_bytes());
+  return AM_STATUS_OK;
+}
+
+am_status_code am_hf_inspect(const char* model_dir, am_model_config* cfg, int64_t* n_tensors, int64_t* total_bytes) {
+  return am_hf_inspect_ex(model_dir, 0, cfg, n_tensors, total_bytes);
+}
+
+am_status_code am_model_save_packed_cache(am_model* m, const char* path) {
+  if (!m || !path) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "save_packed_cache: null argument");
+  return Ret(m->impl->SavePackedCache(path));
+}
+
+am_status_code am_packed_cache_inspect(const char* path, am_model_config* cfg, int64_t* payload_bytes) {
+  if (!path || !cfg) return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "packed_cache_inspect: null argument");
+  auto h = aethermind::packed::Inspect(path);
+  if (!h.ok()) return Ret(h.status());
+  *cfg = h.value().cfg;
+  if (payload_bytes) *payload_bytes = static_cast<int64_t>(h.value().payload_bytes);
+  return AM_STATUS_OK;
+}
+
+am_status_code am_model_load_packed_cache(am_runtime* rt, const char* path, const am_model_load_options* opt,
+                                          am_model** out) {
+  if (!rt || !path || !opt || !out)
+    return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "load_packed_cache: null argument");
+  auto h = aethermind::packed::Inspect(path);
+  if (!h.ok()) return Ret(h.status());
+  const am_model_config& fc = h.value().cfg;
+  if (opt->act_dtype != fc.act_dtype || opt->weight_format != fc.weight_format ||
+      (fc.weight_format == AM_WF_INT4 && opt->group_size != fc.group_size)) {
+    char msg[200];
+    std::snprintf(msg, sizeof(msg),
+                  "load_packed_cache: the cache holds act_dtype %d / weight_format %d / group %d, the options ask "
+                  "for %d / %d / %d",
+                  fc.act_dtype, fc.weight_format, fc.group_size, opt->act_dtype, opt->weight_format, opt->group_size);
+    return am::SetLastError(AM_STATUS_INVALID_ARGUMENT, msg);
+  }
+  auto m = std::make_unique<am_model>();
+  m->rt = rt;
+  m->impl = std::make_unique<LlamaModel>();
+  m->impl->cfg = fc;
+  m->impl->cfg.max_tokens = opt->max_tokens;
+  m->impl->cfg.max_prefill_chunk = opt->max_prefill_chunk;
+  m->impl->stream = rt->stream;
+  const Status s = m->impl->LoadPackedCache(path, h.value());
+  if (!s.ok()) return Ret(s);
+  *out = m.release();
   return AM_STATUS_OK;
 }
 
@@ -1316,11 +1575,13 @@ am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by
 am_runtime_t am_runtime_create(const am_config_t* config) {
   am_config_t c = DefaultConfig(0);
   if (config != nullptr) {
-    if (config->struct_size < sizeof(am_config_t)) {
+    // the first version of the struct ends before load_flags; later fields keep their
+    // defaults when the caller's struct_size stops before them
+    if (config->struct_size < offsetof(am_config_t, load_flags)) {
       (void)am::SetLastError(AM_STATUS_INVALID_ARGUMENT, "am_config_t: struct_size too small");
       return nullptr;
     }
-    c = *config;
+    std::memcpy(&c, config, std::min<size_t>(config->struct_size, sizeof(am_config_t)));
     c.struct_size = sizeof(am_config_t);
   }
   am_runtime* rt = nullptr;
@@ -1343,7 +1604,7 @@ am_model_t am_model_load(am_runtime_t runtime, const char* path, am_error_t* err
   const am_config_t& c = runtime->config;
   const am_model_load_options opt{c.act_dtype, c.weight_format, c.group_size, c.max_tokens, c.max_prefill_chunk};
   am_model* m = nullptr;
-  const am_status_code rc = am_model_load_hf(runtime, path, &opt, &m);
+  const am_status_code rc = am_model_load_hf_ex(runtime, path, &opt, c.load_flags, &m);
   SetError(error, rc);
   return rc == AM_STATUS_OK ? m : nullptr;
 }

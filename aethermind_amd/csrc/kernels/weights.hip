@@ -275,6 +275,49 @@ __global__ __launch_bounds__(256) void dequant_kernel(const void* data, const vo
   }
 }
 
+// ---------------- GPTQ ingestion ----------------
+// One thread per qweight word (input features 8i .. 8i+7 of output column j); j runs
+// fastest, so the qweight, qzeros and scales reads are coalesced.
+struct GptqKernelArgs {
+  const int32_t* qweight;
+  const int32_t* qzeros;
+  const void* scales;
+  const int32_t* g_idx;
+  int64_t n, k, group, groups;
+  int32_t sdt, zoff;
+  float* out_f32;
+  uint8_t* out_logical;
+};
+
+__global__ __launch_bounds__(256) void gptq_unpack_kernel(GptqKernelArgs a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= (a.k / 8) * a.n) return;
+  const int64_t i = idx / a.n, j = idx % a.n;
+  const uint32_t word = static_cast<uint32_t>(a.qweight[i * a.n + j]);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int64_t kk = 8 * i + t;
+    int64_t g = a.g_idx != nullptr ? a.g_idx[kk] : kk / a.group;
+    g = g < 0 ? 0 : (g >= a.groups ? a.groups - 1 : g);
+    const uint32_t zw = static_cast<uint32_t>(a.qzeros[g * (a.n / 8) + j / 8]);
+    const int z = static_cast<int>(((zw >> (4 * (j & 7))) + static_cast<uint32_t>(a.zoff)) & 0xFu);
+    const int d = static_cast<int>((word >> (4 * t)) & 0xFu) - z;
+    if (a.out_f32 != nullptr)
+      a.out_f32[j * a.k + kk] = load_src(a.scales, a.sdt, g * a.n + j) * static_cast<float>(d);
+    packed |= (static_cast<uint32_t>(d) & 0xFu) << (4 * t);  // k order: low nibble = even k
+  }
+  if (a.out_logical != nullptr) reinterpret_cast<uint32_t*>(a.out_logical + j * (a.k / 2))[i] = packed;
+}
+
+// fp16 scales [groups][n] -> [n][groups]
+__global__ __launch_bounds__(256) void gptq_scales_kernel(const uint16_t* s, int64_t n, int64_t groups, uint16_t* out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n * groups) return;
+  const int64_t g = idx / n, j = idx % n;
+  out[j * groups + g] = s[g * n + j];
+}
+
 }  // namespace
 }  // namespace am
 
@@ -396,6 +439,34 @@ extern "C" am_status_code am_gfx950_pack_int4(const am_gfx950_pack_int4_args* a,
   if (hipMemcpyAsync(const_cast<void*>(a->dst.scales), a->scales, static_cast<size_t>(sb), hipMemcpyDeviceToDevice, s) !=
       hipSuccess)
     return SetLastError(AM_STATUS_INTERNAL, "pack_int4: scale copy failed");
+  return AM_STATUS_OK;
+}
+
+extern "C" am_status_code am_gfx950_gptq_unpack(const am_gfx950_gptq_args* a, void* stream) {
+  AM_CHECK_ARG(a != nullptr && a->qweight && a->qzeros && a->scales, "gptq_unpack: null args");
+  AM_CHECK_ARG(a->n > 0 && a->k > 0 && a->n % 8 == 0 && a->k % 8 == 0 && a->n < (int64_t{1} << 31) &&
+                   a->k < (int64_t{1} << 31),
+               "gptq_unpack: n and k must be positive multiples of 8");
+  AM_CHECK_ARG(a->group_size > 0 && a->k % a->group_size == 0, "gptq_unpack: group_size must divide k");
+  AM_CHECK_ARG(a->scales_dtype == AM_DT_F16 || a->scales_dtype == AM_DT_BF16 || a->scales_dtype == AM_DT_F32,
+               "gptq_unpack: scales must be F16, BF16 or F32");
+  AM_CHECK_ARG(a->zero_offset == 0 || a->zero_offset == 1, "gptq_unpack: zero_offset must be 0 or 1");
+  const bool f32 = a->out_f32 != nullptr, logical = a->out_logical != nullptr;
+  AM_CHECK_ARG(f32 != logical, "gptq_unpack: give exactly one of out_f32 and out_logical");
+  if (logical)
+    AM_CHECK_ARG(a->out_scales != nullptr && a->scales_dtype == AM_DT_F16,
+                 "gptq_unpack: the logical INT4 output needs out_scales and F16 scales");
+  am::GptqKernelArgs g{a->qweight, a->qzeros, a->scales, a->g_idx, a->n, a->k, a->group_size, a->k / a->group_size,
+                       a->scales_dtype, a->zero_offset, a->out_f32, a->out_logical};
+  hipStream_t s = AsStream(stream);
+  const int64_t words = (a->k / 8) * a->n;
+  hipLaunchKernelGGL(am::gptq_unpack_kernel, dim3(static_cast<unsigned>(CeilDiv(words, 256))), dim3(256), 0, s, g);
+  AM_RETURN_IF_LAUNCH_FAILED("gptq_unpack");
+  if (logical) {
+    hipLaunchKernelGGL(am::gptq_scales_kernel, dim3(static_cast<unsigned>(CeilDiv(a->n * g.groups, 256))), dim3(256), 0,
+                       s, static_cast<const uint16_t*>(a->scales), a->n, g.groups, a->out_scales);
+    AM_RETURN_IF_LAUNCH_FAILED("gptq_unpack");
+  }
   return AM_STATUS_OK;
 }
 

@@ -12,6 +12,7 @@ import os
 AM_DT_F32, AM_DT_BF16, AM_DT_F16, AM_DT_I8, AM_DT_I4, AM_DT_I32, AM_DT_I64, AM_DT_U32, AM_DT_U8 = range(9)
 AM_WF_F32, AM_WF_BF16, AM_WF_INT8, AM_WF_INT4 = range(4)
 AM_PREFILL_SPLIT, AM_PREFILL_SILU_MUL = 0, 1
+AM_LOAD_STRICT_TENSOR_NAMES, AM_LOAD_REJECT_UNKNOWN_TENSORS, AM_LOAD_ALLOW_QUANTIZED_TENSORS = 1, 2, 4
 (AM_ROLE_QKV, AM_ROLE_O, AM_ROLE_GATE_UP, AM_ROLE_DOWN, AM_ROLE_LM_HEAD, AM_ROLE_Q, AM_ROLE_K, AM_ROLE_V,
  AM_ROLE_GATE, AM_ROLE_UP) = range(10)
 AM_BUF_EMBED, AM_BUF_IN_NORM, AM_BUF_POST_NORM, AM_BUF_FINAL_NORM, AM_BUF_ROPE_COS, AM_BUF_ROPE_SIN = range(6)
@@ -20,6 +21,11 @@ STATUS_NAMES = ["OK", "CANCELLED", "UNKNOWN", "INVALID_ARGUMENT", "DEADLINE_EXCE
                 "ALREADY_EXISTS", "PERMISSION_DENIED", "RESOURCE_EXHAUSTED", "FAILED_PRECONDITION", "ABORTED",
                 "OUT_OF_RANGE", "UNIMPLEMENTED", "INTERNAL", "UNAVAILABLE", "DATA_LOSS", "OVERFLOW",
                 "UNAUTHENTICATED"]
+
+(AM_STATUS_OK, AM_STATUS_CANCELLED, AM_STATUS_UNKNOWN, AM_STATUS_INVALID_ARGUMENT, AM_STATUS_DEADLINE_EXCEEDED,
+ AM_STATUS_NOT_FOUND, AM_STATUS_ALREADY_EXISTS, AM_STATUS_PERMISSION_DENIED, AM_STATUS_RESOURCE_EXHAUSTED,
+ AM_STATUS_FAILED_PRECONDITION, AM_STATUS_ABORTED, AM_STATUS_OUT_OF_RANGE, AM_STATUS_UNIMPLEMENTED, AM_STATUS_INTERNAL,
+ AM_STATUS_UNAVAILABLE, AM_STATUS_DATA_LOSS, AM_STATUS_OVERFLOW, AM_STATUS_UNAUTHENTICATED) = range(len(STATUS_NAMES))
 
 vp, i32, i64, u64, f32, f64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
 
@@ -87,6 +93,12 @@ class PackInt4Args(C.Structure):
     _fields_ = [("logical", vp), ("scales", vp), ("dst", Weight)]
 
 
+class GptqArgs(C.Structure):
+    _fields_ = [("qweight", vp), ("qzeros", vp), ("scales", vp), ("scales_dtype", i32), ("zero_offset", i32),
+                ("g_idx", vp), ("n", i64), ("k", i64), ("group_size", i64), ("out_f32", vp), ("out_logical", vp),
+                ("out_scales", vp)]
+
+
 class DequantArgs(C.Structure):
     _fields_ = [("w", Weight), ("out", vp)]
 
@@ -146,7 +158,7 @@ class ModelLoadOptions(C.Structure):
 
 class Config(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("device", i32), ("act_dtype", i32), ("weight_format", i32),
-                ("group_size", i32), ("max_tokens", i32), ("max_prefill_chunk", i32)]
+                ("group_size", i32), ("max_tokens", i32), ("max_prefill_chunk", i32), ("load_flags", C.c_uint32)]
 
 
 class SessionConfig(C.Structure):
@@ -187,6 +199,7 @@ _SIGS = {
     "am_gfx950_pack_plain": (i32, [C.POINTER(QuantizeArgs), vp]),
     "am_gfx950_pack_int4": (i32, [C.POINTER(PackInt4Args), vp]),
     "am_gfx950_dequant": (i32, [C.POINTER(DequantArgs), vp]),
+    "am_gfx950_gptq_unpack": (i32, [C.POINTER(GptqArgs), vp]),
     "am_gfx950_weight_bytes": (i32, [i64, i64, i32, i32, C.POINTER(i64), C.POINTER(i64)]),
     "am_gfx950_synth_normal": (i32, [C.POINTER(SynthArgs), vp]),
     "am_gfx950_synth_token_ids": (i32, [u64, u64, i64, i64, vp, vp]),
@@ -212,6 +225,11 @@ _SIGS = {
     "am_model_weight": (i32, [vp, i32, i32, C.POINTER(Weight)]),
     "am_model_load_hf": (i32, [vp, C.c_char_p, C.POINTER(ModelLoadOptions), C.POINTER(vp)]),
     "am_hf_inspect": (i32, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(i64), C.POINTER(i64)]),
+    "am_model_load_hf_ex": (i32, [vp, C.c_char_p, C.POINTER(ModelLoadOptions), C.c_uint32, C.POINTER(vp)]),
+    "am_hf_inspect_ex": (i32, [C.c_char_p, C.c_uint32, C.POINTER(ModelConfig), C.POINTER(i64), C.POINTER(i64)]),
+    "am_model_save_packed_cache": (i32, [vp, C.c_char_p]),
+    "am_packed_cache_inspect": (i32, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(i64)]),
+    "am_model_load_packed_cache": (i32, [vp, C.c_char_p, C.POINTER(ModelLoadOptions), C.POINTER(vp)]),
     "am_model_buffer": (i32, [vp, i32, i32, C.POINTER(vp), C.POINTER(i64)]),
     "am_model_weight_bytes_total": (i64, [vp]),
     "am_session_open": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
@@ -265,6 +283,11 @@ class Lib:
 
     def __getattr__(self, name):
         return getattr(self.dll, name)
+
+    def last_error(self) -> str:
+        """this thread's last error text (am_last_error_message)"""
+        msg = self.dll.am_last_error_message()
+        return msg.decode() if msg else ""
 
     def call(self, name: str, *args) -> None:
         rc = getattr(self.dll, name)(*args)

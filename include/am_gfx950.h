@@ -290,6 +290,37 @@ typedef struct am_gfx950_pack_int4_args {
 } am_gfx950_pack_int4_args;
 am_status_code am_gfx950_pack_int4(const am_gfx950_pack_int4_args* args, void* hip_stream);
 
+/* GPTQ (4-bit, AutoGPTQ / optimum layout) -> this library's weight inputs.  No
+ * counterpart kernel in the reference, whose validator only admits such tensors under
+ * allow_quantized_tensors (hf_model_validator.cpp:196-243, model_validation_options.h:12).
+ *   qweight [k/8][n] I32: nibble t of word (i, j) = q[8i + t][j] in 0..15
+ *   qzeros  [groups][n/8] I32: nibble t of word (g, j) = stored zero of column 8j + t;
+ *           z = (stored + zero_offset) & 15 (zero_offset 1 for checkpoint_format "gptq",
+ *           which stores z - 1; 0 for "gptq_v2")
+ *   scales  [groups][n], scales_dtype AM_DT_F16, AM_DT_BF16 or AM_DT_F32
+ *   g_idx   [k] group of input feature k (NULL: k / group_size); out-of-range entries
+ *           are clamped to the last group (the loader rejects them beforehand)
+ * Exactly one output:
+ *   out_f32     [n][k]: w[j][kk] = s * (q - z), one fp32 multiply of exact operands
+ *               (exact: |q - z| <= 15 and s has at most 24 significant bits);
+ *   out_logical [n][k/2] + out_scales [n][groups] fp16: the logical INT4 interchange of
+ *               am_gfx950_pack_int4 (q - z as a two's complement nibble, low nibble =
+ *               even k).  Meaningful only when every z is 8, g_idx is trivial and the
+ *               scales are F16; then it is exact (same q - z and the same fp16 scale). */
+typedef struct am_gfx950_gptq_args {
+  const int32_t* qweight;
+  const int32_t* qzeros;
+  const void* scales;
+  int32_t scales_dtype;
+  int32_t zero_offset;
+  const int32_t* g_idx;
+  int64_t n, k, group_size;
+  float* out_f32;
+  uint8_t* out_logical;
+  uint16_t* out_scales;
+} am_gfx950_gptq_args;
+am_status_code am_gfx950_gptq_unpack(const am_gfx950_gptq_args* args, void* hip_stream);
+
 /* Dequantizes a device weight to fp32 [n][k] in logical k order:
  * w = float(q) * float(scale), one fp32 multiply (bit-exact SPEC). */
 typedef struct am_gfx950_dequant_args {

@@ -89,8 +89,9 @@ void am_model_destroy(am_model* m);
  * device).  The reference's HF reader / validator / weight resolver contract
  * (hf_directory_reader.cpp:333-412, hf_model_validator.cpp:168-644,
  * hf_weight_resolver.cpp:17-110): model_type llama, no bias, no RoPE scaling, every
- * layer tensor present with its exact shape, no unknown tensors, lm_head.weight absent
- * only with tie_word_embeddings (the embedding is then the head). */
+ * layer tensor present with its exact shape, lm_head.weight absent only with
+ * tie_word_embeddings (the embedding is then the head); the validation rules are those
+ * of flags 0 in am_model_load_hf_ex (below). */
 typedef struct am_model_load_options {
   int32_t act_dtype;         /* AM_DT_F32 or AM_DT_BF16 */
   int32_t weight_format;     /* am_weight_format */
@@ -103,6 +104,46 @@ am_status_code am_model_load_hf(am_runtime* rt, const char* model_dir, const am_
 /* Host only (no device work): reads and validates the checkpoint directory and fills
  * the shape fields of cfg (num_layers .. rope_theta), the tensor count and bytes. */
 am_status_code am_hf_inspect(const char* model_dir, am_model_config* cfg, int64_t* n_tensors, int64_t* total_bytes);
+
+/* Checkpoint validation rules: the reference's ModelValidationOptions
+ * (model_validation_options.h:7-16).  0 = the reference's defaults, which
+ * am_model_load_hf / am_hf_inspect use: tensors outside the model are ignored,
+ * quantized tensors are refused (hf_model_validator.cpp:196-243, 364-385).  MoE, bias
+ * and LoRA/adapter tensors and RoPE scaling are refused under every flag. */
+typedef enum am_load_flags {
+  AM_LOAD_STRICT_TENSOR_NAMES = 1,    /* strict_tensor_names: any tensor outside the model is an error */
+  AM_LOAD_REJECT_UNKNOWN_TENSORS = 2, /* allow_unknown_tensors = false */
+  AM_LOAD_ALLOW_QUANTIZED_TENSORS = 4 /* allow_quantized_tensors: a config.json quantization_config of
+                                         4-bit GPTQ (checkpoint_format "gptq" or "gptq_v2") is accepted
+                                         and each projection may be stored as its GPTQ set
+                                         (qweight / qzeros / scales / optional g_idx) instead of .weight.
+                                         INT4 targets with the same group size, F16 scales, in-order
+                                         groups and all zeros 8 are repacked exactly; every other case is
+                                         dequantized exactly (s * (q - z) in fp32) and converted to the
+                                         requested format (see am_gfx950_gptq_unpack). */
+} am_load_flags;
+am_status_code am_model_load_hf_ex(am_runtime* rt, const char* model_dir, const am_model_load_options* opt,
+                                   uint32_t flags, am_model** out);
+am_status_code am_hf_inspect_ex(const char* model_dir, uint32_t flags, am_model_config* cfg, int64_t* n_tensors,
+                                int64_t* total_bytes);
+/* On-disk packed-weight cache: SavePackedCache / LoadPackedCache of the reference's
+ * weight-packing design (model_weight_packing_strategy.md:390-394; design-only there).
+ * The file is the model's repacked device weights exactly as they sit in HBM (embedding,
+ * norms, q|k|v, o, gate|up, down, lm_head in the model's activation dtype and weight
+ * format) behind a 256-byte header naming the shape, formats, device architecture and
+ * layout version, with checksums of header and payload.  Loading reads it sequentially
+ * through a pinned ring straight into HBM: no conversion, no quantization.
+ *   save:    writes path + ".tmp" and renames it when complete.
+ *   inspect: host only; checks the header and that the file holds the whole payload
+ *            (NOT_FOUND, INVALID_ARGUMENT bad magic, FAILED_PRECONDITION other version /
+ *            architecture / layout, DATA_LOSS checksum or size mismatch).
+ *   load:    opt->act_dtype / weight_format (/ group_size for INT4) must equal the
+ *            cache's (INVALID_ARGUMENT otherwise); max_tokens and max_prefill_chunk come
+ *            from opt; a payload checksum mismatch is DATA_LOSS. */
+am_status_code am_model_save_packed_cache(am_model* m, const char* path);
+am_status_code am_packed_cache_inspect(const char* path, am_model_config* cfg, int64_t* payload_bytes);
+am_status_code am_model_load_packed_cache(am_runtime* rt, const char* path, const am_model_load_options* opt,
+                                          am_model** out);
 am_status_code am_model_weight(am_model* m, int32_t layer, int32_t role, am_gfx950_weight* out);
 am_status_code am_model_buffer(am_model* m, int32_t kind, int32_t layer, void** ptr, int64_t* bytes);
 int64_t am_model_weight_bytes_total(am_model* m); /* repacked linear weights incl. scales */
@@ -178,6 +219,8 @@ typedef struct am_config {
   int32_t group_size;        /* INT4 group along k (128) */
   int32_t max_tokens;        /* static KV capacity per sequence (positions) */
   int32_t max_prefill_chunk; /* rows per prefill pass */
+  /* grown at the end (a struct_size that stops before a field leaves its default) */
+  uint32_t load_flags;       /* am_load_flags for am_model_load (default 0) */
 } am_config_t;
 
 typedef struct am_session_config {

@@ -5,12 +5,16 @@
 //   KV layout / manager   tests/unit/execution/test_kv_cache_manager.cpp:13-123
 //   executor order/errors tests/unit/execution/test_executor_backend_path.cpp:266-368
 // Exit code 0 = all checks passed; every failure is printed with its line.
+#include <unistd.h>
+
 #include <cstdio>
+#include <cstring>
 #include <string>
 #include <vector>
 
 #include "am_core.h"
 #include "gfx950_backend.h"
+#include "packed_cache.h"
 
 using namespace aethermind;
 
@@ -403,7 +407,87 @@ void TestGfx950Registrations() {
 
 }  // namespace
 
+// Packed weight cache header (host/packed_cache.h): round trip, and every corruption
+// or foreign file that must be refused before any device memory is touched.
+void TestPackedCacheHeader() {
+  namespace P = aethermind::packed;
+  P::Header h;
+  h.payload_bytes = 4096;
+  h.payload_checksum = 0x1234;
+  h.cfg = am_model_config{2, 64, 4, 2, 16, 128, 100, 1e-5f, 500000.0, AM_DT_BF16, AM_WF_INT4, 32, 0, 0};
+  uint8_t buf[P::kHeaderBytes];
+  P::EncodeHeader(h, buf);
+  {
+    auto d = P::DecodeHeader(buf, sizeof(buf));
+    CHECK(d.ok());
+    if (d.ok()) {
+      const auto& c = d.value().cfg;
+      CHECK(d.value().payload_bytes == 4096 && d.value().payload_checksum == 0x1234);
+      CHECK(c.num_layers == 2 && c.hidden == 64 && c.num_q_heads == 4 && c.num_kv_heads == 2 && c.head_dim == 16 &&
+            c.ffn == 128 && c.vocab == 100 && c.rms_eps == 1e-5f && c.rope_theta == 500000.0 &&
+            c.act_dtype == AM_DT_BF16 && c.weight_format == AM_WF_INT4 && c.group_size == 32);
+    }
+  }
+  // every single-bit flip of the header is refused
+  int refused = 0;
+  for (size_t byte = 0; byte < P::kHeaderBytes; ++byte) {
+    uint8_t b2[P::kHeaderBytes];
+    std::memcpy(b2, buf, sizeof(b2));
+    b2[byte] ^= 0x10;
+    refused += P::DecodeHeader(b2, sizeof(b2)).ok() ? 0 : 1;
+  }
+  CHECK(refused == static_cast<int>(P::kHeaderBytes));
+  CHECK(P::DecodeHeader(buf, 100).status().code() == StatusCode::kDataLoss);
+  {
+    uint8_t b2[P::kHeaderBytes];
+    std::memcpy(b2, buf, sizeof(b2));
+    b2[0] = 'X';
+    CHECK(P::DecodeHeader(b2, sizeof(b2)).status().code() == StatusCode::kInvalidArgument);
+  }
+  auto with_cfg = [&](auto edit) {
+    P::Header h2 = h;
+    edit(h2);
+    uint8_t b2[P::kHeaderBytes];
+    P::EncodeHeader(h2, b2);
+    return P::DecodeHeader(b2, sizeof(b2)).status();
+  };
+  CHECK(with_cfg([](P::Header& x) { x.cfg.num_kv_heads = 3; }).code() == StatusCode::kInvalidArgument);
+  CHECK(with_cfg([](P::Header& x) { x.cfg.hidden = 0; }).code() == StatusCode::kInvalidArgument);
+  CHECK(with_cfg([](P::Header& x) { x.cfg.weight_format = 9; }).code() == StatusCode::kInvalidArgument);
+  CHECK(with_cfg([](P::Header& x) { x.cfg.act_dtype = AM_DT_F16; }).code() == StatusCode::kInvalidArgument);
+  CHECK(with_cfg([](P::Header& x) { x.cfg.group_size = 0; }).code() == StatusCode::kInvalidArgument);
+  CHECK(with_cfg([](P::Header& x) { x.payload_bytes = 1000; }).code() == StatusCode::kDataLoss);
+  // the checksum: order- and content-sensitive, and streaming equals one shot
+  std::vector<uint8_t> data(1 << 12);
+  for (size_t i = 0; i < data.size(); ++i) data[i] = static_cast<uint8_t>(i * 131 + 7);
+  const uint64_t c0 = P::Checksum(data.data(), data.size());
+  P::PayloadHasher st;
+  st.Update(data.data(), 1024);
+  st.Update(data.data() + 1024, data.size() - 1024);
+  CHECK(st.Finish() == c0);
+  std::swap(data[100], data[3000]);
+  CHECK(P::Checksum(data.data(), data.size()) != c0);
+  // Inspect: whole file, truncated, padded, missing
+  const std::string path = "/tmp/am_test_packed_" + std::to_string(::getpid()) + ".bin";
+  auto write = [&](size_t payload) {
+    FILE* f = std::fopen(path.c_str(), "wb");
+    std::fwrite(buf, 1, sizeof(buf), f);
+    std::vector<uint8_t> z(payload, 0);
+    std::fwrite(z.data(), 1, z.size(), f);
+    std::fclose(f);
+  };
+  write(4096);
+  CHECK(P::Inspect(path).ok());
+  write(4000);
+  CHECK(P::Inspect(path).status().code() == StatusCode::kDataLoss);
+  write(4096 + 256);
+  CHECK(P::Inspect(path).status().code() == StatusCode::kDataLoss);
+  std::remove(path.c_str());
+  CHECK(P::Inspect(path).status().code() == StatusCode::kNotFound);
+}
+
 int main() {
+  TestPackedCacheHeader();
   TestRegistry();
   TestKV();
   TestExecutor();
