@@ -485,4 +485,92 @@ Status KVCacheManager::ReleaseSession(KVCacheView& view) noexcept {
   return Status::Ok();
 }
 
+// ------------------------------------------------------------------ KVBlockManager
+KVBlockManager::~KVBlockManager() { Release(); }
+
+void KVBlockManager::Release() noexcept {
+  if (pools_ != nullptr) alloc_.free(pools_, alloc_.user);
+  if (table_dev_ != nullptr) alloc_.free(table_dev_, alloc_.user);
+  pools_ = nullptr;
+  table_dev_ = nullptr;
+  pool_bytes_ = layer_bytes_ = 0;
+  free_.clear();
+  table_.clear();
+  held_.clear();
+  dirty_ = false;
+}
+
+Status KVBlockManager::Init(size_t num_layers, size_t num_kv_heads, size_t head_dim, DataType kv_dtype,
+                            size_t block_size, size_t num_blocks, size_t max_seqs, size_t max_tokens) {
+  Release();
+  if (block_size < 32 || (block_size & (block_size - 1)) != 0)
+    return Status::InvalidArgument("KV blocks: block_size must be a power of two of at least 32");
+  if (num_layers == 0 || num_kv_heads == 0 || head_dim == 0 || num_blocks == 0 || max_seqs == 0 || max_tokens == 0)
+    return Status::InvalidArgument("KV blocks: layers, heads, head_dim, blocks, sequences and tokens must be non-zero");
+  if (num_blocks > static_cast<size_t>(INT32_MAX)) return Status::InvalidArgument("KV blocks: block ids must fit int32");
+  const size_t esz = kv_dtype.nbytes();
+  if (esz == 0) return Status::InvalidArgument("KV blocks: element type has no size");
+  size_t block_bytes = 0, pool = 0;
+  if (CheckOverflowMul(num_kv_heads * head_dim, block_size * esz, &block_bytes) ||
+      CheckOverflowMul(block_bytes, num_blocks, &pool) || CheckOverflowMul(pool, 2 * num_layers, &pool_bytes_))
+    return Status::Overflow("KV blocks: pool size overflows size_t");
+  layer_bytes_ = pool * 2;
+  block_ = block_size;
+  num_blocks_ = num_blocks;
+  max_tokens_ = max_tokens;
+  stride_ = (max_tokens + block_size - 1) / block_size;
+  pools_ = alloc_.alloc(pool_bytes_, alloc_.user);
+  table_dev_ = static_cast<int32_t*>(alloc_.alloc(max_seqs * stride_ * sizeof(int32_t), alloc_.user));
+  if (pools_ == nullptr || table_dev_ == nullptr) {
+    Release();
+    return Status::ResourceExhausted("KV blocks: device allocation failed");
+  }
+  free_.resize(num_blocks);
+  for (size_t i = 0; i < num_blocks; ++i) free_[i] = static_cast<int32_t>(num_blocks - 1 - i);  // lowest at back
+  table_.assign(max_seqs * stride_, -1);
+  held_.assign(max_seqs, 0);
+  dirty_ = true;
+  return Status::Ok();
+}
+
+Status KVBlockManager::EnsureCapacity(size_t seq, size_t n) noexcept {
+  if (pools_ == nullptr) return Status::FailedPrecondition("KV blocks: not initialised");
+  if (seq >= held_.size()) return Status::OutOfRange("KV blocks: sequence out of range");
+  if (n > max_tokens_) return Status::OutOfRange("KV write exceeds reserved session token capacity");
+  const size_t need = (n + block_ - 1) / block_;
+  if (need <= held_[seq]) return Status::Ok();
+  if (need - held_[seq] > free_.size())
+    return Status::ResourceExhausted("KV blocks: the pool has " + std::to_string(free_.size()) + " free blocks, " +
+                                     std::to_string(need - held_[seq]) + " needed");
+  for (size_t b = held_[seq]; b < need; ++b) {
+    table_[seq * stride_ + b] = free_.back();
+    free_.pop_back();
+  }
+  held_[seq] = need;
+  dirty_ = true;
+  return Status::Ok();
+}
+
+Status KVBlockManager::ReleaseSequence(size_t seq) noexcept {
+  if (pools_ == nullptr) return Status::FailedPrecondition("KV blocks: not initialised");
+  if (seq >= held_.size()) return Status::OutOfRange("KV blocks: sequence out of range");
+  for (size_t b = held_[seq]; b-- > 0;) {
+    int32_t& e = table_[seq * stride_ + b];
+    free_.push_back(e);
+    e = -1;
+  }
+  // keep the lowest ids at the back so the next taker gets them first
+  std::sort(free_.begin(), free_.end(), std::greater<int32_t>());
+  held_[seq] = 0;
+  dirty_ = true;
+  return Status::Ok();
+}
+
+void* KVBlockManager::key_pool(size_t layer) const noexcept {
+  return pools_ == nullptr ? nullptr : static_cast<std::byte*>(pools_) + layer * layer_bytes_;
+}
+void* KVBlockManager::value_pool(size_t layer) const noexcept {
+  return pools_ == nullptr ? nullptr : static_cast<std::byte*>(pools_) + layer * layer_bytes_ + layer_bytes_ / 2;
+}
+
 }  // namespace aethermind

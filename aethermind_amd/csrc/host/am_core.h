@@ -572,4 +572,55 @@ class KVCacheManager {
   bool initialized_ = false;
 };
 
+// Paged (block) KV storage, the Phase-2 direction of the reference's KV design
+// (kv_cache_design.md sections 6.7 and 10; aethermind_prd.md:437-444): per layer a
+// K pool and a V pool of num_blocks blocks of [kv heads][block_size][head_dim]
+// elements, a free list of block ids, and one block table row of table_stride int32
+// entries per sequence.  A sequence holds blocks for positions [0, n) only: blocks
+// are taken when it grows (lowest free id first) and returned when it is released, so
+// sequences of different lengths share one pool.  The device copy of the table is
+// the caller's to refresh from host_table() after a change (dirty()).
+class KVBlockManager {
+ public:
+  KVBlockManager() = default;
+  explicit KVBlockManager(DeviceAllocator a) : alloc_(a) {}
+  ~KVBlockManager();
+  KVBlockManager(const KVBlockManager&) = delete;
+  KVBlockManager& operator=(const KVBlockManager&) = delete;
+  // block_size: a power of two of at least 32; max_tokens: positions per sequence.
+  Status Init(size_t num_layers, size_t num_kv_heads, size_t head_dim, DataType kv_dtype, size_t block_size,
+              size_t num_blocks, size_t max_seqs, size_t max_tokens);
+  // Gives sequence `seq` blocks for positions [0, n).  kResourceExhausted when the
+  // free blocks do not cover the growth (then nothing changes); kOutOfRange past
+  // max_tokens or for a bad sequence.
+  Status EnsureCapacity(size_t seq, size_t n) noexcept;
+  // Returns every block of `seq` to the pool and clears its table row.
+  Status ReleaseSequence(size_t seq) noexcept;
+
+  void* key_pool(size_t layer) const noexcept;
+  void* value_pool(size_t layer) const noexcept;
+  int32_t* device_table() const noexcept { return table_dev_; }
+  const std::vector<int32_t>& host_table() const noexcept { return table_; }
+  bool dirty() const noexcept { return dirty_; }
+  void clear_dirty() noexcept { dirty_ = false; }
+  size_t block_size() const noexcept { return block_; }
+  size_t num_blocks() const noexcept { return num_blocks_; }
+  size_t table_stride() const noexcept { return stride_; }
+  size_t free_blocks() const noexcept { return free_.size(); }
+  size_t blocks_of(size_t seq) const noexcept { return seq < held_.size() ? held_[seq] : 0; }
+  size_t pool_bytes() const noexcept { return pool_bytes_; }
+
+ private:
+  void Release() noexcept;
+  DeviceAllocator alloc_ = HipDeviceAllocator();
+  void* pools_ = nullptr;       // [layers][K, V][num_blocks][hkv][block][d]
+  int32_t* table_dev_ = nullptr;
+  size_t pool_bytes_ = 0, layer_bytes_ = 0;
+  size_t block_ = 0, num_blocks_ = 0, stride_ = 0, max_tokens_ = 0;
+  std::vector<int32_t> free_;   // free block ids, the lowest at the back
+  std::vector<int32_t> table_;  // [max_seqs][stride], -1 = no block
+  std::vector<size_t> held_;    // blocks per sequence
+  bool dirty_ = false;
+};
+
 }  // namespace aethermind

@@ -125,6 +125,10 @@ Status RoPEKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_rope(&a, StreamOf(ctx)));
 }
 
+am_gfx950_kv_pages PagesOf(const KvPaging& pg) {
+  return am_gfx950_kv_pages{pg.table, pg.block, pg.stride, pg.num_blocks};
+}
+
 Status KVCacheUpdateKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
   AM_RETURN_IF_ERROR(NeedArgs(p, 5, 0, "KVCacheUpdateKernel"));
@@ -141,6 +145,8 @@ Status KVCacheUpdateKernel(const KernelContext& ctx) noexcept {
   a.head_dim = at.d;
   a.capacity = at.cap;
   a.dtype = p->in[0].dt;
+  const am_gfx950_kv_pages pages = PagesOf(at.pg);
+  if (at.pg.table != nullptr) a.pages = &pages;
   return FromC(am_gfx950_kv_update(&a, StreamOf(ctx)));
 }
 
@@ -171,6 +177,8 @@ Status AttentionKernel(const KernelContext& ctx) noexcept {
   a.num_splits = at.splits;
   a.workspace = ctx.workspace_binding.data;
   a.workspace_bytes = static_cast<int64_t>(ctx.workspace_binding.size);
+  const am_gfx950_kv_pages pages = PagesOf(at.pg);
+  if (at.pg.table != nullptr) a.pages = &pages;
   return FromC(am_gfx950_attention(&a, StreamOf(ctx)));
 }
 
@@ -235,6 +243,8 @@ Status FusedQkvKernel(const KernelContext& ctx) noexcept {
   a.dtype = p->in[0].dt;
   a.rows = p->in[0].rank > 1 ? p->in[0].d[0] : 1;
   a.cache_batch_stride = at.cbs;
+  const am_gfx950_kv_pages pages = PagesOf(at.pg);
+  if (at.pg.table != nullptr) a.pages = &pages;
   return FromC(am_gfx950_fused_qkv(&a, StreamOf(ctx)));
 }
 

@@ -32,11 +32,18 @@ Status BuildGfxParams(std::span<const TensorView> inputs, std::span<const Mutabl
 // rmsnorm_op.cpp:9-29).
 struct NormAttrs { float eps; };
 struct RopeAttrs { int64_t hq, hkv, d, max_pos; };
-struct KvAttrs { int64_t hkv, d, cap; };
+// Paged KV (am_gfx950_kv_pages): the cache inputs are block pools and `table` the
+// device block table (row r = sequence r); a null table is the contiguous layout.
+struct KvPaging {
+  const int32_t* table = nullptr;
+  int32_t block = 0, stride = 0;
+  int64_t num_blocks = 0;
+};
+struct KvAttrs { int64_t hkv, d, cap; KvPaging pg; };
 // batch > 1: q holds batch sequences of seq/batch rows each; sequence r's cache planes
 // start cbs elements after sequence r-1's (cbs is the same batch stride for QkvAttrs).
-struct AttnAttrs { int64_t hq, hkv, d, cap; int32_t splits; int64_t batch, cbs; };
-struct QkvAttrs { float eps; int64_t hq, hkv, d, cap, cbs; };
+struct AttnAttrs { int64_t hq, hkv, d, cap; int32_t splits; int64_t batch, cbs; KvPaging pg; };
+struct QkvAttrs { float eps; int64_t hq, hkv, d, cap, cbs; KvPaging pg; };
 struct DecodeLayersAttrs { float eps; int64_t layers, hidden, hq, hkv, d, ffn, cap; };
 
 template <typename T>

@@ -569,6 +569,12 @@ class LlamaSession {
   std::unique_ptr<KVCacheManager> kv;
   int64_t kv_row_elems = 0;
   std::vector<KVCacheView> views;
+  // Paged KV (opt.kv_block_size > 0) instead: one block pool for every sequence; the
+  // device block table is refreshed from a pinned mirror, on the stream, before the
+  // work that first uses new blocks (table_ev: the last refresh has read the mirror)
+  std::unique_ptr<KVBlockManager> blocks;
+  int32_t* table_pinned = nullptr;
+  hipEvent_t table_ev = nullptr;
 
   // device buffers
   void* act_slab = nullptr;
@@ -607,6 +613,9 @@ class LlamaSession {
     if (graph) (void)hipGraphDestroy(graph);
     views.clear();
     kv.reset();
+    if (table_ev) (void)hipEventSynchronize(table_ev), (void)hipEventDestroy(table_ev);
+    blocks.reset();
+    if (table_pinned) (void)hipHostFree(table_pinned);
     if (act_slab) (void)hipFree(act_slab);
     if (dl_table) (void)hipFree(dl_table);
     if (dl_ws) (void)hipFree(dl_ws);
@@ -618,6 +627,54 @@ class LlamaSession {
   int64_t* step_ptr() const { return state + 2 * B; }
   int64_t* hist_ptr(int64_t r = 0) const { return hist + r * HistStride(); }
   int64_t host_pos() const { return row_pos.empty() ? 0 : row_pos[0]; }
+
+  // Copies a changed block table to the device, ordered on the session stream.
+  Status SyncTable() {
+    if (!blocks || !blocks->dirty()) return Status::Ok();
+    AM_HIP_OK(hipEventSynchronize(table_ev));  // the previous refresh has read the mirror
+    const auto& t = blocks->host_table();
+    std::memcpy(table_pinned, t.data(), t.size() * 4);
+    AM_HIP_OK(hipMemcpyAsync(blocks->device_table(), table_pinned, t.size() * 4, hipMemcpyHostToDevice, stream));
+    AM_HIP_OK(hipEventRecord(table_ev, stream));
+    blocks->clear_dirty();
+    return Status::Ok();
+  }
+
+  // Paging of the ops reading sequence `row` (batched ops: row 0, the table base).
+  gfx950::KvPaging Paging(int64_t row) const {
+    gfx950::KvPaging pg;
+    if (!blocks) return pg;
+    pg.table = blocks->device_table() + row * static_cast<int64_t>(blocks->table_stride());
+    pg.block = static_cast<int32_t>(blocks->block_size());
+    pg.stride = static_cast<int32_t>(blocks->table_stride());
+    pg.num_blocks = static_cast<int64_t>(blocks->num_blocks());
+    return pg;
+  }
+
+  // K and V cache bases of layer l for sequence `row`: its slot's planes, or the
+  // layer's block pools when the KV is paged.
+  Status Planes(int64_t l, int64_t row, void** kp, void** vp) const {
+    if (blocks) {
+      *kp = blocks->key_pool(static_cast<size_t>(l));
+      *vp = blocks->value_pool(static_cast<size_t>(l));
+      return Status::Ok();
+    }
+    auto k = views[static_cast<size_t>(row)].KeyPlane(static_cast<size_t>(l));
+    auto v = views[static_cast<size_t>(row)].ValuePlane(static_cast<size_t>(l));
+    if (!k.ok()) return k.status();
+    if (!v.ok()) return v.status();
+    *kp = k.value();
+    *vp = v.value();
+    return Status::Ok();
+  }
+
+  // Paged KV: blocks for the next n decode steps of every sequence.
+  Status GrowForDecode(int64_t n) {
+    if (!blocks) return Status::Ok();
+    for (int64_t r = 0; r < B; ++r)
+      AM_RETURN_IF_ERROR(blocks->EnsureCapacity(static_cast<size_t>(r), static_cast<size_t>(row_pos[r] + n)));
+    return SyncTable();
+  }
 
   Status Init(LlamaModel* model, const am_session_options* o) {
     m = model;
@@ -635,15 +692,31 @@ class LlamaSession {
     backend = b.value();
     (void)am::DeviceCUs();
 
-    // KV: a pool of B slots of max_tokens positions, sequence r in slot r
-    kv = std::make_unique<KVCacheManager>(HipDeviceAllocator());
-    AM_RETURN_IF_ERROR(kv->Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype), 256,
-                                static_cast<size_t>(B)));
-    kv_row_elems = static_cast<int64_t>(kv->storage().slot_bytes / ActBytes(c.act_dtype));
-    for (int64_t r = 0; r < B; ++r) {
-      auto vw = kv->ReserveSlot(static_cast<size_t>(r), 0, static_cast<size_t>(c.max_tokens));
-      if (!vw.ok()) return vw.status();
-      views.push_back(vw.value());
+    if (opt.kv_block_size > 0) {
+      // paged KV: a pool of blocks shared by the B sequences
+      if (c.act_dtype != AM_DT_BF16) return Status::Unimplemented("paged KV needs bf16 activations");
+      if (opt.persistent_decode > 0) return Status::Unimplemented("paged KV does not run with persistent_decode");
+      const int64_t bs = opt.kv_block_size, per_seq = (c.max_tokens + bs - 1) / bs;
+      const int64_t nb = opt.kv_pool_blocks > 0 ? opt.kv_pool_blocks : B * per_seq;
+      blocks = std::make_unique<KVBlockManager>(HipDeviceAllocator());
+      AM_RETURN_IF_ERROR(blocks->Init(c.num_layers, c.num_kv_heads, c.head_dim, ActType(c.act_dtype),
+                                      static_cast<size_t>(bs), static_cast<size_t>(nb), static_cast<size_t>(B),
+                                      static_cast<size_t>(c.max_tokens)));
+      AM_HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&table_pinned), blocks->host_table().size() * 4,
+                              hipHostMallocDefault));
+      AM_HIP_OK(hipEventCreateWithFlags(&table_ev, hipEventDisableTiming));
+      AM_RETURN_IF_ERROR(SyncTable());
+    } else {
+      // KV: a pool of B slots of max_tokens positions, sequence r in slot r
+      kv = std::make_unique<KVCacheManager>(HipDeviceAllocator());
+      AM_RETURN_IF_ERROR(kv->Init(c.num_layers, c.num_kv_heads, c.max_tokens, c.head_dim, ActType(c.act_dtype), 256,
+                                  static_cast<size_t>(B)));
+      kv_row_elems = static_cast<int64_t>(kv->storage().slot_bytes / ActBytes(c.act_dtype));
+      for (int64_t r = 0; r < B; ++r) {
+        auto vw = kv->ReserveSlot(static_cast<size_t>(r), 0, static_cast<size_t>(c.max_tokens));
+        if (!vw.ok()) return vw.status();
+        views.push_back(vw.value());
+      }
     }
     row_pos.assign(static_cast<size_t>(B), 0);
     row_ready.assign(static_cast<size_t>(B), 0);
@@ -822,10 +895,8 @@ class LlamaSession {
     const auto& c = m->cfg;
     const DataType A = ActType(c.act_dtype);
     const int64_t H = c.hidden, F = c.ffn, d = c.head_dim, Q = m->QRows(), KV = m->KvRows();
-    auto kp = views[static_cast<size_t>(row)].KeyPlane(static_cast<size_t>(l));
-    auto vp = views[static_cast<size_t>(row)].ValuePlane(static_cast<size_t>(l));
-    if (!kp.ok()) return kp.status();
-    if (!vp.ok()) return vp.status();
+    void *kp = nullptr, *vp = nullptr;
+    AM_RETURN_IF_ERROR(Planes(l, row, &kp, &vp));
     const gfx950::NormAttrs na{c.rms_eps};
     auto& W = s_views[static_cast<size_t>(l)];
     const TensorView hv(h, A, {S, H}), xnv(xn, A, {S, H});
@@ -852,14 +923,14 @@ class LlamaSession {
                               TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
                               TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2})},
                              {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV})}));
-    const gfx950::KvAttrs ka{c.num_kv_heads, d, c.max_tokens};
-    const TensorView kplane(kp.value(), A, {c.num_kv_heads, c.max_tokens, d});
-    const TensorView vplane(vp.value(), A, {c.num_kv_heads, c.max_tokens, d});
+    const gfx950::KvAttrs ka{c.num_kv_heads, d, c.max_tokens, Paging(row)};
+    const TensorView kplane(kp, A, {c.num_kv_heads, c.max_tokens, d});
+    const TensorView vplane(vp, A, {c.num_kv_heads, c.max_tokens, d});
     AM_RETURN_IF_ERROR(b.Add(OpType::kKVCacheUpdate, PackAttrs(ka), Sel(false, ph), nullptr,
                              {TensorView(k, A, {S, KV}), TensorView(v, A, {S, KV}), kplane, vplane,
                               TensorView(start, DataType::Int(64), {1})},
                              {}));
-    const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, 1, 0};
+    const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, 1, 0, Paging(row)};
     AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
                              {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},
                              {MutableTensorView(attn, A, {S, Q})}, attn_ws_bytes));
@@ -976,20 +1047,18 @@ class LlamaSession {
         AM_RETURN_IF_ERROR(AddLayerUnfused(b, l, 1, ph, pos_ptr(), pos_ptr(), 0));
         continue;
       }
-      auto kp = views[0].KeyPlane(static_cast<size_t>(l));
-      auto vp = views[0].ValuePlane(static_cast<size_t>(l));
-      if (!kp.ok()) return kp.status();
-      if (!vp.ok()) return vp.status();
-      const TensorView kplane(kp.value(), A, {c.num_kv_heads, c.max_tokens, d});
-      const TensorView vplane(vp.value(), A, {c.num_kv_heads, c.max_tokens, d});
-      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens, kv_row_elems};
+      void *kp = nullptr, *vp = nullptr;
+      AM_RETURN_IF_ERROR(Planes(l, 0, &kp, &vp));
+      const TensorView kplane(kp, A, {c.num_kv_heads, c.max_tokens, d});
+      const TensorView vplane(vp, A, {c.num_kv_heads, c.max_tokens, d});
+      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens, kv_row_elems, Paging(0)};
       AM_RETURN_IF_ERROR(b.Add(OpType::kFusedRmsNormQkvRoPEKVUpdate, PackAttrs(qa), Sel(true, ph), &m->qkv[l],
                                {TensorView(h, A, {B, H}), TensorView(m->in_norm[l], A, {H}),
                                 TensorView(pos_ptr(), DataType::Int(64), {B}),
                                 TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
                                 TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2}), kplane, vplane},
                                {MutableTensorView(q, A, {B, Q})}));
-      const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, B, kv_row_elems};
+      const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, B, kv_row_elems, Paging(0)};
       AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
                                {TensorView(q, A, {B, Q}), kplane, vplane, TensorView(pos_ptr(), DataType::Int(64), {B})},
                                {MutableTensorView(attn, A, {B, Q})}, attn_ws_bytes));
@@ -1032,11 +1101,18 @@ class LlamaSession {
     for (int64_t i = 0; i < n; ++i)
       if (prompt[i] < 0 || prompt[i] >= c.vocab) return Status::OutOfRange("EmbeddingKernel token id is out of vocabulary range");
     const size_t ri = static_cast<size_t>(row);
-    AM_RETURN_IF_ERROR(kv->ReleaseSession(views[ri]));
-    auto vw = kv->ReserveSlot(ri, 0, static_cast<size_t>(c.max_tokens));
-    if (!vw.ok()) return vw.status();
-    views[ri] = vw.value();  // same slot planes: the decode plan and graph stay valid
     row_ready[ri] = 0;
+    if (blocks) {
+      // the row's blocks go back to the pool; the prompt takes blocks for [0, n)
+      AM_RETURN_IF_ERROR(blocks->ReleaseSequence(ri));
+      AM_RETURN_IF_ERROR(blocks->EnsureCapacity(ri, static_cast<size_t>(n)));
+      AM_RETURN_IF_ERROR(SyncTable());
+    } else {
+      AM_RETURN_IF_ERROR(kv->ReleaseSession(views[ri]));
+      auto vw = kv->ReserveSlot(ri, 0, static_cast<size_t>(c.max_tokens));
+      if (!vw.ok()) return vw.status();
+      views[ri] = vw.value();  // same slot planes: the decode plan and graph stay valid
+    }
     const int64_t chunk = c.max_prefill_chunk;
     std::vector<int64_t> pos_host(static_cast<size_t>(chunk));
     for (int64_t p0 = 0; p0 < n; p0 += chunk) {
@@ -1069,7 +1145,7 @@ class LlamaSession {
       AM_RETURN_IF_ERROR(Executor::Execute(plan.value(), bind));
       AM_HIP_OK(hipStreamSynchronize(stream));  // pos_host / state staging reuse
     }
-    AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(n)));
+    if (!blocks) AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(n)));
     int64_t tok = 0;
     AM_HIP_OK(hipMemcpy(&tok, token_ptr(row), 8, hipMemcpyDeviceToHost));
     int32_t e = 0;
@@ -1096,13 +1172,14 @@ class LlamaSession {
     for (int64_t r = 0; r < B; ++r) {
       const size_t ri = static_cast<size_t>(r);
       row_pos[ri] += n;
-      AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(row_pos[ri])));
+      if (!blocks) AM_RETURN_IF_ERROR(views[ri].CommitUntil(static_cast<size_t>(row_pos[ri])));
     }
     return Status::Ok();
   }
 
   Status EnqueueDecode(int64_t n) {
     AM_RETURN_IF_ERROR(CheckDecode(n));
+    AM_RETURN_IF_ERROR(GrowForDecode(n));
     if (opt.use_graph) {
       if (!graph_exec) {
         AM_HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
@@ -1147,6 +1224,7 @@ class LlamaSession {
   // around the step.
   Status Profile(int64_t n, double* ms_by_op, int64_t* count_by_op) {
     AM_RETURN_IF_ERROR(CheckDecode(n));
+    AM_RETURN_IF_ERROR(GrowForDecode(n));
     const auto& steps = decode_plan->steps();
     std::vector<hipEvent_t> e0(steps.size(), nullptr), e1(steps.size(), nullptr);
     Status st;

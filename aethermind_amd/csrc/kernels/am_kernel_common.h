@@ -25,6 +25,34 @@ am_status_code SetLastError(am_status_code code, const char* msg);
 inline hipStream_t AsStream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// KV cache row addressing, in elements from the cache (pool) base.  Contiguous
+// (table == nullptr): sequence b's planes start b * cbs elements in and head g's rows
+// g * cap * d after that.  Paged: the cache is a pool of blocks [hkv][1 << shift][d]
+// and table[b * stride + (pos >> shift)] names the block holding position pos of
+// sequence b (clamped into [0, num_blocks) so a bad table cannot address outside the
+// pool).  A run of positions that starts at a multiple of 32 and stays inside 32
+// positions lies in one block (blocks are at least 32 positions), so kernels look up
+// one block per 32-position step.
+struct KvRows {
+  const int32_t* table = nullptr;
+  int64_t cbs = 0, cap = 0;
+  int64_t num_blocks = 0;
+  int32_t shift = 0, stride = 0;
+  int32_t hkv = 0, d = 0;
+
+  __device__ __forceinline__ int64_t Row(int64_t b, int64_t g, int64_t pos) const {
+    if (table == nullptr) return b * cbs + (g * cap + pos) * d;
+    int64_t blk = table[b * stride + (pos >> shift)];
+    blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);
+    return (((blk * hkv + g) << shift) + (pos & ((int64_t{1} << shift) - 1))) * d;
+  }
+};
+
+// Host side: the KvRows of a cache (pages may be null) after checking the page table
+// arguments against the logical capacity.
+am_status_code MakeKvRows(const am_gfx950_kv_pages* pages, int64_t cbs, int64_t cap, int64_t hkv, int64_t d,
+                          KvRows* out);
+
 // Number of compute units of the current device (cached per device).
 int DeviceCUs();
 

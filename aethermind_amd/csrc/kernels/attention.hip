@@ -50,6 +50,7 @@ struct AttnArgs {
   float scale;  // log2(e) / sqrt(d)
   float* part;
   unsigned* tickets;  // [rows][hkv], zero between calls
+  KvRows kv;          // row addressing of the (possibly paged) cache
 };
 
 constexpr int kWaves = 8;
@@ -483,9 +484,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
   const int64_t g = blockIdx.y;
   const int split = blockIdx.x;
   const int64_t n_keys = row_keys(p, b, s);
-  const int64_t nsplit = live_splits(n_keys, p.splits, p.min_per_split);
+  // Slices are whole 32-position steps (a step then never straddles two cache blocks):
+  // the slice length is rounded up to 32 and the live split count follows from it,
+  // the same in every block of the (row, kv head).
+  const int64_t ns0 = live_splits(n_keys, p.splits, p.min_per_split);
+  const int64_t per = (((n_keys + ns0 - 1) / ns0) + 31) & ~int64_t{31};
+  const int64_t nsplit = (n_keys + per - 1) / per;
   if (split >= nsplit) return;  // surplus block for this context
-  const int64_t per = (n_keys + nsplit - 1) / nsplit;
   const int64_t lo = split * per;
   const int64_t hi = lo + per < n_keys ? lo + per : n_keys;
   const int64_t nsteps = (hi - lo + 31) / 32;
@@ -504,31 +509,36 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
     q3 = *reinterpret_cast<const uint4*>(qp + 96);
   }
 
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.kc) + b * p.cbs + g * p.cap * D;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.vc) + b * p.cbs + g * p.cap * D;
+  const uint16_t* kc0 = static_cast<const uint16_t*>(p.kc);
+  const uint16_t* vc0 = static_cast<const uint16_t*>(p.vc);
 
   struct Buf {
     uint4 k[2][KK];    // two 16-row score tiles
     uint32_t v[8][VW];  // V[position of k slot c][CW j .. CW j + CW)
   };
   // Loads step i (clamped to this wave's last step; rows past the slice read row
-  // hi - 1, whose scores are masked to -inf).  Offsets are 32-bit element offsets from
-  // the (row, kv head) bases: one head's cache is cap * D elements.
-  const uint32_t last_row = static_cast<uint32_t>(hi - 1);
+  // hi - 1, whose scores are masked to -inf).  The step's 32 rows are contiguous from
+  // its first row, whose offset (the same in K and V) is looked up once per step;
+  // lanes add 32-bit row offsets to it.
+  const int64_t last_row = hi - 1;
   auto issue = [&](Buf& bf, int64_t i) {
     if (i >= my) i = my - 1;
-    const uint32_t base = static_cast<uint32_t>(lo + 32 * (wave + i * NW));
+    const int64_t base = lo + 32 * (wave + i * NW);
+    const int64_t off = p.kv.Row(b, g, base);
+    const uint16_t* ks = kc0 + off;
+    const uint16_t* vs = vc0 + off;
+    const uint32_t lim = static_cast<uint32_t>(last_row - base);  // last readable row of the step
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const uint32_t pos = min(base + 16 * tt + j, last_row);
-      const uint16_t* kp = kbase + (pos * D + 8 * h);
+      const uint32_t r = min(static_cast<uint32_t>(16 * tt + j), lim);
+      const uint16_t* kp = ks + (r * D + 8 * h);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) bf.k[tt][kk] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const uint32_t pos = min(base + 16 * (c >> 2) + 4 * h + (c & 3), last_row);
-      const uint16_t* vp = vbase + (pos * D + CW * j);
+      const uint32_t r = min(static_cast<uint32_t>(16 * (c >> 2) + 4 * h + (c & 3)), lim);
+      const uint16_t* vp = vs + (r * D + CW * j);
       if constexpr (VW == 4) {
         const uint4 t = *reinterpret_cast<const uint4*>(vp);
         bf.v[c][0] = t.x, bf.v[c][1] = t.y, bf.v[c][2] = t.z, bf.v[c][3] = t.w;
@@ -726,17 +736,20 @@ __global__ __launch_bounds__(kPreWaves * 64) void attention_prefill_kernel(AttnA
       qop[kk] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.kc) + b * p.cbs + g * p.cap * D;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.vc) + b * p.cbs + g * p.cap * D;
-  const uint32_t last_row = static_cast<uint32_t>(kend - 1);
+  const uint16_t* kc0 = static_cast<const uint16_t*>(p.kc);
+  const uint16_t* vc0 = static_cast<const uint16_t*>(p.vc);
+  const int64_t last_row = kend - 1;
   uint4 kr[PCH], vr[PCH];
-  // piece c of the thread: tile row tid / PR + c * NT / PR, 8 columns at 8 * (tid % PR)
+  // piece c of the thread: tile row tid / PR + c * NT / PR, 8 columns at 8 * (tid % PR);
+  // a tile's 32 rows are contiguous from its first row (one offset lookup per tile)
   auto load_tile = [&](int64_t t) {
+    const int64_t off = p.kv.Row(b, g, t * TP);
+    const uint32_t lim = static_cast<uint32_t>(min(last_row - t * TP, int64_t{TP - 1}));
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
-      const uint32_t pos = min(static_cast<uint32_t>(t * TP + tid / PR + c * (NT / PR)), last_row);
-      kr[c] = *reinterpret_cast<const uint4*>(kbase + (pos * D + 8 * (tid % PR)));
-      vr[c] = *reinterpret_cast<const uint4*>(vbase + (pos * D + 8 * (tid % PR)));
+      const uint32_t r = min(static_cast<uint32_t>(tid / PR + c * (NT / PR)), lim);
+      kr[c] = *reinterpret_cast<const uint4*>(kc0 + off + (r * D + 8 * (tid % PR)));
+      vr[c] = *reinterpret_cast<const uint4*>(vc0 + off + (r * D + 8 * (tid % PR)));
     }
   };
   auto store_tile = [&](int buf) {
@@ -1027,6 +1040,9 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
   p.start = a->start_pos;
   p.start_dev = a->start_pos_dev;
   p.cbs = batch > 1 ? a->cache_batch_stride : 0;
+  if (auto st = MakeKvRows(a->pages, p.cbs, a->capacity, a->hkv, a->head_dim, &p.kv); st != AM_STATUS_OK) return st;
+  if (a->pages != nullptr)
+    AM_CHECK_ARG(a->dtype == AM_DT_BF16, "attention: a paged KV cache needs bf16 activations");
   p.splits = splits;
   p.scale = kLog2e / sqrtf(static_cast<float>(a->head_dim));
   if (splits > 1) {

@@ -64,6 +64,7 @@ struct GemvArgs {
   int64_t* pi;
   int32_t out_f32;
   int32_t vec;  // x, norm_w, residual 16-byte aligned and whole 16-byte pieces
+  KvRows kv;    // K/V row addressing of the q/k/v epilogue
 };
 
 // k values per 16-byte chunk of a weight row
@@ -609,13 +610,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
           A::store(q, head * p.d + i + half, o1);
         } else if (posv < p.cap) {
           T* kc = static_cast<T*>(p.k_cache);
-          const int64_t base = ((head - p.hq) * p.cap + posv) * p.d;
+          const int64_t base = p.kv.Row(0, head - p.hq, posv);
           A::store(kc, base + i, o0);
           A::store(kc, base + i + half, o1);
         }
       } else if (posv < p.cap) {
         T* vc = static_cast<T*>(p.v_cache);
-        const int64_t base = ((head - p.hq - p.hkv) * p.cap + posv) * p.d;
+        const int64_t base = p.kv.Row(0, head - p.hq - p.hkv, posv);
         A::store(vc, base + i, y0);
         A::store(vc, base + i + half, y1);
       }
@@ -1110,6 +1111,7 @@ extern "C" am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* a,
   g.hkv = static_cast<int32_t>(a->hkv);
   g.d = static_cast<int32_t>(a->head_dim);
   g.cap = a->capacity;
+  if (auto st = MakeKvRows(a->pages, 0, a->capacity, a->hkv, a->head_dim, &g.kv); st != AM_STATUS_OK) return st;
   return Dispatch<true, kEpiQkv>(a->dtype, a->w_qkv.format, g, AsStream(stream));
 }
 

@@ -66,6 +66,7 @@ struct BatchArgs {
   uint16_t* v_cache;
   int32_t hq, hkv, d;
   int64_t cap, cbs;  // cache capacity (positions), elements between rows' caches
+  KvRows kv;         // K/V row addressing (contiguous rows cbs apart, or paged)
 };
 
 // k values per step (64 bytes of a weight row) and MFMAs per 16-byte lane slice
@@ -421,12 +422,12 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
             q[i] = f32_to_bf16_bits(o0);
             q[i + half] = f32_to_bf16_bits(o1);
           } else if (in_cache) {
-            uint16_t* kc = p.k_cache + b * p.cbs + ((head - p.hq) * p.cap + pos) * p.d;
+            uint16_t* kc = p.k_cache + p.kv.Row(b, head - p.hq, pos);
             kc[i] = f32_to_bf16_bits(o0);
             kc[i + half] = f32_to_bf16_bits(o1);
           }
         } else if (in_cache) {
-          uint16_t* vc = p.v_cache + b * p.cbs + ((head - p.hq - p.hkv) * p.cap + pos) * p.d;
+          uint16_t* vc = p.v_cache + p.kv.Row(b, head - p.hq - p.hkv, pos);
           vc[i] = f32_to_bf16_bits(y0);
           vc[i + half] = f32_to_bf16_bits(y1);
         }
@@ -586,6 +587,7 @@ am_status_code BatchQkv(const am_gfx950_fused_qkv_args* q, hipStream_t s) {
   a.d = static_cast<int32_t>(q->head_dim);
   a.cap = q->capacity;
   a.cbs = q->cache_batch_stride;
+  if (auto st = MakeKvRows(q->pages, a.cbs, a.cap, q->hkv, q->head_dim, &a.kv); st != AM_STATUS_OK) return st;
   a.units = static_cast<int32_t>((q->hq + 2 * q->hkv) * (q->head_dim / 32));
   return DispatchBatch<kBQkv, true, 2>(q->w_qkv.format, a, lds, s);
 }

@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const uint8_t* k, const 
                                                         uint8_t* vc, int64_t seq, int64_t hkv,
                                                         int64_t row_bytes, int64_t cap,
                                                         int64_t start, const int64_t* start_dev,
-                                                        int32_t* err) {
+                                                        int32_t* err, KvRows kv, int64_t esz) {
   const int64_t st = start_dev != nullptr ? *start_dev : start;
   const int64_t g16 = row_bytes / 16;
   const int64_t total = seq * hkv * g16;
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const uint8_t* k, const 
       continue;
     }
     const int64_t src = (s * hkv + h) * row_bytes + c * 16;
-    const int64_t dst = (h * cap + p) * row_bytes + c * 16;
+    const int64_t dst = kv.Row(0, h, p) * esz + c * 16;
     *reinterpret_cast<uint4*>(kc + dst) = *reinterpret_cast<const uint4*>(k + src);
     *reinterpret_cast<uint4*>(vc + dst) = *reinterpret_cast<const uint4*>(v + src);
   }
@@ -364,6 +364,31 @@ extern "C" am_status_code am_gfx950_rope(const am_gfx950_rope_args* a, void* str
   return AM_STATUS_OK;
 }
 
+namespace am {
+am_status_code MakeKvRows(const am_gfx950_kv_pages* pages, int64_t cbs, int64_t cap, int64_t hkv, int64_t d,
+                          KvRows* out) {
+  KvRows r;
+  r.cbs = cbs;
+  r.cap = cap;
+  r.hkv = static_cast<int32_t>(hkv);
+  r.d = static_cast<int32_t>(d);
+  if (pages != nullptr) {
+    AM_CHECK_ARG(pages->block_table != nullptr, "kv pages: null block table");
+    AM_CHECK_ARG(pages->block_size >= 32 && (pages->block_size & (pages->block_size - 1)) == 0,
+                 "kv pages: block_size must be a power of two of at least 32");
+    AM_CHECK_ARG(pages->table_stride > 0 && pages->num_blocks > 0, "kv pages: bad table stride or block count");
+    AM_CHECK_ARG(cap <= static_cast<int64_t>(pages->table_stride) * pages->block_size,
+                 "kv pages: capacity exceeds table_stride * block_size");
+    r.table = pages->block_table;
+    r.num_blocks = pages->num_blocks;
+    r.stride = pages->table_stride;
+    r.shift = __builtin_ctz(static_cast<unsigned>(pages->block_size));
+  }
+  *out = r;
+  return AM_STATUS_OK;
+}
+}  // namespace am
+
 extern "C" am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* a, void* stream) {
   AM_CHECK_ARG(a != nullptr, "kv_update: null args");
   AM_CHECK_ARG(IsAct(a->dtype), "kv_update: dtype must be f32 or bf16");
@@ -376,11 +401,13 @@ extern "C" am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* a,
     if (a->start_pos < 0 || a->start_pos + a->seq > a->capacity)
       return SetLastError(AM_STATUS_OUT_OF_RANGE, "KV write exceeds physical KV capacity");
   }
+  KvRows kv;
+  if (auto st = MakeKvRows(a->pages, 0, a->capacity, a->hkv, a->head_dim, &kv); st != AM_STATUS_OK) return st;
   const int grid = GridFor(a->seq * a->hkv * (row_bytes / 16));
   hipLaunchKernelGGL(kv_update_kernel, dim3(grid), dim3(256), 0, AsStream(stream),
                      static_cast<const uint8_t*>(a->k), static_cast<const uint8_t*>(a->v),
                      static_cast<uint8_t*>(a->k_cache), static_cast<uint8_t*>(a->v_cache), a->seq, a->hkv,
-                     row_bytes, a->capacity, a->start_pos, a->start_pos_dev, a->err_flag);
+                     row_bytes, a->capacity, a->start_pos, a->start_pos_dev, a->err_flag, kv, esz);
   AM_RETURN_IF_LAUNCH_FAILED("kv_update");
   return AM_STATUS_OK;
 }

@@ -58,17 +58,21 @@ class RopeArgs(C.Structure):
                 ("seq", i64), ("hq", i64), ("hkv", i64), ("head_dim", i64), ("max_pos", i64), ("dtype", i32)]
 
 
+class KvPages(C.Structure):
+    _fields_ = [("block_table", vp), ("block_size", i32), ("table_stride", i32), ("num_blocks", i64)]
+
+
 class KvUpdateArgs(C.Structure):
     _fields_ = [("k", vp), ("v", vp), ("k_cache", vp), ("v_cache", vp), ("seq", i64), ("hkv", i64),
                 ("head_dim", i64), ("capacity", i64), ("start_pos", i64), ("start_pos_dev", vp), ("dtype", i32),
-                ("err_flag", vp)]
+                ("err_flag", vp), ("pages", C.POINTER(KvPages))]
 
 
 class AttentionArgs(C.Structure):
     _fields_ = [("q", vp), ("k_cache", vp), ("v_cache", vp), ("out", vp), ("seq", i64), ("hq", i64), ("hkv", i64),
                 ("head_dim", i64), ("capacity", i64), ("start_pos", i64), ("start_pos_dev", vp), ("batch", i64),
                 ("cache_batch_stride", i64), ("dtype", i32), ("num_splits", i32), ("workspace", vp),
-                ("workspace_bytes", i64)]
+                ("workspace_bytes", i64), ("pages", C.POINTER(KvPages))]
 
 
 class SiluMulArgs(C.Structure):
@@ -111,7 +115,8 @@ class SynthArgs(C.Structure):
 class FusedQkvArgs(C.Structure):
     _fields_ = [("h", vp), ("norm_w", vp), ("eps", f32), ("w_qkv", Weight), ("cos_tab", vp), ("sin_tab", vp),
                 ("pos", vp), ("q_out", vp), ("k_cache", vp), ("v_cache", vp), ("hq", i64), ("hkv", i64),
-                ("head_dim", i64), ("capacity", i64), ("dtype", i32), ("rows", i64), ("cache_batch_stride", i64)]
+                ("head_dim", i64), ("capacity", i64), ("dtype", i32), ("rows", i64), ("cache_batch_stride", i64),
+                ("pages", C.POINTER(KvPages))]
 
 
 class FusedLinearResidualArgs(C.Structure):
@@ -166,7 +171,8 @@ class SessionConfig(C.Structure):
 
 
 class SessionOptions(C.Structure):
-    _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32)]
+    _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32),
+                ("kv_block_size", i32), ("kv_pool_blocks", i32)]
 
 
 _SIGS = {

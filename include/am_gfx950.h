@@ -163,10 +163,28 @@ am_status_code am_gfx950_rope(const am_gfx950_rope_args* args, void* hip_stream)
 am_status_code am_gfx950_rope_table(int64_t max_pos, int64_t head_dim, double theta,
                                     float* cos_tab_host, float* sin_tab_host);
 
+/* Paged (block) KV cache.  The PRD's Phase-2 direction (aethermind_prd.md:437-444;
+ * kv_cache_design.md 6.7 and 10: "replace the storage and offset resolution under a
+ * stable logical view").  With pages, k_cache / v_cache of a layer are pools of
+ * num_blocks blocks, each [hkv][block_size][head_dim] elements, and position pos of
+ * sequence b lives in block block_table[b * table_stride + pos / block_size] at row
+ * pos % block_size.  capacity stays the logical position limit per sequence (at most
+ * table_stride * block_size); cache_batch_stride is unused.  Block ids outside
+ * [0, num_blocks) are clamped into it on the device (the runtime never writes one).
+ * Without pages (pages == NULL) a sequence's cache is contiguous: head g's rows start
+ * g * capacity * head_dim elements into its planes. */
+typedef struct am_gfx950_kv_pages {
+  const int32_t* block_table; /* device [batch][table_stride] */
+  int32_t block_size;         /* positions per block: a power of two, at least 32 */
+  int32_t table_stride;       /* table entries per sequence */
+  int64_t num_blocks;         /* blocks in each pool */
+} am_gfx950_kv_pages;
+
 /* OpType::kKVCacheUpdate (kvcache_update_op.cpp:50-138): writes k/v [seq][hkv*d]
  * into the layer planes at positions [start, start+seq), start = *start_pos_dev if
  * start_pos_dev != NULL else start_pos.  Rows past capacity are rejected on the host
- * when start is a host value, and skipped (err_flag set) when it is a device value. */
+ * when start is a host value, and skipped (err_flag set) when it is a device value.
+ * pages != NULL: the sequence's table row is pages->block_table (bf16 or f32). */
 typedef struct am_gfx950_kv_update_args {
   const void* k;
   const void* v;
@@ -177,6 +195,7 @@ typedef struct am_gfx950_kv_update_args {
   const int64_t* start_pos_dev;
   int32_t dtype;
   int32_t* err_flag;
+  const am_gfx950_kv_pages* pages; /* NULL: contiguous planes */
 } am_gfx950_kv_update_args;
 am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* args, void* hip_stream);
 
@@ -190,7 +209,8 @@ am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* args, void* h
  * over positions when the context is long; the last block of each (row, kv head)
  * merges the partial records, so one launch produces the output.
  * batch > 1 stacks independent sequences: q [batch][seq][hq*d], caches
- * [batch] planes of cache_batch_stride elements, start positions start_pos_dev[b]. */
+ * [batch] planes of cache_batch_stride elements, start positions start_pos_dev[b].
+ * pages != NULL (bf16 only): paged caches, sequence b's table row b. */
 typedef struct am_gfx950_attention_args {
   const void* q;
   const void* k_cache;
@@ -205,6 +225,7 @@ typedef struct am_gfx950_attention_args {
   int32_t num_splits; /* 0 = choose */
   void* workspace;
   int64_t workspace_bytes;
+  const am_gfx950_kv_pages* pages; /* NULL: contiguous planes */
 } am_gfx950_attention_args;
 am_status_code am_gfx950_attention(const am_gfx950_attention_args* args, void* hip_stream);
 int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv,
@@ -360,7 +381,8 @@ am_status_code am_gfx950_fill(void* out, int32_t dtype, int64_t n, float value,
  * (device).  Rounds at every reference op boundary.
  * rows > 1 (up to 16, bf16 activations): one token of each of `rows` independent
  * sequences: h [rows][hidden], pos [rows], q_out [rows][hq*d], and sequence r's cache
- * planes start cache_batch_stride elements after sequence r-1's.  rows 0 means 1. */
+ * planes start cache_batch_stride elements after sequence r-1's.  rows 0 means 1.
+ * pages != NULL (bf16): paged caches, sequence r's table row r. */
 typedef struct am_gfx950_fused_qkv_args {
   const void* h;
   const void* norm_w;
@@ -376,6 +398,7 @@ typedef struct am_gfx950_fused_qkv_args {
   int32_t dtype;
   int64_t rows;
   int64_t cache_batch_stride;
+  const am_gfx950_kv_pages* pages; /* NULL: contiguous planes */
 } am_gfx950_fused_qkv_args;
 am_status_code am_gfx950_fused_qkv(const am_gfx950_fused_qkv_args* args, void* hip_stream);
 

@@ -157,6 +157,18 @@ typedef struct am_session_options {
                                 all layers (am_gfx950_decode_layers); session creation
                                 fails when the model does not qualify.  0 or -1: the
                                 per-op fused plan (default) */
+  int32_t kv_block_size;     /* 0: each sequence owns a contiguous KV slot of max_tokens
+                                positions (default).  > 0: paged KV (am_gfx950_kv_pages)
+                                with blocks of this many positions (a power of two, at
+                                least 32; bf16 activations, not with persistent_decode):
+                                a sequence holds blocks only for the positions it has
+                                reached, taken from one pool at prefill and as decode
+                                grows it, and returned when the row is prefilled again or
+                                the session ends */
+  int32_t kv_pool_blocks;    /* paged KV: blocks in the pool (0: enough for every
+                                sequence at max_tokens).  A prefill or decode that would
+                                need more returns AM_STATUS_RESOURCE_EXHAUSTED before any
+                                work is enqueued */
 } am_session_options;
 
 am_status_code am_session_open(am_model* m, const am_session_options* opt, am_session** out);

@@ -486,7 +486,43 @@ void TestPackedCacheHeader() {
   CHECK(P::Inspect(path).status().code() == StatusCode::kNotFound);
 }
 
+// Paged KV block manager (host/am_core.h): growth, exhaustion, release and reuse, the
+// table rows, and the pool addresses.
+void TestKVBlocks() {
+  KVBlockManager m(HostTestAllocator());
+  CHECK(m.Init(2, 8, 128, DataType::BFloat(16), 48, 10, 2, 1000).code() == StatusCode::kInvalidArgument);
+  CHECK(m.Init(2, 8, 128, DataType::BFloat(16), 64, 10, 3, 1000).ok());
+  CHECK(m.table_stride() == 16 && m.free_blocks() == 10 && m.dirty());
+  CHECK(m.pool_bytes() == size_t{2} * 2 * 10 * 8 * 64 * 128 * 2);
+  CHECK(static_cast<char*>(m.value_pool(0)) - static_cast<char*>(m.key_pool(0)) ==
+        static_cast<ptrdiff_t>(10 * 8 * 64 * 128 * 2));
+  CHECK(static_cast<char*>(m.key_pool(1)) - static_cast<char*>(m.key_pool(0)) ==
+        static_cast<ptrdiff_t>(2 * 10 * 8 * 64 * 128 * 2));
+  m.clear_dirty();
+  CHECK(m.EnsureCapacity(0, 100).ok());  // 2 blocks: ids 0, 1
+  CHECK(m.blocks_of(0) == 2 && m.free_blocks() == 8 && m.dirty());
+  CHECK(m.host_table()[0] == 0 && m.host_table()[1] == 1 && m.host_table()[2] == -1);
+  m.clear_dirty();
+  CHECK(m.EnsureCapacity(0, 128).ok() && !m.dirty());  // still 2 blocks
+  CHECK(m.EnsureCapacity(1, 65).ok());                 // ids 2, 3
+  CHECK(m.host_table()[16] == 2 && m.host_table()[17] == 3);
+  CHECK(m.EnsureCapacity(0, 129).ok() && m.host_table()[2] == 4);
+  // exhaustion changes nothing
+  CHECK(m.EnsureCapacity(2, 64 * 6).code() == StatusCode::kResourceExhausted);
+  CHECK(m.blocks_of(2) == 0 && m.free_blocks() == 5);
+  CHECK(m.EnsureCapacity(2, 1001).code() == StatusCode::kOutOfRange);
+  CHECK(m.EnsureCapacity(3, 1).code() == StatusCode::kOutOfRange);
+  // release returns blocks; the lowest free ids are reused first
+  CHECK(m.ReleaseSequence(0).ok());
+  CHECK(m.free_blocks() == 8 && m.blocks_of(0) == 0 && m.host_table()[0] == -1);
+  CHECK(m.EnsureCapacity(2, 64 * 3).ok());
+  CHECK(m.host_table()[32] == 0 && m.host_table()[33] == 1 && m.host_table()[34] == 4);
+  CHECK(m.EnsureCapacity(0, 64 * 5).ok() && m.free_blocks() == 0);
+  CHECK(m.EnsureCapacity(1, 64 * 3).code() == StatusCode::kResourceExhausted);
+}
+
 int main() {
+  TestKVBlocks();
   TestPackedCacheHeader();
   TestRegistry();
   TestKV();
