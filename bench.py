@@ -173,7 +173,7 @@ def run_long(args, N, L):
     m = N.vp()
     L.call("am_model_create_synthetic", rt, C.byref(mc), 1, C.byref(m))
     s = N.vp()
-    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, B)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, B, 0, args.kv_block, 0)), C.byref(s))
     prompts = []
     for r in range(B):
         pr = np.empty(P, np.int64)
@@ -245,6 +245,7 @@ def run_long(args, N, L):
         "data": "synthetic (seeded N(0,0.02) weights generated on device, seeded uniform prompt ids)",
         "config": {"workload": f"llama3-8b-shape-int4-g128, {B} sequences x {P} prompt ids prefilled in {CHUNK}-token "
                                f"chunks, batch-{B} greedy decode, {steps} timed steps, KV cache {CAP} bf16",
+                   "kv": f"paged, {args.kv_block}-position blocks" if args.kv_block else "contiguous slot per sequence",
                    "model": "llama3-8b-shape-int4-g128", "global_batch": B, "seq_len": P,
                    "parallelism": "none (1 GPU)", "prefill_s": round(prefill_s, 3),
                    "prefill_tokens_per_s": round(B * P / prefill_s, 1)},
@@ -274,6 +275,8 @@ def main():
                     help="int4 (the headline), int8, bf16, or long (configs[4]: batch-4 decode over 8192-token prompts)")
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--kv-block", type=int, default=0,
+                    help="paged KV with blocks of this many positions (0: one contiguous slot per sequence)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (PMC counter calibration)")
@@ -310,7 +313,7 @@ def main():
     log(f"model {cfgd['name']} created in {time.perf_counter() - t0:.1f}s; linear weight bytes/token "
         f"{L.am_model_weight_bytes_total(m)}")
     s = N.vp()
-    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1)), C.byref(s))
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, 1, 0, args.kv_block, 0)), C.byref(s))
 
     import numpy as np
     prompt = np.empty(args.prompt, np.int64)
@@ -394,7 +397,8 @@ def main():
         "config": {"workload": f"{cfgd['name']} batch-1 greedy decode, prompt {args.prompt}, "
                                f"{steps} timed decode tokens after {args.warmup} warmup, KV cache 4096 bf16",
                    "model": cfgd["name"], "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
-                   "prefill_ms": round(prefill_s * 1e3, 2), "kernels_per_token": plan_size},
+                   "prefill_ms": round(prefill_s * 1e3, 2), "kernels_per_token": plan_size,
+                   "kv": f"paged, {args.kv_block}-position blocks" if args.kv_block else "contiguous"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": pmc.get("hbm_bytes_per_token") if pmc else None,
