@@ -258,7 +258,14 @@ Status FusedLinearAddKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_fused_linear_residual(&a, StreamOf(ctx)));
 }
 
-// Prefill Linear -> Add on the MFMA GEMM: in: x; out: h (in/out residual)
+// Optional trailing input of the prefill GEMM ops: a u8 workspace [bytes] that lets the
+// INT4 GEMM split K (am_gfx950_gemm_workspace_bytes).
+void GemmWorkspace(const GfxParams* p, int index, void** ws, int64_t* bytes) {
+  *ws = p->nin > index ? p->in[index].p : nullptr;
+  *bytes = p->nin > index ? p->in[index].d[0] : 0;
+}
+
+// Prefill Linear -> Add on the MFMA GEMM: in: x (, workspace); out: h (in/out residual)
 Status PrefillLinearAddKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
   AM_RETURN_IF_ERROR(NeedArgs(p, 1, 1, "PrefillLinearAdd"));
@@ -272,12 +279,13 @@ Status PrefillLinearAddKernel(const KernelContext& ctx) noexcept {
   a.out_dtype = p->out[0].dt;
   a.residual = p->out[0].p;
   a.mode = 2;
+  GemmWorkspace(p, 1, &a.workspace, &a.workspace_bytes);
   if (p->out[0].d[1] != a.w.n || p->in[0].d[1] != a.w.k)
     return Status::InvalidArgument("PrefillLinearAdd: tensor shapes do not match the packed weight");
   return FromC(am_gfx950_linear(&a, StreamOf(ctx)));
 }
 
-// Prefill q|k|v: in: x; out: the row ranges of the weight, in order (2 or 3 outputs)
+// Prefill q|k|v: in: x (, workspace); out: the row ranges of the weight, in order (2 or 3 outputs)
 Status FusedLinearSplitKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
   if (p->nin < 1 || p->nout < 2 || p->nout > 3) return Status::InvalidArgument("FusedLinearSplit: needs 1 input, 2-3 outputs");
@@ -287,6 +295,7 @@ Status FusedLinearSplitKernel(const KernelContext& ctx) noexcept {
   a.m = p->in[0].d[0];
   a.w = *W(ctx);
   a.epilogue = AM_PREFILL_SPLIT;
+  GemmWorkspace(p, 1, &a.workspace, &a.workspace_bytes);
   int64_t col = 0;
   for (int i = 0; i < p->nout; ++i) {
     a.out[i] = p->out[i].p;
@@ -298,7 +307,7 @@ Status FusedLinearSplitKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));
 }
 
-// Prefill gate|up -> SiluMul: in: x; out: act [m][n/2]
+// Prefill gate|up -> SiluMul: in: x (, workspace); out: act [m][n/2]
 Status FusedLinearSiluMulKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
   AM_RETURN_IF_ERROR(NeedArgs(p, 1, 1, "FusedLinearSiluMul"));
@@ -309,6 +318,7 @@ Status FusedLinearSiluMulKernel(const KernelContext& ctx) noexcept {
   a.w = *W(ctx);
   a.epilogue = AM_PREFILL_SILU_MUL;
   a.out[0] = p->out[0].p;
+  GemmWorkspace(p, 1, &a.workspace, &a.workspace_bytes);
   if (2 * p->out[0].d[1] != a.w.n || p->in[0].d[1] != a.w.k)
     return Status::InvalidArgument("FusedLinearSiluMul: tensor shapes do not match the packed weight");
   return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));

@@ -588,6 +588,8 @@ class LlamaSession {
   int32_t* err = nullptr;
   void* attn_ws = nullptr;
   size_t attn_ws_bytes = 0;
+  void* gemm_ws = nullptr;  // split-K workspace of the prefill INT4 GEMMs
+  size_t gemm_ws_bytes = 0;
   void* lm_ws = nullptr;
   void* am_ws = nullptr;
   int64_t am_ws_bytes = 0;
@@ -727,6 +729,11 @@ class LlamaSession {
         am_gfx950_attention_workspace_bytes(1, S, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0),
         am_gfx950_attention_workspace_bytes(B, 1, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0)));
     am_ws_bytes = am_gfx950_argmax_workspace_bytes(1);
+    if (c.weight_format == AM_WF_INT4) {
+      const int64_t g = c.group_size;
+      for (auto nk : {std::pair<int64_t, int64_t>{m->QRows() + 2 * m->KvRows(), H}, {H, m->QRows()}, {2 * F, H}, {H, F}})
+        gemm_ws_bytes = std::max(gemm_ws_bytes, static_cast<size_t>(am_gfx950_gemm_workspace_bytes(S, nk.first, nk.second, g)));
+    }
     const size_t sizes[] = {
         static_cast<size_t>(S) * 8,                   // ids
         static_cast<size_t>(S) * 8,                   // positions
@@ -746,14 +753,16 @@ class LlamaSession {
         64,                                           // err
         attn_ws_bytes,                                // attention workspace
         static_cast<size_t>(am_gfx950_lm_head_workspace_bytes()),
-        static_cast<size_t>(am_ws_bytes)};
+        static_cast<size_t>(am_ws_bytes),
+        gemm_ws_bytes};                               // prefill GEMM split-K workspace
+    constexpr int kParts = static_cast<int>(sizeof(sizes) / sizeof(sizes[0]));
     size_t total = 0;
     for (size_t s : sizes) total += (s + 255) & ~size_t{255};
     AM_HIP_OK(hipMalloc(&act_slab, total));
     AM_HIP_OK(hipMemsetAsync(act_slab, 0, total, stream));
     Slab sl{act_slab, total, 0};
-    void* ptrs[19];
-    for (int i = 0; i < 19; ++i) ptrs[i] = sl.Take(sizes[i]);
+    void* ptrs[kParts];
+    for (int i = 0; i < kParts; ++i) ptrs[i] = sl.Take(sizes[i]);
     ids = static_cast<int64_t*>(ptrs[0]);
     positions = static_cast<int64_t*>(ptrs[1]);
     h = ptrs[2];
@@ -773,6 +782,7 @@ class LlamaSession {
     attn_ws = ptrs[16];
     lm_ws = ptrs[17];
     am_ws = ptrs[18];
+    gemm_ws = gemm_ws_bytes ? ptrs[19] : nullptr;
     decode_bind.SetStream(hs.get());
     decode_bind.SetWorkspace(attn_ws, attn_ws_bytes);
     AM_HIP_OK(hipStreamSynchronize(stream));
@@ -907,8 +917,14 @@ class LlamaSession {
                       c.group_size % 64 == 0 && c.ffn % 64 == 0;
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
                              {hv, TensorView(m->in_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
+    // the prefill GEMMs' inputs, with the split-K workspace when the session has one
+    auto gemm_in = [&](TensorView x) {
+      std::vector<TensorView> v{x};
+      if (gemm_ws != nullptr) v.push_back(TensorView(gemm_ws, DataType::UInt(8), {static_cast<int64_t>(gemm_ws_bytes)}));
+      return v;
+    };
     if (fuse) {
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSplit, {}, Sel(true, ph), &m->qkv[l], {xnv},
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSplit, {}, Sel(true, ph), &m->qkv[l], gemm_in(xnv),
                                {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV}),
                                 MutableTensorView(v, A, {S, KV})}));
     } else {
@@ -935,7 +951,7 @@ class LlamaSession {
                              {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},
                              {MutableTensorView(attn, A, {S, Q})}, attn_ws_bytes));
     if (fuse) {
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->o[l], gemm_in(TensorView(attn, A, {S, Q})),
                                {MutableTensorView(h, A, {S, H})}));
     } else {
       AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &m->o[l], {TensorView(attn, A, {S, Q})},
@@ -946,10 +962,10 @@ class LlamaSession {
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
                              {hv, TensorView(m->post_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
     if (fuse) {
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSiluMul, {}, Sel(true, ph), &m->gate_up[l], {xnv},
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSiluMul, {}, Sel(true, ph), &m->gate_up[l], gemm_in(xnv),
                                {MutableTensorView(act, A, {S, F})}));
-      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l], {TensorView(act, A, {S, F})},
-                               {MutableTensorView(h, A, {S, H})}));
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearAdd, {}, Sel(true, ph), &m->down[l],
+                               gemm_in(TensorView(act, A, {S, F})), {MutableTensorView(h, A, {S, H})}));
       return Status::Ok();
     }
     AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.gate, {xnv}, {MutableTensorView(gate, A, {S, F})}));

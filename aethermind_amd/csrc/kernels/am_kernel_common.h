@@ -67,9 +67,12 @@ am_status_code BatchNormLogits(const am_gfx950_fused_lm_head_args* a, hipStream_
 
 // Prefill INT4 GEMM (gemm_i4.hip): epilogue 0 store, 1 residual, 2 column split into
 // out0|out1|out2 at columns c1, c2, 3 SiLU-Mul of the gate|up halves into out0.
+// ws (optional, tickets zero, left zero) lets shapes with few tiles split K.
 bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x);
+int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group);
 am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
-                      void* out2, int64_t c1, int64_t c2, const void* residual, hipStream_t s);
+                      void* out2, int64_t c1, int64_t c2, const void* residual, void* ws, int64_t ws_bytes,
+                      hipStream_t s);
 
 // ---- device: numeric helpers ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }

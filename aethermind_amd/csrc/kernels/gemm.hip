@@ -329,6 +329,10 @@ am_status_code ValidateLinearWeight(const am_gfx950_weight& w) {
 }
 }  // namespace
 
+extern "C" int64_t am_gfx950_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t group_size) {
+  return GemmI4WorkspaceBytes(m, n, k, group_size);
+}
+
 extern "C" am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* a, void* stream) {
   AM_CHECK_ARG(a != nullptr, "prefill_linear: null args");
   if (auto st = ValidateLinearWeight(a->w); st != AM_STATUS_OK) return st;
@@ -339,9 +343,10 @@ extern "C" am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linea
   switch (a->epilogue) {
     case AM_PREFILL_SPLIT:
       return GemmI4(a->x, a->m, a->w, 2, a->out[0], a->out[1], a->out[2], a->split[0], a->split[1], nullptr,
-                    AsStream(stream));
+                    a->workspace, a->workspace_bytes, AsStream(stream));
     case AM_PREFILL_SILU_MUL:
-      return GemmI4(a->x, a->m, a->w, 3, a->out[0], nullptr, nullptr, 0, 0, nullptr, AsStream(stream));
+      return GemmI4(a->x, a->m, a->w, 3, a->out[0], nullptr, nullptr, 0, 0, nullptr, a->workspace, a->workspace_bytes,
+                    AsStream(stream));
     default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "prefill_linear: unknown epilogue");
   }
 }
@@ -363,7 +368,8 @@ extern "C" am_status_code am_gfx950_linear(const am_gfx950_linear_args* a, void*
     return BatchLinear(a->x, a->m, w, a->out, a->out_dtype, a->residual, s);
   const bool use_gemm = a->mode == 2 || (a->mode == 0 && a->m > 8 && gemm_ok);
   if (use_gemm && a->out_dtype == AM_DT_BF16 && GemmI4Eligible(w, a->m, a->x))
-    return GemmI4(a->x, a->m, w, a->residual != nullptr ? 1 : 0, a->out, nullptr, nullptr, 0, 0, a->residual, s);
+    return GemmI4(a->x, a->m, w, a->residual != nullptr ? 1 : 0, a->out, nullptr, nullptr, 0, 0, a->residual,
+                  a->workspace, a->workspace_bytes, s);
   if (use_gemm) {
     AM_CHECK_ARG(gemm_ok, "linear: MFMA GEMM needs bf16 activations, bf16/int8/int4 weights, K % 128 == 0");
     if (w.format >= AM_WF_INT8) AM_CHECK_ARG(w.scales != nullptr, "linear: quantized weight needs scales");

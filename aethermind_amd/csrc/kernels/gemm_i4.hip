@@ -20,11 +20,25 @@
 //     output tiles.  Each group's sum is scaled by its fp16 scale when the group (two k
 //     steps) completes.  Products are exact and accumulation is fp32.
 //   * Rows past the M or N edge read row 0 and are never stored.
+//   * The k loop runs one INT4 group per iteration: the group's first MFMAs start from
+//     a zero accumulator, so closing a group is one fma per output and no clearing.
+//   * Split-K (tiles that would leave CUs idle): split s of a tile owns a contiguous
+//     range of whole groups.  Each split block stores its fp32 accumulators with
+//     device-scope stores, waits for them, and takes a ticket; the last block of the
+//     tile reads the other partials back with device-scope loads and sums all of them
+//     in split order (the same order whichever block is last, so results do not depend
+//     on scheduling), resets the ticket and runs the epilogue.
 //   * Epilogues (the op boundaries of the reference graph, model_graph_builder.cpp:
-//     133-290): store; residual (out = round(res + round(acc)), Linear then Add);
-//     column split (one q|k|v weight, three outputs); SiLU-Mul (the block's waves
-//     wn = 0 hold gate columns u, its waves wn = 1 the up columns F + u of the same u;
-//     act = round(silu(round(gate)) * round(up)), exchanged through LDS).
+//     133-290) go through LDS: the block writes round(acc) as a bf16 tile, then every
+//     thread moves 16-byte row chunks (one load of residual, one store per chunk).
+//     Store; residual (out = round(res + round(acc)), Linear then Add); column split
+//     (one q|k|v weight, three outputs); SiLU-Mul (tile columns [0, BN/2) are gate
+//     features u, [BN/2, BN) the up rows of the same u: act = round(silu(round(gate))
+//     * round(up))).  Chunks that cross the N edge or a split column, or outputs whose
+//     rows are not 16-byte aligned, take the per-element path.
+
+#include <algorithm>
+#include <type_traits>
 
 #include "am_gemv_common.h"
 #include "am_launch_timing.h"
@@ -75,6 +89,10 @@ struct I4Args {
   uint16_t* out2;
   int32_t c1, c2;             // split: columns [0,c1) -> out0, [c1,c2) -> out1, [c2,N) -> out2
   const uint16_t* residual;   // [M][N] bf16, may alias out0
+  int32_t vec;                // 1: 16-byte output chunks (row strides and split columns % 8 == 0, aligned)
+  int32_t splits;             // k splits per tile (1: none)
+  float* part;                // [tiles][splits][waves][16][64] x 4 fp32 partial accumulators
+  unsigned* tickets;          // [tiles], zero between launches
 };
 
 __device__ __forceinline__ bf16x8_t unpack8(uint32_t word, uint32_t mask, uint32_t magic) {
@@ -125,7 +143,9 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   // tile mapping: bands of 8 M-tiles, N fastest inside a band
   const int32_t tiles_m = (p.M + QBM - 1) / QBM;
   const int32_t tiles_n = EPI == kI4SiluMul ? p.ffn / (BN / 2) : (p.N + BN - 1) / BN;
-  const int32_t bid = blockIdx.x;
+  const int32_t tiles = tiles_m * tiles_n;
+  const int32_t split = blockIdx.x / tiles;
+  const int32_t bid = blockIdx.x - split * tiles;
   const int32_t per_band = 8 * tiles_n;
   const int32_t b0 = bid / per_band, rem = bid - b0 * per_band;
   const int32_t bands_m = min(tiles_m - b0 * 8, 8);
@@ -133,8 +153,10 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   const int32_t m0 = tm * QBM;
 
   const int32_t ng = p.K / p.group;
-  const int32_t nk = p.K / QBK;
   const int32_t spg = p.group / QBK;  // k steps per group
+  // this split's groups [g0, g1) = k steps [k0, k0 + nk)
+  const int32_t g0 = split * ng / p.splits, g1 = (split + 1) * ng / p.splits;
+  const int32_t k0 = g0 * spg, nk = (g1 - g0) * spg;
 
   // ---- DMA sources of this lane ----
   // X: wave w moves rows [8 kXi w, 8 kXi (w + 1)), 8 rows per instruction
@@ -155,8 +177,9 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   const int sr = (wave % NWN) * 64 + lane;
   const int64_t sbase = static_cast<int64_t>(wrow<EPI, BN>(p, tn, sr)) * ng;
 
-  auto issue = [&](int32_t ks) {
-    uint8_t* st = lds + (ks % NST) * STG;
+  auto issue = [&](int32_t j) {  // local step j = k step k0 + j
+    const int32_t ks = k0 + j;
+    uint8_t* st = lds + (j % NST) * STG;
 #pragma unroll
     for (int i = 0; i < S::kXi; ++i) dma16(xsrc[i] + ks * (QBK * 2), st + (wave * S::kXi + i) * 1024);
     dma16(wsrc + ks * (QBK / 2), st + XST + wave * 1024);
@@ -209,13 +232,16 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   for (int i = 0; i < NST - 1; ++i)
     if (i < nk) issue(i);
 
-  for (int32_t ks = 0; ks < nk; ++ks) {
-    // this wave's DMA for step ks has landed (younger steps may still be in flight);
-    // after the barrier every wave's has, and step ks-1 is no longer read
+  const f32x4_t zero4 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // one k step: FIRST starts the group's partial sums from zero
+  auto step = [&](int32_t j, auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+    // this wave's DMA for step j has landed (younger steps may still be in flight);
+    // after the barrier every wave's has, and step j-1 is no longer read
     static_assert(NST <= 4, "wait_barrier keeps at most two younger steps in flight");
-    wait_barrier<S::kLoads>(min(nk - 1 - ks, NST - 2));
-    if (ks + NST - 1 < nk) issue(ks + NST - 1);
-    const uint8_t* st = lds + (ks % NST) * STG;
+    wait_barrier<S::kLoads>(min(nk - 1 - j, NST - 2));
+    if (j + NST - 1 < nk) issue(j + NST - 1);
+    const uint8_t* st = lds + (j % NST) * STG;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       bf16x8_t af[4], bfr[4];
@@ -226,111 +252,241 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
         bfr[nt] = unpack8(*reinterpret_cast<const uint32_t*>(st + boff[nt][kk]), mask, magic);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        corr[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bneg, corr[mt], 0, 0, 0);
+        corr[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bneg, (FIRST && kk == 0) ? zero4 : corr[mt], 0, 0, 0);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)
-          part[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], part[mt][nt], 0, 0, 0);
+          part[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], (FIRST && kk == 0) ? zero4 : part[mt][nt],
+                                                                 0, 0, 0);
       }
     }
-    if ((ks + 1) % spg == 0) {  // the group closes: scale and fold into acc
-      const int32_t g = ks / spg;
+  };
+  int32_t j = 0;
+  for (int32_t g = g0; g < g1; ++g) {
+    step(j++, std::true_type{});
+    for (int32_t t = 1; t < spg; ++t) step(j++, std::false_type{});
+    // the group closes: scale and fold into acc
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + soff[nt] + (g & 3) * S::kScSlot);
-        const uint32_t bits = ((shalf_base[nt] + g) & 1) ? (sw >> 16) : (sw & 0xFFFFu);
-        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+    for (int nt = 0; nt < 4; ++nt) {
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + soff[nt] + (g & 3) * S::kScSlot);
+      const uint32_t bits = ((shalf_base[nt] + g) & 1) ? (sw >> 16) : (sw & 0xFFFFu);
+      const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(sc, part[mt][nt][r] + corr[mt][r], acc[mt][nt][r]);
-          part[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) corr[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(sc, part[mt][nt][r] + corr[mt][r], acc[mt][nt][r]);
     }
   }
+
+  if (p.splits > 1) {
+    // partial of this split: device-scope stores, acknowledged before the ticket
+    float* mine = p.part + ((static_cast<int64_t>(bid) * p.splits + split) * S::kWaves + wave) * (16 * 64 * 4);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const f32x4_t v = acc[i / 4][i % 4];
+      uint64_t* d = reinterpret_cast<uint64_t*>(mine + (i * 64 + lane) * 4);
+      __hip_atomic_store(d, (static_cast<uint64_t>(__float_as_uint(v[1])) << 32) | __float_as_uint(v[0]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(d + 1, (static_cast<uint64_t>(__float_as_uint(v[3])) << 32) | __float_as_uint(v[2]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ unsigned last;
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(&p.tickets[bid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             static_cast<unsigned>(p.splits - 1);
+    __syncthreads();
+    if (!last) return;
+    // the tile's sum in split order
+    f32x4_t sum[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum[i] = zero4;
+    for (int sp = 0; sp < p.splits; ++sp) {
+      if (sp == split) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum[i] += acc[i / 4][i % 4];
+        continue;
+      }
+      const float* src = p.part + ((static_cast<int64_t>(bid) * p.splits + sp) * S::kWaves + wave) * (16 * 64 * 4);
+      uint64_t v[32];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint64_t* d = reinterpret_cast<const uint64_t*>(src + (i * 64 + lane) * 4);
+        v[2 * i] = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[2 * i + 1] = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        sum[i] += f32x4_t{__uint_as_float(static_cast<uint32_t>(v[2 * i])), __uint_as_float(static_cast<uint32_t>(v[2 * i] >> 32)),
+                          __uint_as_float(static_cast<uint32_t>(v[2 * i + 1])),
+                          __uint_as_float(static_cast<uint32_t>(v[2 * i + 1] >> 32))};
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i / 4][i % 4] = sum[i];
+    if (tid == 0) __hip_atomic_store(&p.tickets[bid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // ---- epilogue: round(acc) as a bf16 tile in LDS (lane holds D[4*(lane/16)+r][lane%16]
+  // of each 16x16 tile), then 16-byte row chunks ----
+  constexpr int TS = BN + 8;  // tile row stride in bf16 (16-byte pad)
+  uint16_t* T = reinterpret_cast<uint16_t*>(lds);
+  __syncthreads();  // every wave is done with the ring
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        T[(wm * 64 + mt * 16 + 4 * (lane >> 4) + r) * TS + wn * 64 + nt * 16 + (lane & 15)] =
+            f32_to_bf16_bits(acc[mt][nt][r]);
   __syncthreads();
 
-  // ---- epilogue: lane holds D[4*(lane/16)+r][lane%16] of each 16x16 tile ----
   if constexpr (EPI == kI4SiluMul) {
-    // the up waves (wn >= NWN/2) hand round(up) to the gate waves wn - NWN/2 through LDS
-    constexpr int HN = NWN / 2;
-    float* ex = reinterpret_cast<float*>(lds) + (wm * HN + wn % HN) * 64 * 64;
-    if (wn >= HN) {
+    constexpr int CPR = BN / 16;  // 16-byte output chunks per row (BN/2 features)
+    constexpr int IT = QBM * CPR / S::kThreads;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+    for (int i = 0; i < IT; ++i) {
+      const int c = tid + S::kThreads * i, row = c / CPR, cc = c % CPR;
+      const int32_t gm = m0 + row;
+      if (gm >= p.M) continue;
+      const uint16_t* gt = T + row * TS + cc * 8;
+      const uint16_t* ut = gt + BN / 2;
+      uint16_t* o = p.out0 + static_cast<int64_t>(gm) * p.ffn + tn * (BN / 2) + cc * 8;
+      if (p.vec) {
+        const uint4 gv = *reinterpret_cast<const uint4*>(gt), uv = *reinterpret_cast<const uint4*>(ut);
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+        uint32_t ow[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+        for (int q = 0; q < 4; ++q)
+          ow[q] = f32_to_bf16_bits(silu_ref(bf16_bits_to_f32(gw[q] & 0xFFFFu)) * bf16_bits_to_f32(uw[q] & 0xFFFFu)) |
+                  (static_cast<uint32_t>(
+                       f32_to_bf16_bits(silu_ref(bf16_bits_to_f32(gw[q] >> 16)) * bf16_bits_to_f32(uw[q] >> 16)))
+                   << 16);
+        *reinterpret_cast<uint4*>(o) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            ex[(mt * 16 + 4 * (lane >> 4) + r) * 64 + nt * 16 + (lane & 15)] =
-                bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][nt][r]));
-    }
-    __syncthreads();
-    if (wn < HN) {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int32_t gm = m0 + wm * 64 + mt * 16 + 4 * (lane >> 4) + r;
-          if (gm >= p.M) continue;
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) {
-            const int col = nt * 16 + (lane & 15);
-            const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][nt][r]));
-            const float u = ex[(mt * 16 + 4 * (lane >> 4) + r) * 64 + col];
-            p.out0[static_cast<int64_t>(gm) * p.ffn + tn * (BN / 2) + wn * 64 + col] = f32_to_bf16_bits(silu_ref(g) * u);
-          }
-        }
+        for (int e = 0; e < 8; ++e) o[e] = f32_to_bf16_bits(silu_ref(bf16_bits_to_f32(gt[e])) * bf16_bits_to_f32(ut[e]));
+      }
     }
     return;
   }
+
+  constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+  constexpr int IT = QBM * CPR / S::kThreads;
+  // residual chunks first, all loads in flight (each thread reads only the chunks it
+  // writes, so an aliased residual is read before it is overwritten)
+  uint4 rres[EPI == kI4Residual ? IT : 1];
+  if constexpr (EPI == kI4Residual) {
+    if (p.vec) {
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int32_t gn = tn * BN + wn * 64 + nt * 16 + (lane & 15);
-    if (gn >= p.N) continue;
+      for (int i = 0; i < IT; ++i) {
+        const int c = tid + S::kThreads * i, row = c / CPR, cc = c % CPR;
+        const int32_t gm = m0 + row, gn = tn * BN + cc * 8;
+        const int64_t idx = (gm < p.M && gn + 8 <= p.N) ? static_cast<int64_t>(gm) * p.N + gn : 0;
+        rres[i] = *reinterpret_cast<const uint4*>(p.residual + idx);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = tid + S::kThreads * i, row = c / CPR, cc = c % CPR;
+    const int32_t gm = m0 + row, gn = tn * BN + cc * 8;
+    if (gm >= p.M || gn >= p.N) continue;
+    const uint16_t* t = T + row * TS + cc * 8;
+    // destination of column gn (split: the output whose column range holds it)
     uint16_t* o = p.out0;
-    int32_t col = gn, ld = p.N;
+    int32_t col = gn, ld = p.N, lim = p.N;  // lim: end of the destination's columns
     if constexpr (EPI == kI4Split) {
       if (gn < p.c1) {
-        ld = p.c1;
+        ld = lim = p.c1;
       } else if (gn < p.c2) {
         o = p.out1;
         col = gn - p.c1;
         ld = p.c2 - p.c1;
+        lim = p.c2;
       } else {
         o = p.out2;
         col = gn - p.c2;
         ld = p.N - p.c2;
       }
     }
+    uint16_t* dst = o + static_cast<int64_t>(gm) * ld + col;
+    if (p.vec && gn + 8 <= lim) {
+      const uint4 tv = *reinterpret_cast<const uint4*>(t);
+      uint4 ov = tv;
+      if constexpr (EPI == kI4Residual) {
+        const uint32_t tw[4] = {tv.x, tv.y, tv.z, tv.w}, rw[4] = {rres[i].x, rres[i].y, rres[i].z, rres[i].w};
+        uint32_t ow[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int32_t gm = m0 + wm * 64 + mt * 16 + 4 * (lane >> 4) + r;
-        if (gm >= p.M) continue;
-        const int64_t idx = static_cast<int64_t>(gm) * ld + col;
-        float v = acc[mt][nt][r];
-        if constexpr (EPI == kI4Residual) v = bf16_bits_to_f32(p.residual[idx]) + bf16_bits_to_f32(f32_to_bf16_bits(v));
-        o[idx] = f32_to_bf16_bits(v);
+        for (int q = 0; q < 4; ++q)
+          ow[q] = f32_to_bf16_bits(bf16_bits_to_f32(rw[q] & 0xFFFFu) + bf16_bits_to_f32(tw[q] & 0xFFFFu)) |
+                  (static_cast<uint32_t>(f32_to_bf16_bits(bf16_bits_to_f32(rw[q] >> 16) + bf16_bits_to_f32(tw[q] >> 16)))
+                   << 16);
+        ov = make_uint4(ow[0], ow[1], ow[2], ow[3]);
       }
+      *reinterpret_cast<uint4*>(dst) = ov;
+    } else {
+      // per element: the N edge, a chunk that straddles split outputs, unaligned rows
+      for (int e = 0; e < 8 && gn + e < p.N; ++e) {
+        int32_t ge = gn + e;
+        uint16_t* de = p.out0 + static_cast<int64_t>(gm) * p.N + ge;
+        if constexpr (EPI == kI4Split) {
+          if (ge < p.c1) de = p.out0 + static_cast<int64_t>(gm) * p.c1 + ge;
+          else if (ge < p.c2) de = p.out1 + static_cast<int64_t>(gm) * (p.c2 - p.c1) + (ge - p.c1);
+          else de = p.out2 + static_cast<int64_t>(gm) * (p.N - p.c2) + (ge - p.c2);
+        }
+        uint16_t v = t[e];
+        if constexpr (EPI == kI4Residual)
+          v = f32_to_bf16_bits(bf16_bits_to_f32(p.residual[static_cast<int64_t>(gm) * p.N + ge]) + bf16_bits_to_f32(v));
+        *de = v;
+      }
+    }
   }
 }
 
+// Tiles of a launch with NWN waves along N.
 template <int EPI, int NWN>
-am_status_code LaunchI4(const I4Args& p, hipStream_t s) {
+int64_t TilesOf(const I4Args& p) {
+  const int64_t tiles_m = CeilDiv(p.M, QBM);
+  return tiles_m * (EPI == kI4SiluMul ? p.ffn / (Shape<NWN>::kBN / 2) : CeilDiv(p.N, Shape<NWN>::kBN));
+}
+
+// Split-K count: the largest power of two <= 4 that still gives every CU at most one
+// block with >= 8 groups per split; long rows (>= 24 groups per split) may take two
+// blocks per CU.  The loop's per-CU rate is nearly the same with one block per CU as
+// with two, so splits pay when tiles alone leave CUs idle, and the partial merge
+// (~9 us) must be amortised.
+int SplitsFor(int64_t tiles, int64_t groups, int64_t cus) {
+  int s = 1;
+  while (s < 4 && tiles * s * 2 <= cus && groups / (s * 2) >= 8) s *= 2;
+  if (s < 4 && tiles * s * 2 <= 2 * cus && groups / (s * 2) >= 24) s *= 2;
+  return s;
+}
+
+// Workspace layout: tickets (one u32 per tile, 256-byte rounded), then the partials.
+int64_t TicketBytes(int64_t tiles) { return 256 * CeilDiv(tiles * 4, 256); }
+template <int NWN>
+int64_t PartialBytes(int64_t tiles, int splits) {
+  return splits > 1 ? tiles * splits * Shape<NWN>::kWaves * (16 * 64 * 16) : 0;
+}
+
+template <int EPI, int NWN>
+am_status_code LaunchI4(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
   using S = Shape<NWN>;
   static const bool lds_ok =
       hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i4_kernel<EPI, NWN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds) == hipSuccess;
   if (!lds_ok) return SetLastError(AM_STATUS_INTERNAL, "gemm_i4: could not set the dynamic LDS size");
-  const int64_t tiles_m = CeilDiv(p.M, QBM);
-  const int64_t tiles_n = EPI == kI4SiluMul ? p.ffn / (S::kBN / 2) : CeilDiv(p.N, S::kBN);
-  const int64_t blocks = tiles_m * tiles_n;
+  const int64_t tiles = TilesOf<EPI, NWN>(p);
+  int splits = ws != nullptr ? SplitsFor(tiles, p.K / p.group, DeviceCUs()) : 1;
+  if (splits > 1 && TicketBytes(tiles) + PartialBytes<NWN>(tiles, splits) > ws_bytes) splits = 1;
+  p.splits = splits;
+  if (splits > 1) {
+    p.tickets = static_cast<unsigned*>(ws);
+    p.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + TicketBytes(tiles));
+  }
+  const int64_t blocks = tiles * splits;
   static const char* const names[] = {"store", "residual", "split", "silu_mul"};
-  RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_i4<%s,bn=%d>", names[EPI], S::kBN);
+  RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_i4<%s,bn=%d,splits=%d>", names[EPI], S::kBN, splits);
   hipLaunchKernelGGL((gemm_i4_kernel<EPI, NWN>), dim3(static_cast<unsigned>(blocks)), dim3(S::kThreads), S::kLds, s, p);
   AM_RETURN_IF_LAUNCH_FAILED("gemm_i4");
   return AM_STATUS_OK;
@@ -338,12 +494,18 @@ am_status_code LaunchI4(const I4Args& p, hipStream_t s) {
 
 // Tile width per shape: the 256-wide tile when it still gives every CU a block.
 template <int EPI>
-am_status_code LaunchI4Any(const I4Args& p, hipStream_t s) {
+bool WideI4(const I4Args& p) {
   const int64_t tiles_m = CeilDiv(p.M, QBM);
   const int64_t cols = EPI == kI4SiluMul ? 2 * static_cast<int64_t>(p.ffn) : p.N;
-  const bool wide = (EPI != kI4SiluMul || p.ffn % 128 == 0) && tiles_m * CeilDiv(cols, 256) >= DeviceCUs();
-  return wide ? LaunchI4<EPI, 4>(p, s) : LaunchI4<EPI, 2>(p, s);
+  return (EPI != kI4SiluMul || p.ffn % 128 == 0) && tiles_m * CeilDiv(cols, 256) >= DeviceCUs();
 }
+
+template <int EPI>
+am_status_code LaunchI4Any(const I4Args& p, void* ws, int64_t ws_bytes, hipStream_t s) {
+  return WideI4<EPI>(p) ? LaunchI4<EPI, 4>(p, ws, ws_bytes, s) : LaunchI4<EPI, 2>(p, ws, ws_bytes, s);
+}
+
+bool Aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 }  // namespace
 
@@ -354,9 +516,26 @@ bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x) {
          m * w.n < (int64_t{1} << 31) && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
+// Workspace that lets the launch of this shape split K (0: it never splits).  The same
+// bound serves every epilogue (the SiLU-Mul tiles are never more numerous).
+int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group) {
+  if (m <= 0 || n <= 0 || k <= 0 || group <= 0 || k % group != 0) return 0;
+  const int64_t cus = DeviceCUs();
+  int64_t best = 0;
+  for (int nwn : {2, 4}) {
+    const int64_t tiles = CeilDiv(m, QBM) * CeilDiv(n, 64 * nwn);
+    const int sp = SplitsFor(tiles, k / group, cus);
+    if (sp > 1)
+      best = std::max(best, TicketBytes(tiles) + (nwn == 2 ? PartialBytes<2>(tiles, sp) : PartialBytes<4>(tiles, sp)));
+  }
+  return best;
+}
+
 am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
-                      void* out2, int64_t c1, int64_t c2, const void* residual, hipStream_t s) {
+                      void* out2, int64_t c1, int64_t c2, const void* residual, void* ws, int64_t ws_bytes,
+                      hipStream_t s) {
   if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unsupported shape or weight");
+  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm_i4: workspace must be 16-byte aligned");
   I4Args p{};
   p.x = static_cast<const uint16_t*>(x);
   p.w = static_cast<const uint8_t*>(w.data);
@@ -371,19 +550,32 @@ am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32
   p.c1 = static_cast<int32_t>(c1);
   p.c2 = static_cast<int32_t>(c2);
   p.residual = static_cast<const uint16_t*>(residual);
+  p.splits = 1;
+  // 16-byte chunks need every output row (and the residual's) to start 16-byte aligned
+  bool vec = Aligned16(out0) && (!residual || Aligned16(residual));
   switch (epi) {
-    case kI4Store: return LaunchI4Any<kI4Store>(p, s);
+    case kI4Store: vec = vec && w.n % 8 == 0; break;
+    case kI4Residual: vec = vec && w.n % 8 == 0; break;
+    case kI4Split:
+      vec = vec && c1 % 8 == 0 && c2 % 8 == 0 && w.n % 8 == 0 && (c2 == c1 || Aligned16(out1)) &&
+            (c2 == w.n || Aligned16(out2));
+      break;
+    default: vec = vec && (w.n / 2) % 8 == 0; break;
+  }
+  p.vec = vec ? 1 : 0;
+  switch (epi) {
+    case kI4Store: return LaunchI4Any<kI4Store>(p, ws, ws_bytes, s);
     case kI4Residual:
       AM_CHECK_ARG(residual != nullptr, "gemm_i4: residual epilogue without a residual");
-      return LaunchI4Any<kI4Residual>(p, s);
+      return LaunchI4Any<kI4Residual>(p, ws, ws_bytes, s);
     case kI4Split:
       AM_CHECK_ARG(0 < c1 && c1 <= c2 && c2 <= w.n && out0 && (c2 == c1 || out1) && (c2 == w.n || out2),
                    "gemm_i4: bad column split");
-      return LaunchI4Any<kI4Split>(p, s);
+      return LaunchI4Any<kI4Split>(p, ws, ws_bytes, s);
     case kI4SiluMul:
       AM_CHECK_ARG(w.n % 128 == 0, "gemm_i4: SiLU-Mul needs 2*ffn rows with ffn a multiple of 64");
       p.ffn = static_cast<int32_t>(w.n / 2);
-      return LaunchI4Any<kI4SiluMul>(p, s);
+      return LaunchI4Any<kI4SiluMul>(p, ws, ws_bytes, s);
     default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unknown epilogue");
   }
 }

@@ -46,11 +46,12 @@ class RmsNormArgs(C.Structure):
 
 class LinearArgs(C.Structure):
     _fields_ = [("x", vp), ("x_dtype", i32), ("m", i64), ("w", Weight), ("out", vp), ("out_dtype", i32),
-                ("residual", vp), ("mode", i32)]
+                ("residual", vp), ("mode", i32), ("workspace", vp), ("workspace_bytes", i64)]
 
 
 class PrefillLinearArgs(C.Structure):
-    _fields_ = [("x", vp), ("m", i64), ("w", Weight), ("epilogue", i32), ("out", vp * 3), ("split", i64 * 2)]
+    _fields_ = [("x", vp), ("m", i64), ("w", Weight), ("epilogue", i32), ("out", vp * 3), ("split", i64 * 2),
+                ("workspace", vp), ("workspace_bytes", i64)]
 
 
 class RopeArgs(C.Structure):
@@ -190,6 +191,7 @@ _SIGS = {
     "am_gfx950_rmsnorm": (i32, [C.POINTER(RmsNormArgs), vp]),
     "am_gfx950_linear": (i32, [C.POINTER(LinearArgs), vp]),
     "am_gfx950_prefill_linear": (i32, [C.POINTER(PrefillLinearArgs), vp]),
+    "am_gfx950_gemm_workspace_bytes": (i64, [i64, i64, i64, i64]),
     "am_gfx950_rope": (i32, [C.POINTER(RopeArgs), vp]),
     "am_gfx950_rope_table": (i32, [i64, i64, f64, vp, vp]),
     "am_gfx950_kv_update": (i32, [C.POINTER(KvUpdateArgs), vp]),

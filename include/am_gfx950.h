@@ -114,6 +114,10 @@ typedef struct am_gfx950_linear_args {
   int32_t out_dtype;
   const void* residual; /* optional, out_dtype */
   int32_t mode;
+  void* workspace;      /* optional (NULL): am_gfx950_gemm_workspace_bytes(m, n, k, group) bytes,
+                           16-byte aligned, zero before the first call (left zero); lets the
+                           INT4 MFMA GEMM split K when its tiles alone leave CUs idle */
+  int64_t workspace_bytes;
 } am_gfx950_linear_args;
 am_status_code am_gfx950_linear(const am_gfx950_linear_args* args, void* hip_stream);
 
@@ -138,8 +142,18 @@ typedef struct am_gfx950_prefill_linear_args {
   int32_t epilogue;
   void* out[3];
   int64_t split[2];
+  void* workspace;      /* optional, as in am_gfx950_linear_args */
+  int64_t workspace_bytes;
 } am_gfx950_prefill_linear_args;
 am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* args, void* hip_stream);
+
+/* Workspace bytes with which the INT4 prefill GEMM of an m x n x k product (INT4
+ * group size group_size) may split K: split s of an output tile sums a contiguous
+ * range of whole groups, and the tile's last split block adds the fp32 partials in
+ * split order (results are independent of block scheduling).  0: the shape never
+ * splits (its tiles already fill the device).  The first bytes are one u32 ticket per
+ * tile, which must be zero before the first call and are left zero. */
+int64_t am_gfx950_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t group_size);
 
 /* OpType::kRoPE (rope_op.cpp:202-223; RoPEOp design :588-622): split-half rotation of
  * q [seq][hq*d] and k [seq][hkv*d] at positions pos[seq] (I64, device) using the

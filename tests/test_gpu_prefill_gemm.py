@@ -3,6 +3,9 @@ the C ABI, against the CPU oracle: am_gfx950_linear (store, residual) and
 am_gfx950_prefill_linear (q|k|v column split, gate|up SiLU-Mul) at the 8B prefill
 shapes (512 rows; q|k|v 6144x4096, gate|up 28672x4096, down 4096x14336) and at ragged
 shapes (rows and columns that are not tile multiples, a k of one group, groups of 256).
+With a workspace, shapes whose tiles leave CUs idle split K; the split launches are
+checked against the oracle and repeated to show that they are deterministic and leave
+their tickets at zero.
 
 Bar: bf16 outputs within 2e-2 of the largest reference magnitude per row (north-star
 tolerance); the oracle computes a sample of rows in full, covering every 128-row tile.
@@ -20,7 +23,7 @@ if not torch.cuda.is_available():  # pragma: no cover
 
 import aethermind_amd.native as N  # noqa: E402
 import oracle_lib as O  # noqa: E402
-from gpu_util import bf16_dev, bits_host, empty, p, pack_weight, stream  # noqa: E402
+from gpu_util import bf16_dev, bits_host, empty, host, p, pack_weight, stream  # noqa: E402
 from test_gpu_decode_shapes import act_rows, bf16_rne_bits, bits_f32, close, launched, rbf  # noqa: E402
 
 L = N.lib()
@@ -74,7 +77,8 @@ def test_silu_mul_gate_up(m):
     out = empty((m, F), torch.int16)
     a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0))
     L.call("am_gfx950_prefill_linear", a, stream())
-    assert launched() == ("gemm_i4<silu_mul,bn=256>" if m >= 256 else "gemm_i4<silu_mul,bn=128>"), launched()
+    assert launched() == ("gemm_i4<silu_mul,bn=256,splits=1>" if m >= 256 else "gemm_i4<silu_mul,bn=128,splits=1>"), \
+        launched()
     rows = sample_rows(m)
     gu = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
     ref = rbf(O.silu_mul(gu[:, :F], gu[:, F:]))
@@ -107,6 +111,111 @@ def test_linear_store_and_residual(shape):
     got = rd(rdv)
     for i, r in enumerate(rows):
         close(got[r], rbf(res[r] + rbf(ref[i])), TOL, f"residual row {r} {shape}")
+
+
+def workspace(m, n, k, group):
+    nbytes = L.am_gfx950_gemm_workspace_bytes(m, n, k, group)
+    return nbytes, (torch.zeros(max(nbytes, 16), dtype=torch.uint8, device="cuda") if nbytes else None)
+
+
+def splits_of(name):
+    return int(name.split("splits=")[1].rstrip(">"))
+
+
+def tickets_zero(ws, tiles):
+    return not host(ws)[:4 * tiles].any()
+
+
+# (m, n, k, group, expected splits): the 8B o and down shapes, ragged tiles, a split
+# count capped by the group count, per-element epilogue chunks (n % 8 != 0)
+SPLIT_SHAPES = [(512, 4096, 4096, 128, 2), (512, 4096, 14336, 128, 4), (100, 520, 4096, 128, 4),
+                (33, 130, 2048, 128, 2), (64, 1000, 8192, 256, 4)]
+
+
+@pytest.mark.parametrize("shape", SPLIT_SHAPES)
+def test_split_k_residual(shape):
+    m, n, k, group, want = shape
+    w, dw, keep = int4_weight(n, k, seed=241 + n, group=group)
+    x = act_rows(242, m, k)
+    res = act_rows(243, m, n)
+    xd = bf16_dev(bf16_rne_bits(x))
+    nbytes, ws = workspace(m, n, k, group)
+    assert nbytes > 0
+    rows = sample_rows(m)
+    ref = O.linear(np.ascontiguousarray(x[rows]), w)
+    outs = []
+    for rep in range(2):  # the second call runs on the tickets the first left behind
+        rdv = bf16_dev(bf16_rne_bits(res))
+        args = N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(rdv), N.AM_DT_BF16, p(rdv), 2)
+        args.workspace, args.workspace_bytes = p(ws), nbytes
+        L.call("am_gfx950_linear", args, stream())
+        assert launched().startswith("gemm_i4<residual,") and splits_of(launched()) == want, launched()
+        got = rd(rdv)
+        for i, r in enumerate(rows):
+            close(got[r], rbf(res[r] + rbf(ref[i])), TOL, f"split residual row {r} {shape} call {rep}")
+        outs.append(bits_host(rdv))
+    assert np.array_equal(outs[0], outs[1]), "split-K results differ between calls"
+    assert tickets_zero(ws, -(-m // 128) * -(-n // 128)), "tickets not left at zero"
+    # the store epilogue on the same workspace
+    out = empty((m, n), torch.int16)
+    args = N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2)
+    args.workspace, args.workspace_bytes = p(ws), nbytes
+    L.call("am_gfx950_linear", args, stream())
+    assert launched().startswith("gemm_i4<store,") and splits_of(launched()) == want, launched()
+    got = rd(out)
+    for i, r in enumerate(rows):
+        close(got[r], rbf(ref[i]), TOL, f"split store row {r} {shape}")
+
+
+def test_split_k_qkv_and_silu_few_rows():
+    m, k = 64, 4096
+    n_q, n_kv = 4096, 1024
+    w, dw, keep = int4_weight(n_q + 2 * n_kv, k, seed=251)
+    x = act_rows(252, m, k)
+    xd = bf16_dev(bf16_rne_bits(x))
+    nbytes, ws = workspace(m, n_q + 2 * n_kv, k, 128)
+    outs = [empty((m, n), torch.int16) for n in (n_q, n_kv, n_kv)]
+    a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SPLIT, (N.vp * 3)(*[p(o) for o in outs]),
+                            (N.i64 * 2)(n_q, n_q + n_kv), p(ws), nbytes)
+    L.call("am_gfx950_prefill_linear", a, stream())
+    assert launched().startswith("gemm_i4<split,") and splits_of(launched()) > 1, launched()
+    rows = sample_rows(m)
+    ref = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
+    got = np.concatenate([rd(o) for o in outs], axis=1)
+    for i, r in enumerate(rows):
+        close(got[r], ref[i], TOL, f"split-K q|k|v row {r}")
+    F = 2048
+    w, dw, keep = int4_weight(2 * F, k, seed=253)
+    nbytes, ws = workspace(m, 2 * F, k, 128)
+    out = empty((m, F), torch.int16)
+    a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0),
+                            p(ws), nbytes)
+    L.call("am_gfx950_prefill_linear", a, stream())
+    assert launched().startswith("gemm_i4<silu_mul,") and splits_of(launched()) > 1, launched()
+    gu = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
+    ref = rbf(O.silu_mul(gu[:, :F], gu[:, F:]))
+    got = rd(out)
+    for i, r in enumerate(rows):
+        close(got[r], ref[i], TOL, f"split-K silu row {r}")
+    assert tickets_zero(ws, F // 64), "tickets not left at zero"
+
+
+def test_workspace_too_small_runs_unsplit():
+    m, n, k = 512, 4096, 4096
+    w, dw, keep = int4_weight(n, k, seed=261)
+    x = act_rows(262, m, k)
+    xd = bf16_dev(bf16_rne_bits(x))
+    ws = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    out = empty((m, n), torch.int16)
+    args = N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2)
+    args.workspace, args.workspace_bytes = p(ws), 4096
+    L.call("am_gfx950_linear", args, stream())
+    assert launched() == "gemm_i4<store,bn=128,splits=1>", launched()
+    rows = sample_rows(m)
+    ref = O.linear(np.ascontiguousarray(x[rows]), w)
+    got = rd(out)
+    for i, r in enumerate(rows):
+        close(got[r], rbf(ref[i]), TOL, f"row {r}")
 
 
 def test_prefill_linear_rejects_other_formats():
