@@ -450,20 +450,27 @@ int64_t TilesOf(const I4Args& p) {
   return tiles_m * (EPI == kI4SiluMul ? p.ffn / (Shape<NWN>::kBN / 2) : CeilDiv(p.N, Shape<NWN>::kBN));
 }
 
+constexpr int64_t kTicketRegion = 4096;               // bytes at the start of the workspace
+constexpr int64_t kMaxSplitTiles = kTicketRegion / 4;  // tiles of a launch that may split
+
 // Split-K count: the largest power of two <= 4 that still gives every CU at most one
 // block with >= 8 groups per split; long rows (>= 24 groups per split) may take two
 // blocks per CU.  The loop's per-CU rate is nearly the same with one block per CU as
 // with two, so splits pay when tiles alone leave CUs idle, and the partial merge
 // (~9 us) must be amortised.
 int SplitsFor(int64_t tiles, int64_t groups, int64_t cus) {
+  if (tiles > kMaxSplitTiles) return 1;
   int s = 1;
   while (s < 4 && tiles * s * 2 <= cus && groups / (s * 2) >= 8) s *= 2;
   if (s < 4 && tiles * s * 2 <= 2 * cus && groups / (s * 2) >= 24) s *= 2;
   return s;
 }
 
-// Workspace layout: tickets (one u32 per tile, 256-byte rounded), then the partials.
-int64_t TicketBytes(int64_t tiles) { return 256 * CeilDiv(tiles * 4, 256); }
+// Workspace layout: a fixed ticket region (one u32 per tile of a splitting launch),
+// then the partials.  The region's size does not depend on the launch's shape, so
+// launches of different shapes can share one workspace: no launch's partials land on
+// another launch's tickets.
+int64_t TicketBytes(int64_t) { return kTicketRegion; }
 template <int NWN>
 int64_t PartialBytes(int64_t tiles, int splits) {
   return splits > 1 ? tiles * splits * Shape<NWN>::kWaves * (16 * 64 * 16) : 0;

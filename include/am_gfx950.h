@@ -151,8 +151,10 @@ am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* arg
  * group size group_size) may split K: split s of an output tile sums a contiguous
  * range of whole groups, and the tile's last split block adds the fp32 partials in
  * split order (results are independent of block scheduling).  0: the shape never
- * splits (its tiles already fill the device).  The first bytes are one u32 ticket per
- * tile, which must be zero before the first call and are left zero. */
+ * splits (its tiles already fill the device).  The first 4096 bytes are the tickets
+ * (one u32 per tile of the launch), which must be zero before the first call and are
+ * left zero; the region has the same size for every shape, so one workspace sized for
+ * the largest shape serves launches of different shapes in turn. */
 int64_t am_gfx950_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t group_size);
 
 /* OpType::kRoPE (rope_op.cpp:202-223; RoPEOp design :588-622): split-half rotation of

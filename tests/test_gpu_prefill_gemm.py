@@ -200,6 +200,56 @@ def test_split_k_qkv_and_silu_few_rows():
     assert tickets_zero(ws, F // 64), "tickets not left at zero"
 
 
+def test_split_k_shapes_share_one_workspace():
+    """A session's prefill runs q|k|v, o, gate|up and down on one workspace: a launch
+    with few tiles leaves its partials where a launch with more tiles keeps tickets
+    unless the ticket region is the same for every shape.  2048-wide layer at 24 rows:
+    q|k|v 24 tiles, gate|up 88 tiles, down 16 tiles, all split."""
+    m, H, F, nq, nkv = 24, 2048, 5632, 2048, 512
+    shapes = [(nq + 2 * nkv, H), (2 * F, H), (H, F)]
+    nbytes = max(L.am_gfx950_gemm_workspace_bytes(m, n, k, 128) for n, k in shapes)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    # the third value keeps the device tensors the weight structs point into alive
+    wq, dq, kq = int4_weight(nq + 2 * nkv, H, seed=271)
+    wg, dg, kg = int4_weight(2 * F, H, seed=272)
+    wd, dd, kd = int4_weight(H, F, seed=273)
+    x = act_rows(274, m, H)
+    xd = bf16_dev(bf16_rne_bits(x))
+    rows = sample_rows(m)
+    for rep in range(2):
+        outs = [empty((m, n), torch.int16) for n in (nq, nkv, nkv)]
+        a = N.PrefillLinearArgs(p(xd), m, dq, N.AM_PREFILL_SPLIT, (N.vp * 3)(*[p(o) for o in outs]),
+                                (N.i64 * 2)(nq, nq + nkv), p(ws), nbytes)
+        L.call("am_gfx950_prefill_linear", a, stream())
+        assert launched().startswith("gemm_i4<split,") and splits_of(launched()) > 1, launched()
+        got = np.concatenate([rd(o) for o in outs], axis=1)
+        ref = rbf(O.linear(np.ascontiguousarray(x[rows]), wq))
+        for i, r in enumerate(rows):
+            close(got[r], ref[i], TOL, f"shared workspace q|k|v row {r} call {rep}")
+        act = empty((m, F), torch.int16)
+        a = N.PrefillLinearArgs(p(xd), m, dg, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(act), None, None),
+                                (N.i64 * 2)(0, 0), p(ws), nbytes)
+        L.call("am_gfx950_prefill_linear", a, stream())
+        assert launched().startswith("gemm_i4<silu_mul,") and splits_of(launched()) > 1, launched()
+        gu = rbf(O.linear(np.ascontiguousarray(x[rows]), wg))
+        ref = rbf(O.silu_mul(gu[:, :F], gu[:, F:]))
+        got = rd(act)
+        for i, r in enumerate(rows):
+            close(got[r], ref[i], TOL, f"shared workspace silu row {r} call {rep}")
+        a_host = rd(act)
+        out = empty((m, H), torch.int16)
+        args = N.LinearArgs(p(act), N.AM_DT_BF16, m, dd, p(out), N.AM_DT_BF16, None, 2)
+        args.workspace, args.workspace_bytes = p(ws), nbytes
+        L.call("am_gfx950_linear", args, stream())
+        assert launched().startswith("gemm_i4<store,") and splits_of(launched()) > 1, launched()
+        ref = rbf(O.linear(np.ascontiguousarray(a_host[rows]), wd))
+        got = rd(out)
+        for i, r in enumerate(rows):
+            close(got[r], ref[i], TOL, f"shared workspace down row {r} call {rep}")
+    assert tickets_zero(ws, 4096 // 4), "tickets not left at zero"
+    del kq, kg, kd
+
+
 def test_workspace_too_small_runs_unsplit():
     m, n, k = 512, 4096, 4096
     w, dw, keep = int4_weight(n, k, seed=261)
