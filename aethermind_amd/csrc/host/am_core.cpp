@@ -105,6 +105,7 @@ const char* ToString(OpType op) noexcept {
     case OpType::kEmbedToken: return "EmbedToken";
     case OpType::kFusedLinearSplit: return "FusedLinearSplit";
     case OpType::kFusedLinearSiluMul: return "FusedLinearSiluMul";
+    case OpType::kFusedLinearRoPEKVUpdate: return "FusedLinearRoPEKVUpdate";
     default: return "Unknown";
   }
 }

@@ -211,6 +211,7 @@ enum class OpType : uint16_t {
   kFusedDecodeLayers,  // every layer of one decode token in one persistent launch
   kFusedLinearSplit,   // prefill: one weight whose row ranges are several Linears (q|k|v)
   kFusedLinearSiluMul, // prefill: Linear gate|up -> SiluMul
+  kFusedLinearRoPEKVUpdate,  // prefill: Linear q|k|v -> RoPE -> KVCacheUpdate
 };
 const char* ToString(OpType op) noexcept;
 

@@ -307,6 +307,40 @@ Status FusedLinearSplitKernel(const KernelContext& ctx) noexcept {
   return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));
 }
 
+// Prefill q|k|v -> RoPE -> KVCacheUpdate (one sequence): in: x, cos, sin, start,
+// k plane, v plane (, workspace); out: q [m][hq*d]
+Status FusedLinearRoPEKVKernel(const KernelContext& ctx) noexcept {
+  const GfxParams* p = P(ctx);
+  AM_RETURN_IF_ERROR(NeedArgs(p, 6, 1, "FusedLinearRoPEKVUpdate"));
+  if (W(ctx) == nullptr) return Status::InvalidArgument("FusedLinearRoPEKVUpdate requires packed weights");
+  QkvAttrs at{};
+  if (!ReadAttrs(ctx, &at)) return Status::InvalidArgument("FusedLinearRoPEKVUpdate requires QkvAttrs");
+  am_gfx950_prefill_rope_kv r{};
+  r.cos_tab = static_cast<const float*>(p->in[1].p);
+  r.sin_tab = static_cast<const float*>(p->in[2].p);
+  r.max_pos = p->in[1].d[0];
+  r.start_pos_dev = static_cast<const int64_t*>(p->in[3].p);
+  r.k_cache = const_cast<void*>(p->in[4].p);
+  r.v_cache = const_cast<void*>(p->in[5].p);
+  r.hq = at.hq;
+  r.hkv = at.hkv;
+  r.head_dim = at.d;
+  r.capacity = at.cap;
+  const am_gfx950_kv_pages pages = PagesOf(at.pg);
+  if (at.pg.table != nullptr) r.pages = &pages;
+  am_gfx950_prefill_linear_args a{};
+  a.x = p->in[0].p;
+  a.m = p->in[0].d[0];
+  a.w = *W(ctx);
+  a.epilogue = AM_PREFILL_QKV_ROPE_KV;
+  a.out[0] = p->out[0].p;
+  a.rope_kv = &r;
+  GemmWorkspace(p, 6, &a.workspace, &a.workspace_bytes);
+  if (p->out[0].d[1] != at.hq * at.d || p->in[0].d[1] != a.w.k)
+    return Status::InvalidArgument("FusedLinearRoPEKVUpdate: tensor shapes do not match the packed weight");
+  return FromC(am_gfx950_prefill_linear(&a, StreamOf(ctx)));
+}
+
 // Prefill gate|up -> SiluMul: in: x (, workspace); out: act [m][n/2]
 Status FusedLinearSiluMulKernel(const KernelContext& ctx) noexcept {
   const GfxParams* p = P(ctx);
@@ -552,6 +586,8 @@ AM_REGISTER_KERNEL(HipPreLinAddBF16I4, Desc(OpType::kFusedLinearAdd, HipSelector
                                             &PrefillLinearAddKernel, "gfx950::gemm_add_bf16_int4"))
 AM_REGISTER_KERNEL(HipPreSplitBF16I4, Desc(OpType::kFusedLinearSplit, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
                                            &FusedLinearSplitKernel, "gfx950::gemm_split_bf16_int4"))
+AM_REGISTER_KERNEL(HipPreQkvRopeBF16I4, Desc(OpType::kFusedLinearRoPEKVUpdate, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
+                                             &FusedLinearRoPEKVKernel, "gfx950::gemm_qkv_rope_kv_bf16_int4"))
 AM_REGISTER_KERNEL(HipPreSiluBF16I4, Desc(OpType::kFusedLinearSiluMul, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
                                           &FusedLinearSiluMulKernel, "gfx950::gemm_silu_mul_bf16_int4"))
 }  // namespace

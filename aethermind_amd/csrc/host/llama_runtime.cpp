@@ -923,7 +923,19 @@ class LlamaSession {
       if (gemm_ws != nullptr) v.push_back(TensorView(gemm_ws, DataType::UInt(8), {static_cast<int64_t>(gemm_ws_bytes)}));
       return v;
     };
-    if (fuse) {
+    const TensorView kplane(kp, A, {c.num_kv_heads, c.max_tokens, d});
+    const TensorView vplane(vp, A, {c.num_kv_heads, c.max_tokens, d});
+    // q|k|v GEMM with RoPE and the KV cache write in its epilogue (positions *start + i)
+    const bool fuse_rope = fuse && (d == 64 || d == 128);
+    if (fuse_rope) {
+      const gfx950::QkvAttrs qa{c.rms_eps, c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, Paging(row)};
+      std::vector<TensorView> in = gemm_in(xnv);
+      in.insert(in.begin() + 1, {TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+                                 TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+                                 TensorView(start, DataType::Int(64), {1}), kplane, vplane});
+      AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearRoPEKVUpdate, PackAttrs(qa), Sel(true, ph), &m->qkv[l], in,
+                               {MutableTensorView(q, A, {S, Q})}));
+    } else if (fuse) {
       AM_RETURN_IF_ERROR(b.Add(OpType::kFusedLinearSplit, {}, Sel(true, ph), &m->qkv[l], gemm_in(xnv),
                                {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV}),
                                 MutableTensorView(v, A, {S, KV})}));
@@ -932,20 +944,20 @@ class LlamaSession {
       AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.k, {xnv}, {MutableTensorView(k, A, {S, KV})}));
       AM_RETURN_IF_ERROR(b.Add(OpType::kLinear, {}, Sel(true, ph), &W.v, {xnv}, {MutableTensorView(v, A, {S, KV})}));
     }
-    const gfx950::RopeAttrs ra{c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
-    AM_RETURN_IF_ERROR(b.Add(OpType::kRoPE, PackAttrs(ra), Sel(false, ph), nullptr,
-                             {TensorView(q, A, {S, Q}), TensorView(k, A, {S, KV}),
-                              TensorView(pos_rows, DataType::Int(64), {S}),
-                              TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
-                              TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2})},
-                             {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV})}));
-    const gfx950::KvAttrs ka{c.num_kv_heads, d, c.max_tokens, Paging(row)};
-    const TensorView kplane(kp, A, {c.num_kv_heads, c.max_tokens, d});
-    const TensorView vplane(vp, A, {c.num_kv_heads, c.max_tokens, d});
-    AM_RETURN_IF_ERROR(b.Add(OpType::kKVCacheUpdate, PackAttrs(ka), Sel(false, ph), nullptr,
-                             {TensorView(k, A, {S, KV}), TensorView(v, A, {S, KV}), kplane, vplane,
-                              TensorView(start, DataType::Int(64), {1})},
-                             {}));
+    if (!fuse_rope) {
+      const gfx950::RopeAttrs ra{c.num_q_heads, c.num_kv_heads, d, c.max_tokens};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kRoPE, PackAttrs(ra), Sel(false, ph), nullptr,
+                               {TensorView(q, A, {S, Q}), TensorView(k, A, {S, KV}),
+                                TensorView(pos_rows, DataType::Int(64), {S}),
+                                TensorView(m->cos_tab, DataType::Float32(), {c.max_tokens, d / 2}),
+                                TensorView(m->sin_tab, DataType::Float32(), {c.max_tokens, d / 2})},
+                               {MutableTensorView(q, A, {S, Q}), MutableTensorView(k, A, {S, KV})}));
+      const gfx950::KvAttrs ka{c.num_kv_heads, d, c.max_tokens, Paging(row)};
+      AM_RETURN_IF_ERROR(b.Add(OpType::kKVCacheUpdate, PackAttrs(ka), Sel(false, ph), nullptr,
+                               {TensorView(k, A, {S, KV}), TensorView(v, A, {S, KV}), kplane, vplane,
+                                TensorView(start, DataType::Int(64), {1})},
+                               {}));
+    }
     const gfx950::AttnAttrs aa{c.num_q_heads, c.num_kv_heads, d, c.max_tokens, 0, 1, 0, Paging(row)};
     AM_RETURN_IF_ERROR(b.Add(OpType::kAttention, PackAttrs(aa), Sel(false, ph), nullptr,
                              {TensorView(q, A, {S, Q}), kplane, vplane, TensorView(start, DataType::Int(64), {1})},

@@ -73,6 +73,8 @@ int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group);
 am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
                       void* out2, int64_t c1, int64_t c2, const void* residual, void* ws, int64_t ws_bytes,
                       hipStream_t s);
+am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight& w, const am_gfx950_prefill_rope_kv& r,
+                               void* q_out, void* ws, int64_t ws_bytes, hipStream_t s);
 
 // ---- device: numeric helpers ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }

@@ -347,6 +347,10 @@ extern "C" am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linea
     case AM_PREFILL_SILU_MUL:
       return GemmI4(a->x, a->m, a->w, 3, a->out[0], nullptr, nullptr, 0, 0, nullptr, a->workspace, a->workspace_bytes,
                     AsStream(stream));
+    case AM_PREFILL_QKV_ROPE_KV:
+      AM_CHECK_ARG(a->rope_kv != nullptr, "prefill_linear: the q|k|v RoPE epilogue needs rope_kv");
+      return GemmI4QkvRopeKv(a->x, a->m, a->w, *a->rope_kv, a->out[0], a->workspace, a->workspace_bytes,
+                             AsStream(stream));
     default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "prefill_linear: unknown epilogue");
   }
 }

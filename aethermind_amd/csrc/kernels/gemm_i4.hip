@@ -76,7 +76,7 @@ struct Shape {
 // 16 rows taken as two parity classes, land in distinct LDS banks.
 __device__ __forceinline__ int xsw(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-enum I4Epi { kI4Store = 0, kI4Residual = 1, kI4Split = 2, kI4SiluMul = 3 };
+enum I4Epi { kI4Store = 0, kI4Residual = 1, kI4Split = 2, kI4SiluMul = 3, kI4QkvRope = 4 };
 
 struct I4Args {
   const uint16_t* x;  // bf16 [M][K]
@@ -93,6 +93,16 @@ struct I4Args {
   int32_t splits;             // k splits per tile (1: none)
   float* part;                // [tiles][splits][waves][16][64] x 4 fp32 partial accumulators
   unsigned* tickets;          // [tiles], zero between launches
+  // q|k|v + RoPE + KV epilogue: columns [0,c1) q -> out0 (rotated), [c1,c2) k (rotated)
+  // and [c2,N) v into the cache planes at position *start + row
+  const float* cos_tab;       // [cap][hd/2]
+  const float* sin_tab;
+  const int64_t* start;
+  uint16_t* kc;
+  uint16_t* vc;
+  KvRows kv;
+  int32_t hd, cap;
+  int32_t* err;               // optional: set when a row's position is outside [0, cap)
 };
 
 __device__ __forceinline__ bf16x8_t unpack8(uint32_t word, uint32_t mask, uint32_t magic) {
@@ -340,6 +350,67 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
             f32_to_bf16_bits(acc[mt][nt][r]);
   __syncthreads();
 
+  if constexpr (EPI == kI4QkvRope) {
+    // A thread takes a chunk pair: 8 columns of the first half of a head and the 8
+    // columns d/2 later (the RoPE partners), from the rounded tile.  q and k pairs are
+    // rotated in fp32 from the bf16 values and rounded once (the RoPE node); k and v
+    // go straight to the cache rows of their positions (the KVCacheUpdate node).
+    const int32_t d = p.hd, half = d >> 1, hpt = d >> 4;  // chunk pairs per head
+    const int64_t start = *p.start;
+    constexpr int PPR = BN / 16;  // chunk pairs per tile row (BN is a multiple of d)
+    for (int c = tid; c < QBM * PPR; c += S::kThreads) {
+      const int row = c / PPR, pr = c % PPR;
+      const int32_t gm = m0 + row;
+      const int i0 = (pr % hpt) * 8;              // offset of the chunk inside its head
+      const int col = (pr / hpt) * d + i0;        // tile column of the first-half chunk
+      const int32_t gn = tn * BN + col;
+      if (gm >= p.M || gn >= p.N) continue;
+      const uint4 a1 = *reinterpret_cast<const uint4*>(T + row * TS + col);
+      const uint4 a2 = *reinterpret_cast<const uint4*>(T + row * TS + col + half);
+      const int64_t pos = start + gm;
+      const bool ok = pos >= 0 && pos < p.cap;
+      uint4 o1 = a1, o2 = a2;
+      if (gn < p.c2 && ok) {
+        const float4* cp = reinterpret_cast<const float4*>(p.cos_tab + pos * half + i0);
+        const float4* sp = reinterpret_cast<const float4*>(p.sin_tab + pos * half + i0);
+        const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        const uint32_t w1[4] = {a1.x, a1.y, a1.z, a1.w}, w2[4] = {a2.x, a2.y, a2.z, a2.w};
+        uint32_t r1[4], r2[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t y1[2], y2[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float x1 = bf16_bits_to_f32(hh ? (w1[q] >> 16) : (w1[q] & 0xFFFFu));
+            const float x2 = bf16_bits_to_f32(hh ? (w2[q] >> 16) : (w2[q] & 0xFFFFu));
+            const float cc = cv[2 * q + hh], sn = sv[2 * q + hh];
+            y1[hh] = f32_to_bf16_bits(x1 * cc - x2 * sn);
+            y2[hh] = f32_to_bf16_bits(x2 * cc + x1 * sn);
+          }
+          r1[q] = y1[0] | (y1[1] << 16);
+          r2[q] = y2[0] | (y2[1] << 16);
+        }
+        o1 = make_uint4(r1[0], r1[1], r1[2], r1[3]);
+        o2 = make_uint4(r2[0], r2[1], r2[2], r2[3]);
+      }
+      if (!ok && p.err != nullptr) *p.err = 1;
+      if (gn < p.c1) {
+        uint16_t* dst = p.out0 + static_cast<int64_t>(gm) * p.c1 + gn;
+        *reinterpret_cast<uint4*>(dst) = o1;
+        *reinterpret_cast<uint4*>(dst + half) = o2;
+      } else if (ok) {
+        const bool isk = gn < p.c2;
+        const int32_t hc = isk ? gn - p.c1 : gn - p.c2;
+        uint16_t* dst = (isk ? p.kc : p.vc) + p.kv.Row(0, hc / d, pos) + i0;
+        *reinterpret_cast<uint4*>(dst) = o1;
+        *reinterpret_cast<uint4*>(dst + half) = o2;
+      }
+    }
+    return;
+  }
+
   if constexpr (EPI == kI4SiluMul) {
     constexpr int CPR = BN / 16;  // 16-byte output chunks per row (BN/2 features)
     constexpr int IT = QBM * CPR / S::kThreads;
@@ -492,7 +563,7 @@ am_status_code LaunchI4(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
     p.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + TicketBytes(tiles));
   }
   const int64_t blocks = tiles * splits;
-  static const char* const names[] = {"store", "residual", "split", "silu_mul"};
+  static const char* const names[] = {"store", "residual", "split", "silu_mul", "qkv_rope_kv"};
   RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_i4<%s,bn=%d,splits=%d>", names[EPI], S::kBN, splits);
   hipLaunchKernelGGL((gemm_i4_kernel<EPI, NWN>), dim3(static_cast<unsigned>(blocks)), dim3(S::kThreads), S::kLds, s, p);
   AM_RETURN_IF_LAUNCH_FAILED("gemm_i4");
@@ -536,6 +607,46 @@ int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group) {
       best = std::max(best, TicketBytes(tiles) + (nwn == 2 ? PartialBytes<2>(tiles, sp) : PartialBytes<4>(tiles, sp)));
   }
   return best;
+}
+
+// q|k|v GEMM with the RoPE and KVCacheUpdate nodes in the epilogue (one sequence).
+am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight& w, const am_gfx950_prefill_rope_kv& r,
+                               void* q_out, void* ws, int64_t ws_bytes, hipStream_t s) {
+  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unsupported shape or weight");
+  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm_i4: workspace must be 16-byte aligned");
+  AM_CHECK_ARG(r.head_dim == 64 || r.head_dim == 128, "prefill q|k|v RoPE: head_dim must be 64 or 128");
+  AM_CHECK_ARG(r.hq > 0 && r.hkv > 0 && r.hq % r.hkv == 0 && w.n == (r.hq + 2 * r.hkv) * r.head_dim,
+               "prefill q|k|v RoPE: the weight rows must be hq + 2 hkv heads");
+  AM_CHECK_ARG(r.capacity > 0 && r.max_pos >= r.capacity && r.capacity * r.head_dim < (int64_t{1} << 31),
+               "prefill q|k|v RoPE: bad capacity or table length");
+  AM_CHECK_ARG(q_out && r.cos_tab && r.sin_tab && r.start_pos_dev && r.k_cache && r.v_cache,
+               "prefill q|k|v RoPE: null pointer");
+  AM_CHECK_ARG(Aligned16(q_out) && Aligned16(r.k_cache) && Aligned16(r.v_cache) && Aligned16(r.cos_tab) &&
+                   Aligned16(r.sin_tab),
+               "prefill q|k|v RoPE: q, the cache planes and the tables must be 16-byte aligned");
+  I4Args p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.w = static_cast<const uint8_t*>(w.data);
+  p.s = static_cast<const uint16_t*>(w.scales);
+  p.M = static_cast<int32_t>(m);
+  p.N = static_cast<int32_t>(w.n);
+  p.K = static_cast<int32_t>(w.k);
+  p.group = w.group_size;
+  p.out0 = static_cast<uint16_t*>(q_out);
+  p.c1 = static_cast<int32_t>(r.hq * r.head_dim);
+  p.c2 = static_cast<int32_t>((r.hq + r.hkv) * r.head_dim);
+  p.vec = 1;
+  p.splits = 1;
+  p.cos_tab = r.cos_tab;
+  p.sin_tab = r.sin_tab;
+  p.start = r.start_pos_dev;
+  p.kc = static_cast<uint16_t*>(r.k_cache);
+  p.vc = static_cast<uint16_t*>(r.v_cache);
+  p.hd = static_cast<int32_t>(r.head_dim);
+  p.cap = static_cast<int32_t>(r.capacity);
+  p.err = r.err_flag;
+  if (auto st = MakeKvRows(r.pages, 0, r.capacity, r.hkv, r.head_dim, &p.kv); st != AM_STATUS_OK) return st;
+  return LaunchI4Any<kI4QkvRope>(p, ws, ws_bytes, s);
 }
 
 am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,

@@ -3,9 +3,11 @@
 // All of them are HBM-bound streaming kernels: 16-byte vector accesses where the
 // row length allows, one block per row for the row reductions.
 
+#include <algorithm>
 #include <cmath>
 
 #include "am_kernel_common.h"
+#include "am_launch_timing.h"
 
 namespace am {
 namespace {
@@ -54,6 +56,51 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const typename X::T* x, co
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
   for (int64_t j = threadIdx.x; j < hidden; j += 256)
     O::store(orow, j, (X::load(xr, j) * inv) * W::load(w, j));
+}
+
+// bf16 rows with hidden = 512 NV (prefill): one wave per row, the row and the gain
+// held in registers as NV 16-byte pieces per lane, all loads issued at once; 16-byte
+// stores.  The same formula and roundings as rmsnorm_kernel.
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_rows_bf16_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                                                                int32_t rows, int64_t xs, int64_t os, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int32_t row = static_cast<int32_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * xs);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  uint4 xv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) xv[v] = xr[lane + 64 * v];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wv[v] = wr[lane + 64 * v];
+  float ss = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const uint32_t q[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float a = bf16_bits_to_f32(q[t] & 0xFFFFu), b = bf16_bits_to_f32(q[t] >> 16);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(NV * 512) + eps);
+  uint4* orow = reinterpret_cast<uint4*>(out + row * os);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const uint32_t q[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+    const uint32_t g[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float lo = (bf16_bits_to_f32(q[t] & 0xFFFFu) * inv) * bf16_bits_to_f32(g[t] & 0xFFFFu);
+      const float hi = (bf16_bits_to_f32(q[t] >> 16) * inv) * bf16_bits_to_f32(g[t] >> 16);
+      o[t] = f32_to_bf16_bits(lo) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    }
+    orow[lane + 64 * v] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 // ---------------- RoPE ----------------
@@ -296,8 +343,31 @@ extern "C" am_status_code am_gfx950_rmsnorm(const am_gfx950_rmsnorm_args* a, voi
   AM_CHECK_ARG(a->rows <= 0x7FFFFFFF, "rmsnorm: too many rows");
   if (a->rows == 0) return AM_STATUS_OK;
   AM_CHECK_ARG(a->x && a->w && a->out, "rmsnorm: null data pointer");
-  const dim3 grid(static_cast<unsigned>(a->rows));
   hipStream_t s = AsStream(stream);
+  // bf16 rows of 512, 1024, 2048, 4096 or 8192 values, 16-byte aligned: the wave-per-row kernel
+  const int64_t nv = a->hidden / 512;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(a->x) | reinterpret_cast<uintptr_t>(a->w) |
+                         reinterpret_cast<uintptr_t>(a->out)) & 15u) == 0 && a->x_stride % 8 == 0 && a->out_stride % 8 == 0;
+  if (a->x_dtype == AM_DT_BF16 && a->w_dtype == AM_DT_BF16 && a->out_dtype == AM_DT_BF16 && aligned &&
+      a->hidden % 512 == 0 && (nv == 1 || nv == 2 || nv == 4 || nv == 8 || nv == 16) &&
+      a->rows * std::max(a->x_stride, a->out_stride) < (int64_t{1} << 31)) {
+    const dim3 g4(static_cast<unsigned>(CeilDiv(a->rows, 4)));
+    const auto* xp = static_cast<const uint16_t*>(a->x);
+    const auto* wp = static_cast<const uint16_t*>(a->w);
+    auto* op = static_cast<uint16_t*>(a->out);
+    const int32_t rows = static_cast<int32_t>(a->rows);
+    switch (nv) {
+      case 1: hipLaunchKernelGGL(rmsnorm_rows_bf16_kernel<1>, g4, dim3(256), 0, s, xp, wp, op, rows, a->x_stride, a->out_stride, a->eps); break;
+      case 2: hipLaunchKernelGGL(rmsnorm_rows_bf16_kernel<2>, g4, dim3(256), 0, s, xp, wp, op, rows, a->x_stride, a->out_stride, a->eps); break;
+      case 4: hipLaunchKernelGGL(rmsnorm_rows_bf16_kernel<4>, g4, dim3(256), 0, s, xp, wp, op, rows, a->x_stride, a->out_stride, a->eps); break;
+      case 8: hipLaunchKernelGGL(rmsnorm_rows_bf16_kernel<8>, g4, dim3(256), 0, s, xp, wp, op, rows, a->x_stride, a->out_stride, a->eps); break;
+      default: hipLaunchKernelGGL(rmsnorm_rows_bf16_kernel<16>, g4, dim3(256), 0, s, xp, wp, op, rows, a->x_stride, a->out_stride, a->eps); break;
+    }
+    RecordLaunch(static_cast<int64_t>(g4.x), 256, 0, "rmsnorm_rows_bf16<nv=%d>", static_cast<int>(nv));
+    AM_RETURN_IF_LAUNCH_FAILED("rmsnorm");
+    return AM_STATUS_OK;
+  }
+  const dim3 grid(static_cast<unsigned>(a->rows));
 #define AM_RMS(X, W, O)                                                                        \
   hipLaunchKernelGGL((rmsnorm_kernel<X, W, O>), grid, dim3(256), 0, s,                        \
                      static_cast<const X::T*>(a->x), static_cast<const W::T*>(a->w),           \

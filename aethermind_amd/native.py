@@ -11,7 +11,7 @@ import os
 
 AM_DT_F32, AM_DT_BF16, AM_DT_F16, AM_DT_I8, AM_DT_I4, AM_DT_I32, AM_DT_I64, AM_DT_U32, AM_DT_U8 = range(9)
 AM_WF_F32, AM_WF_BF16, AM_WF_INT8, AM_WF_INT4 = range(4)
-AM_PREFILL_SPLIT, AM_PREFILL_SILU_MUL = 0, 1
+AM_PREFILL_SPLIT, AM_PREFILL_SILU_MUL, AM_PREFILL_QKV_ROPE_KV = 0, 1, 2
 AM_LOAD_STRICT_TENSOR_NAMES, AM_LOAD_REJECT_UNKNOWN_TENSORS, AM_LOAD_ALLOW_QUANTIZED_TENSORS = 1, 2, 4
 (AM_ROLE_QKV, AM_ROLE_O, AM_ROLE_GATE_UP, AM_ROLE_DOWN, AM_ROLE_LM_HEAD, AM_ROLE_Q, AM_ROLE_K, AM_ROLE_V,
  AM_ROLE_GATE, AM_ROLE_UP) = range(10)
@@ -49,18 +49,24 @@ class LinearArgs(C.Structure):
                 ("residual", vp), ("mode", i32), ("workspace", vp), ("workspace_bytes", i64)]
 
 
+class KvPages(C.Structure):
+    _fields_ = [("block_table", vp), ("block_size", i32), ("table_stride", i32), ("num_blocks", i64)]
+
+
+class PrefillRopeKv(C.Structure):
+    _fields_ = [("cos_tab", vp), ("sin_tab", vp), ("max_pos", i64), ("start_pos_dev", vp), ("k_cache", vp),
+                ("v_cache", vp), ("hq", i64), ("hkv", i64), ("head_dim", i64), ("capacity", i64),
+                ("pages", C.POINTER(KvPages)), ("err_flag", vp)]
+
+
 class PrefillLinearArgs(C.Structure):
     _fields_ = [("x", vp), ("m", i64), ("w", Weight), ("epilogue", i32), ("out", vp * 3), ("split", i64 * 2),
-                ("workspace", vp), ("workspace_bytes", i64)]
+                ("workspace", vp), ("workspace_bytes", i64), ("rope_kv", C.POINTER(PrefillRopeKv))]
 
 
 class RopeArgs(C.Structure):
     _fields_ = [("q", vp), ("k", vp), ("q_out", vp), ("k_out", vp), ("pos", vp), ("cos_tab", vp), ("sin_tab", vp),
                 ("seq", i64), ("hq", i64), ("hkv", i64), ("head_dim", i64), ("max_pos", i64), ("dtype", i32)]
-
-
-class KvPages(C.Structure):
-    _fields_ = [("block_table", vp), ("block_size", i32), ("table_stride", i32), ("num_blocks", i64)]
 
 
 class KvUpdateArgs(C.Structure):

@@ -130,11 +130,30 @@ am_status_code am_gfx950_linear(const am_gfx950_linear_args* args, void* hip_str
  *                        to bf16 as its own Linear's output
  *   AM_PREFILL_SILU_MUL  Linear gate|up (rows [0, n/2) gate, [n/2, n) up) -> SiluMul:
  *                        out[0] [m][n/2] = round(silu(round(gate)) * round(up))
+ *   AM_PREFILL_QKV_ROPE_KV  Linear q|k|v -> RoPE -> KVCacheUpdate for one sequence
+ *                        (rope_op.cpp:11-223, kvcache_update_op.cpp:50-138): row i is
+ *                        position *rope_kv->start_pos_dev + i; out[0] [m][hq*d] gets
+ *                        the rotated q; k (rotated) and v go straight into the cache
+ *                        planes (pages: the sequence's block-table row).  Rows whose
+ *                        position is outside [0, capacity) write no cache row, keep
+ *                        q unrotated and set *err_flag (when not NULL).
  * (model_graph_builder.cpp:133-290 node order; SiluMul formula const_eval_silu_mul.cpp:18-31) */
 typedef enum am_gfx950_prefill_epilogue {
   AM_PREFILL_SPLIT = 0,
-  AM_PREFILL_SILU_MUL = 1
+  AM_PREFILL_SILU_MUL = 1,
+  AM_PREFILL_QKV_ROPE_KV = 2
 } am_gfx950_prefill_epilogue;
+typedef struct am_gfx950_prefill_rope_kv {
+  const float* cos_tab;          /* [max_pos][head_dim/2], am_gfx950_rope_table */
+  const float* sin_tab;
+  int64_t max_pos;               /* at least capacity */
+  const int64_t* start_pos_dev;  /* device: position of row 0 */
+  void* k_cache;                 /* the layer's planes [hkv][capacity][d] (or block pools) */
+  void* v_cache;
+  int64_t hq, hkv, head_dim, capacity;
+  const struct am_gfx950_kv_pages* pages; /* NULL: contiguous planes (struct defined below) */
+  int32_t* err_flag;             /* optional */
+} am_gfx950_prefill_rope_kv;
 typedef struct am_gfx950_prefill_linear_args {
   const void* x;
   int64_t m;
@@ -144,6 +163,7 @@ typedef struct am_gfx950_prefill_linear_args {
   int64_t split[2];
   void* workspace;      /* optional, as in am_gfx950_linear_args */
   int64_t workspace_bytes;
+  const am_gfx950_prefill_rope_kv* rope_kv; /* AM_PREFILL_QKV_ROPE_KV only */
 } am_gfx950_prefill_linear_args;
 am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* args, void* hip_stream);
 

@@ -250,6 +250,67 @@ def test_split_k_shapes_share_one_workspace():
     del kq, kg, kd
 
 
+def qkv_rope_run(m, start, hq=16, hkv=4, d=128, H=2048, cap=256, with_ws=True, seed=281):
+    """One AM_PREFILL_QKV_ROPE_KV launch on fresh zeroed cache planes; returns the
+    oracle inputs and the device outputs."""
+    import ctypes as C
+    n = (hq + 2 * hkv) * d
+    w, dw, keep = int4_weight(n, H, seed=seed)
+    x = act_rows(seed + 1, m, H)
+    xd = bf16_dev(bf16_rne_bits(x))
+    ctab, stab = O.rope_tables(cap, d, 10000.0)
+    cd, sd = torch.from_numpy(ctab).cuda(), torch.from_numpy(stab).cuda()
+    kc = torch.zeros(hkv * cap * d, dtype=torch.int16, device="cuda")
+    vc = torch.zeros(hkv * cap * d, dtype=torch.int16, device="cuda")
+    q = empty((m, hq * d), torch.int16)
+    startd = torch.tensor([start], dtype=torch.int64, device="cuda")
+    errd = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nbytes, ws = workspace(m, n, H, 128) if with_ws else (0, None)
+    r = N.PrefillRopeKv(p(cd), p(sd), cap, p(startd), p(kc), p(vc), hq, hkv, d, cap, None, p(errd))
+    a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_QKV_ROPE_KV, (N.vp * 3)(p(q), None, None), (N.i64 * 2)(0, 0),
+                            p(ws), nbytes, C.pointer(r))
+    L.call("am_gfx950_prefill_linear", a, stream())
+    name = launched()
+    out = dict(q=rd(q), k=rd(kc).reshape(hkv, cap, d), v=rd(vc).reshape(hkv, cap, d), err=int(host(errd)[0]))
+    del keep
+    return x, w, ctab, stab, out, name
+
+
+@pytest.mark.parametrize("m,start", [(200, 37), (24, 100), (1, 255)])
+def test_qkv_rope_kv_epilogue(m, start):
+    """q|k|v GEMM with RoPE and the KV cache write in the epilogue, against the
+    oracle's Linear -> bf16 -> RoPE -> bf16 (q, k) and Linear -> bf16 (v) at positions
+    start + i; cache rows outside [start, start + m) stay untouched.  24 rows split K."""
+    hq, hkv, d, cap = 16, 4, 128, 256
+    x, w, ctab, stab, out, name = qkv_rope_run(m, start)
+    assert name.startswith("gemm_i4<qkv_rope_kv,"), name
+    if m == 24:
+        assert splits_of(name) > 1, name
+    rows = sample_rows(m)
+    lin = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
+    pos = start + np.asarray(rows, np.int64)
+    qref = rbf(O.rope(lin[:, :hq * d], hq, d, pos, ctab, stab))
+    kref = rbf(O.rope(lin[:, hq * d:(hq + hkv) * d], hkv, d, pos, ctab, stab))
+    vref = lin[:, (hq + hkv) * d:]
+    for i, r in enumerate(rows):
+        close(out["q"][r], qref[i], TOL, f"q row {r}")
+        close(out["k"][:, start + r, :].reshape(-1), kref[i], TOL, f"k row {r}")
+        close(out["v"][:, start + r, :].reshape(-1), vref[i], TOL, f"v row {r}")
+    for t in ("k", "v"):
+        assert not out[t][:, :start].any() and not out[t][:, start + m:].any(), f"{t} rows outside the chunk written"
+    assert out["err"] == 0
+
+
+def test_qkv_rope_kv_rows_past_capacity():
+    """Rows whose position reaches the capacity write no cache row and set the flag."""
+    cap, m, start = 256, 24, 246
+    x, w, ctab, stab, out, name = qkv_rope_run(m, start, with_ws=False)
+    assert name.startswith("gemm_i4<qkv_rope_kv,") and splits_of(name) == 1, name
+    assert out["err"] == 1
+    assert out["k"][:, start:cap].any() and out["v"][:, start:cap].any()
+    assert not out["k"][:, :start].any() and not out["v"][:, :start].any()
+
+
 def test_workspace_too_small_runs_unsplit():
     m, n, k = 512, 4096, 4096
     w, dw, keep = int4_weight(n, k, seed=261)
