@@ -79,6 +79,15 @@ am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight&
 // ---- device: numeric helpers ----
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+// RoPE rotation of the pair (x1, x2) = (value i, value i + d/2) of a head (rope_op.cpp
+// split-half form): y1 = x1 c - x2 s, y2 = x2 c + x1 s in fp32.  The fused multiply-adds
+// are written out so every kernel that rotates (the RoPE node, and the q|k|v epilogues
+// that replace it) rounds identically whatever the compiler would contract.
+__device__ __forceinline__ void rope_rotate(float x1, float x2, float c, float s, float& y1, float& y2) {
+  y1 = __builtin_fmaf(x1, c, -(x2 * s));
+  y2 = __builtin_fmaf(x1, s, x2 * c);
+}
+
 // float -> bf16 round-to-nearest-even, NaN -> 0x7FC0 (the reference's conversion,
 // bfloat16.cpp:20-32).
 // The conversion is v_cvt_pk_bf16_f32 (RNE); only NaN needs the canonical pattern.

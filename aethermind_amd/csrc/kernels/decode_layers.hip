@@ -479,8 +479,7 @@ __device__ __forceinline__ bool phase_qkv(int l, uint32_t E0, int64_t pos, int S
         if (head < hq + hkv) {
           const float cq = (qd == q0) ? cs_c : a.cos_tab[pc * (kD / 2) + i0 + pp];
           const float sq = (qd == q0) ? cs_s : a.sin_tab[pc * (kD / 2) + i0 + pp];
-          o0 = y0 * cq - y1 * sq;
-          o1 = y1 * cq + y0 * sq;
+          rope_rotate(y0, y1, cq, sq, o0, o1);
         } else {
           o0 = y0;
           o1 = y1;

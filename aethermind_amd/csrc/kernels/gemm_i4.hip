@@ -386,8 +386,10 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
             const float x1 = bf16_bits_to_f32(hh ? (w1[q] >> 16) : (w1[q] & 0xFFFFu));
             const float x2 = bf16_bits_to_f32(hh ? (w2[q] >> 16) : (w2[q] & 0xFFFFu));
             const float cc = cv[2 * q + hh], sn = sv[2 * q + hh];
-            y1[hh] = f32_to_bf16_bits(x1 * cc - x2 * sn);
-            y2[hh] = f32_to_bf16_bits(x2 * cc + x1 * sn);
+            float r1v, r2v;
+            rope_rotate(x1, x2, cc, sn, r1v, r2v);
+            y1[hh] = f32_to_bf16_bits(r1v);
+            y2[hh] = f32_to_bf16_bits(r2v);
           }
           r1[q] = y1[0] | (y1[1] << 16);
           r2[q] = y2[0] | (y2[1] << 16);

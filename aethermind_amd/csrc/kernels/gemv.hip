@@ -602,8 +602,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
       const float y0 = A::round(a0), y1 = A::round(a1);
       if (head < p.hq + p.hkv) {
         const float c = cs_lds[i], s = cs_lds[half + i];
-        const float o0 = y0 * c - y1 * s;
-        const float o1 = y1 * c + y0 * s;
+        float o0, o1;
+        rope_rotate(y0, y1, c, s, o0, o1);
         if (head < p.hq) {
           T* q = static_cast<T*>(p.q_out);
           A::store(q, head * p.d + i, o0);

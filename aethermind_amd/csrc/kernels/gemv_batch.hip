@@ -415,8 +415,8 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
         const int64_t pr = in_cache ? pos : 0;  // table row (the tables hold cap positions)
         if (head < p.hq + p.hkv) {
           const float c = p.cos_tab[pr * half + i], sn = p.sin_tab[pr * half + i];
-          const float o0 = y0 * c - y1 * sn;
-          const float o1 = y1 * c + y0 * sn;
+          float o0, o1;
+          rope_rotate(y0, y1, c, sn, o0, o1);
           if (head < p.hq) {
             uint16_t* q = p.q_out + static_cast<int64_t>(b) * p.hq * p.d + head * p.d;
             q[i] = f32_to_bf16_bits(o0);

@@ -128,8 +128,10 @@ __global__ __launch_bounds__(256) void rope_kernel(const typename A::T* x, typen
     }
     const float c = cos_tab[p * half + i];
     const float sn = sin_tab[p * half + i];
-    A::store(out, base + i, x1 * c - x2 * sn);
-    A::store(out, base + i + half, x2 * c + x1 * sn);
+    float y1, y2;
+    rope_rotate(x1, x2, c, sn, y1, y2);
+    A::store(out, base + i, y1);
+    A::store(out, base + i + half, y2);
   }
 }
 

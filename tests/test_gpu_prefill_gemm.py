@@ -311,6 +311,42 @@ def test_qkv_rope_kv_rows_past_capacity():
     assert not out["k"][:, :start].any() and not out["v"][:, :start].any()
 
 
+def test_qkv_rope_kv_bit_identical_to_separate_nodes_long_chunk():
+    """The fused epilogue against the nodes it replaces, bit for bit, at the long-context
+    chunk: 2048 rows at positions 6144..8191 of the 8B q|k|v shape (16 row tiles, two
+    tile bands): split GEMM, then am_gfx950_rope, then am_gfx950_kv_update."""
+    import ctypes as C
+    m, start, cap, hq, hkv, d, H = 2048, 6144, 8192, 32, 8, 128, 4096
+    n = (hq + 2 * hkv) * d
+    w, dw, keep = int4_weight(n, H, seed=291)
+    xd = bf16_dev(bf16_rne_bits(act_rows(292, m, H)))
+    ctab, stab = O.rope_tables(cap, d, 500000.0)
+    cd, sd = torch.from_numpy(ctab).cuda(), torch.from_numpy(stab).cuda()
+    startd = torch.tensor([start], dtype=torch.int64, device="cuda")
+    posd = torch.arange(start, start + m, dtype=torch.int64, device="cuda")
+    planes = [torch.zeros(hkv * cap * d, dtype=torch.int16, device="cuda") for _ in range(4)]
+    # fused
+    qf = empty((m, hq * d), torch.int16)
+    r = N.PrefillRopeKv(p(cd), p(sd), cap, p(startd), p(planes[0]), p(planes[1]), hq, hkv, d, cap, None, None)
+    L.call("am_gfx950_prefill_linear", N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_QKV_ROPE_KV,
+                                                            (N.vp * 3)(p(qf), None, None), (N.i64 * 2)(0, 0), None, 0,
+                                                            C.pointer(r)), stream())
+    assert launched().startswith("gemm_i4<qkv_rope_kv,"), launched()
+    # the three nodes
+    q, k, v = empty((m, hq * d), torch.int16), empty((m, hkv * d), torch.int16), empty((m, hkv * d), torch.int16)
+    L.call("am_gfx950_prefill_linear", N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SPLIT,
+                                                            (N.vp * 3)(p(q), p(k), p(v)),
+                                                            (N.i64 * 2)(hq * d, (hq + hkv) * d)), stream())
+    L.call("am_gfx950_rope", N.RopeArgs(p(q), p(k), p(q), p(k), p(posd), p(cd), p(sd), m, hq, hkv, d, cap,
+                                        N.AM_DT_BF16), stream())
+    L.call("am_gfx950_kv_update", N.KvUpdateArgs(p(k), p(v), p(planes[2]), p(planes[3]), m, hkv, d, cap, 0,
+                                                 p(startd), N.AM_DT_BF16, None, None), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(qf, q), int((qf != q).sum())
+    assert torch.equal(planes[0], planes[2]) and torch.equal(planes[1], planes[3])
+    del keep
+
+
 def test_workspace_too_small_runs_unsplit():
     m, n, k = 512, 4096, 4096
     w, dw, keep = int4_weight(n, k, seed=261)
