@@ -67,6 +67,7 @@ struct BatchArgs {
   int32_t hq, hkv, d;
   int64_t cap, cbs;  // cache capacity (positions), elements between rows' caches
   KvRows kv;         // K/V row addressing (contiguous rows cbs apart, or paged)
+  int32_t row0;      // sequence index of token row 0 (a launch may cover a group of rows)
 };
 
 // k values per step (64 bytes of a weight row) and MFMAs per 16-byte lane slice
@@ -422,12 +423,12 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
             q[i] = f32_to_bf16_bits(o0);
             q[i + half] = f32_to_bf16_bits(o1);
           } else if (in_cache) {
-            uint16_t* kc = p.k_cache + p.kv.Row(b, head - p.hq, pos);
+            uint16_t* kc = p.k_cache + p.kv.Row(p.row0 + b, head - p.hq, pos);
             kc[i] = f32_to_bf16_bits(o0);
             kc[i + half] = f32_to_bf16_bits(o1);
           }
         } else if (in_cache) {
-          uint16_t* vc = p.v_cache + p.kv.Row(b, head - p.hq - p.hkv, pos);
+          uint16_t* vc = p.v_cache + p.kv.Row(p.row0 + b, head - p.hq - p.hkv, pos);
           vc[i] = f32_to_bf16_bits(y0);
           vc[i + half] = f32_to_bf16_bits(y1);
         }
@@ -495,6 +496,22 @@ am_status_code DispatchBatch(int32_t fmt, const BatchArgs& a, size_t lds, hipStr
 
 bool Aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
+// LDS of one block for `rows` token rows: the rows (bf16, padded by 16 bytes), the
+// per-wave partial tiles, 1/rms per row and, for INT4, the unit's group scales.
+size_t BatchLdsOf(const am_gfx950_weight& w, int64_t rows, int tpb) {
+  size_t b = (static_cast<size_t>(rows) * (w.k + 8) * 2 + 15) & ~size_t{15};
+  b += static_cast<size_t>(kBWaves) * tpb * 256 * 4 + kBWaves * 16 * 4;
+  if (w.format == AM_WF_INT4) b += static_cast<size_t>(2) * tpb * 16 * (w.k / 128 + 1) * 4;
+  return b;
+}
+
+// Most token rows (up to 16) whose block fits the 160 KB of LDS (0: not even one).
+int64_t BatchRowsFit(const am_gfx950_weight& w, int tpb) {
+  for (int64_t r = kBatchMaxRows; r >= 1; --r)
+    if (BatchLdsOf(w, r, tpb) <= 160 * 1024) return r;
+  return 0;
+}
+
 // Shape / format checks shared by every batched entry; fills the weight fields and
 // returns the dynamic LDS bytes through *lds.
 am_status_code PrepareBatch(const am_gfx950_weight& w, int64_t rows, const void* x, int64_t x_stride, int tpb,
@@ -511,13 +528,9 @@ am_status_code PrepareBatch(const am_gfx950_weight& w, int64_t rows, const void*
   AM_CHECK_ARG(Aligned16(w.data) && x != nullptr && Aligned16(x) && x_stride % 8 == 0 && x_stride >= w.k,
                "batched decode: weights and token rows must be 16-byte aligned");
   const int64_t S = w.k / ks;
-  size_t b = ((static_cast<size_t>(rows) * (w.k + 8) * 2 + 15) & ~size_t{15});
-  b += static_cast<size_t>(kBWaves) * tpb * 256 * 4 + kBWaves * 16 * 4;
-  if (w.format == AM_WF_INT4) {
+  if (w.format == AM_WF_INT4)
     AM_CHECK_ARG(tpb * 16 * S <= 4 * kBWaves * 64, "batched decode: int4 rows too long for the scale tile");
-    b += static_cast<size_t>(2) * tpb * 16 * (S + 1) * 4;
-  }
-  AM_CHECK_ARG(b <= 160 * 1024, "batched decode: token rows do not fit in LDS (rows x in_features too large)");
+  AM_CHECK_ARG(BatchRowsFit(w, tpb) >= 1, "batched decode: one token row does not fit in LDS (in_features too large)");
   a->x = static_cast<const uint16_t*>(x);
   a->x_stride = x_stride;
   a->w = static_cast<const uint8_t*>(w.data);
@@ -526,7 +539,25 @@ am_status_code PrepareBatch(const am_gfx950_weight& w, int64_t rows, const void*
   a->k = static_cast<int32_t>(w.k);
   a->rows = static_cast<int32_t>(rows);
   a->row_bytes = w.format == AM_WF_BF16 ? 2 * w.k : (w.format == AM_WF_INT8 ? w.k : w.k / 2);
-  *lds = b;
+  *lds = BatchLdsOf(w, std::min<int64_t>(rows, BatchRowsFit(w, tpb)), tpb);
+  return AM_STATUS_OK;
+}
+
+// Runs launch(args, lds) over groups of token rows small enough for one block's LDS
+// (every group re-reads the weights): the k = 14336 down projection of the 8B shape
+// fits 5 rows of 14336 bf16 values; shorter rows fit all 16.  off(args, g0) moves the
+// group's row pointers (token rows, outputs, residuals, positions) to row g0.
+template <class Launch, class Offset>
+am_status_code ForRowGroups(const BatchArgs& a, const am_gfx950_weight& w, int tpb, Launch launch, Offset off) {
+  const int64_t per = std::min<int64_t>(a.rows, BatchRowsFit(w, tpb));
+  for (int64_t g0 = 0; g0 < a.rows; g0 += per) {
+    BatchArgs ga = a;
+    ga.rows = static_cast<int32_t>(std::min<int64_t>(per, a.rows - g0));
+    ga.row0 = a.row0 + static_cast<int32_t>(g0);
+    ga.x = a.x + g0 * a.x_stride;
+    off(ga, g0);
+    if (auto st = launch(ga, BatchLdsOf(w, ga.rows, tpb)); st != AM_STATUS_OK) return st;
+  }
   return AM_STATUS_OK;
 }
 
@@ -557,13 +588,19 @@ am_status_code BatchLinear(const void* x, int64_t m, const am_gfx950_weight& w, 
   a.out_stride = w.n;
   a.out_f32 = out_dtype == AM_DT_F32 ? 1 : 0;
   a.units = static_cast<int32_t>(CeilDiv(w.n, 16));
+  auto off = [&](BatchArgs& g, int64_t g0) {
+    g.out = static_cast<uint8_t*>(out) + g0 * a.out_stride * (a.out_f32 ? 4 : 2);
+    if (g.residual != nullptr) g.residual = a.residual + g0 * a.res_stride;
+  };
   if (residual != nullptr) {
     AM_CHECK_ARG(out_dtype == AM_DT_BF16, "linear: residual needs out dtype == activation dtype");
     a.residual = static_cast<const uint16_t*>(residual);
     a.res_stride = w.n;
-    return DispatchBatch<kBResidual, false, 1>(w.format, a, lds, s);
+    return ForRowGroups(a, w, 1, [&](const BatchArgs& g, size_t l) {
+      return DispatchBatch<kBResidual, false, 1>(w.format, g, l, s); }, off);
   }
-  return DispatchBatch<kBStore, false, 1>(w.format, a, lds, s);
+  return ForRowGroups(a, w, 1, [&](const BatchArgs& g, size_t l) {
+    return DispatchBatch<kBStore, false, 1>(w.format, g, l, s); }, off);
 }
 
 am_status_code BatchQkv(const am_gfx950_fused_qkv_args* q, hipStream_t s) {
@@ -589,7 +626,12 @@ am_status_code BatchQkv(const am_gfx950_fused_qkv_args* q, hipStream_t s) {
   a.cbs = q->cache_batch_stride;
   if (auto st = MakeKvRows(q->pages, a.cbs, a.cap, q->hkv, q->head_dim, &a.kv); st != AM_STATUS_OK) return st;
   a.units = static_cast<int32_t>((q->hq + 2 * q->hkv) * (q->head_dim / 32));
-  return DispatchBatch<kBQkv, true, 2>(q->w_qkv.format, a, lds, s);
+  return ForRowGroups(a, q->w_qkv, 2, [&](const BatchArgs& g, size_t l) {
+    return DispatchBatch<kBQkv, true, 2>(q->w_qkv.format, g, l, s); },
+    [&](BatchArgs& g, int64_t g0) {
+      g.q_out = a.q_out + g0 * a.hq * a.d;
+      g.pos = a.pos + g0;
+    });
 }
 
 am_status_code BatchLinearResidual(const am_gfx950_fused_linear_residual_args* r, hipStream_t s) {
@@ -602,7 +644,12 @@ am_status_code BatchLinearResidual(const am_gfx950_fused_linear_residual_args* r
   a.residual = static_cast<const uint16_t*>(r->h);
   a.res_stride = r->w.n;
   a.units = static_cast<int32_t>(CeilDiv(r->w.n, 16));
-  return DispatchBatch<kBResidual, false, 1>(r->w.format, a, lds, s);
+  return ForRowGroups(a, r->w, 1, [&](const BatchArgs& g, size_t l) {
+    return DispatchBatch<kBResidual, false, 1>(r->w.format, g, l, s); },
+    [&](BatchArgs& g, int64_t g0) {
+      g.out = static_cast<uint16_t*>(a.out) + g0 * a.out_stride;
+      g.residual = a.residual + g0 * a.res_stride;
+    });
 }
 
 am_status_code BatchGateUp(const am_gfx950_fused_gate_up_args* gu, hipStream_t s) {
@@ -618,7 +665,9 @@ am_status_code BatchGateUp(const am_gfx950_fused_gate_up_args* gu, hipStream_t s
   a.out = gu->act_out;
   a.out_stride = gu->w_gate_up.n / 2;
   a.units = static_cast<int32_t>(gu->w_gate_up.n / 32);
-  return DispatchBatch<kBGateUp, true, 2>(gu->w_gate_up.format, a, lds, s);
+  return ForRowGroups(a, gu->w_gate_up, 2, [&](const BatchArgs& g, size_t l) {
+    return DispatchBatch<kBGateUp, true, 2>(gu->w_gate_up.format, g, l, s); },
+    [&](BatchArgs& g, int64_t g0) { g.out = static_cast<uint16_t*>(a.out) + g0 * a.out_stride; });
 }
 
 // RMSNorm -> lm_head logits (fp32) for rows token rows.
@@ -635,7 +684,9 @@ am_status_code BatchNormLogits(const am_gfx950_fused_lm_head_args* lm, hipStream
   a.out_stride = lm->w.n;
   a.out_f32 = 1;
   a.units = static_cast<int32_t>(CeilDiv(lm->w.n, 16));
-  return DispatchBatch<kBStore, true, 1>(lm->w.format, a, lds, s);
+  return ForRowGroups(a, lm->w, 1, [&](const BatchArgs& g, size_t l) {
+    return DispatchBatch<kBStore, true, 1>(lm->w.format, g, l, s); },
+    [&](BatchArgs& g, int64_t g0) { g.out = static_cast<float*>(a.out) + g0 * a.out_stride; });
 }
 
 }  // namespace am

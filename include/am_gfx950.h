@@ -104,7 +104,8 @@ am_status_code am_gfx950_rmsnorm(const am_gfx950_rmsnorm_args* args, void* hip_s
  * mode: 0 auto (bf16 activations with 2 <= m <= 16 -> batched decode GEMV when the
  * weight format allows it; otherwise m <= 8 -> GEMV, else MFMA GEMM), 1 GEMV per row,
  * 2 GEMM, 3 batched decode GEMV (m <= 16, bf16 activations, bf16/int8 weights or
- * int4 with group 128). */
+ * int4 with group 128; when m rows of k values do not fit one block's LDS the rows
+ * run in groups that do, each group reading the weights again). */
 typedef struct am_gfx950_linear_args {
   const void* x;
   int32_t x_dtype;

@@ -112,12 +112,22 @@ def test_linear_batched_rejects_unsupported():
     with pytest.raises(N.NativeError) as e:  # 17 rows
         L.call("am_gfx950_linear", N.LinearArgs(p(x), N.AM_DT_BF16, 17, dw, p(out), N.AM_DT_BF16, None, 3), stream())
     assert e.value.status == "INVALID_ARGUMENT"
+
+
+def test_linear_batched_row_groups():
+    """8 rows x 16384 bf16 values do not fit one block's LDS: the launch runs in row
+    groups (each re-reading the weights), with outputs and residuals at their rows."""
     w2, dw2, keep2 = weights(64, 16384, N.AM_WF_BF16, seed=34)
-    x2 = bf16_dev(O.bf16_bits(bf_rows(35, 0, 8, 16384)))
+    x2 = bf_rows(35, 0, 8, 16384)
+    x2d = bf16_dev(O.bf16_bits(x2))
+    ref = O.linear(x2, w2)
     out2 = empty((8, 64), torch.int16)
-    with pytest.raises(N.NativeError) as e:  # 8 rows x 16384 do not fit in LDS
-        L.call("am_gfx950_linear", N.LinearArgs(p(x2), N.AM_DT_BF16, 8, dw2, p(out2), N.AM_DT_BF16, None, 3), stream())
-    assert e.value.status == "INVALID_ARGUMENT"
+    L.call("am_gfx950_linear", N.LinearArgs(p(x2d), N.AM_DT_BF16, 8, dw2, p(out2), N.AM_DT_BF16, None, 3), stream())
+    rows_close(rd(out2), ref, TOL, "row groups")
+    res = bf_rows(36, 0, 8, 64)
+    rdv = bf16_dev(O.bf16_bits(res))
+    L.call("am_gfx950_linear", N.LinearArgs(p(x2d), N.AM_DT_BF16, 8, dw2, p(rdv), N.AM_DT_BF16, p(rdv), 3), stream())
+    rows_close(rd(rdv), rbf(res + rbf(ref)), TOL, "row groups residual")
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -293,6 +303,48 @@ def test_batched_session_matches_oracle_per_sequence(fmt, graph):
     L.call("am_session_logits", s, got.ctypes.data)
     for r in range(B):
         assert int(out[r, 2]) == O.argmax(got[r])
+    for o in orcs:
+        o.close()
+    L.am_session_destroy(s)
+    L.am_model_destroy(m)
+    rt.close()
+
+
+def test_batched_session_rows_in_groups_match_oracle():
+    """Eight sequences with a 14336-wide FFN: the down projection's token rows (8 x 14336
+    bf16) exceed one block's LDS, so its batched launches run in row groups (5 + 3),
+    each re-reading the weights; every sequence's logits still match its own oracle."""
+    cfg = dict(O.TINY, act="bf16", weight_format=N.AM_WF_INT4, ffn=14336, vocab=4096, num_layers=2, max_tokens=48)
+    B, seed = 8, 9
+    rt = _Rt()
+    mc = N.ModelConfig(cfg["num_layers"], cfg["hidden"], cfg["num_q_heads"], cfg["num_kv_heads"], cfg["head_dim"],
+                       cfg["ffn"], cfg["vocab"], cfg["rms_eps"], cfg["rope_theta"], N.AM_DT_BF16, N.AM_WF_INT4, 128,
+                       cfg["max_tokens"], 8)
+    m = N.vp()
+    L.call("am_model_create_synthetic", rt.rt, C.byref(mc), seed, C.byref(m))
+    s = N.vp()
+    L.call("am_session_open", m, C.byref(N.SessionOptions(1, 1, B)), C.byref(s))
+    prompts = [O.token_ids(seed, 20 + r, cfg["vocab"], 3 + 2 * r) for r in range(B)]
+    orcs = [O.OracleModel(cfg, seed) for _ in range(B)]
+    V = cfg["vocab"]
+    got = np.zeros((B, V), np.float32)
+    toks = []
+    for r in range(B):
+        first = N.i64()
+        L.call("am_session_prefill_row", s, r, prompts[r].ctypes.data, prompts[r].size, C.byref(first))
+        orcs[r].forward(prompts[r], 0)
+        toks.append(int(first.value))
+    posn = [pr.size for pr in prompts]
+    for step in range(3):
+        out = np.zeros((B, 1), np.int64)
+        L.call("am_session_decode", s, 1, out.ctypes.data)
+        L.call("am_session_logits", s, got.ctypes.data)
+        for r in range(B):
+            ref = orcs[r].forward(np.array([toks[r]], np.int64), posn[r])
+            close(got[r], ref, TOL, f"decode step {step} seq {r}")
+            assert int(out[r, 0]) == O.argmax(got[r])
+            toks[r] = int(out[r, 0])
+            posn[r] += 1
     for o in orcs:
         o.close()
     L.am_session_destroy(s)
