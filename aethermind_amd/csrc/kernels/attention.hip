@@ -679,180 +679,252 @@ __global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnAr
 
 // ---- prefill / chunked prefill: many query rows, bf16, both products on MFMA ----
 //
-// grid = (ceil(seq / QB), kv_heads, batch) with kPreWaves-wave blocks.  Each wave owns
-// 16 query columns: 16/G consecutive query positions x the G heads of the kv group
-// (column j = position j / G, head j % G).  The block walks the key positions up to its
-// last query's position in tiles of 32, each K and V tile loaded once into LDS
-// (double-buffered: tile t+1 is fetched into registers while tile t is consumed) and
-// shared by the block's waves.  Per tile a wave computes S^T = K Q^T (A = 16 K rows
-// from LDS, B = its 16 query columns held in registers), masks keys after each query's
-// position, updates the base-2 online softmax of its columns exactly as the decode
-// kernel does, and adds P V on MFMA (P as bf16 hi + lo, V gathered by column from the
-// padded LDS tile).  Waves own distinct queries, so there is no merge: each wave
-// normalises its columns and writes them.
-constexpr int kPreWaves = 4;
+// One block owns QB consecutive query positions of one (row, kv head): NW waves, each
+// with CG column groups of 16 MFMA columns (16/G positions x the G query heads of the
+// kv group), so a K/V load serves G heads and NW*CG*16/G positions.  The block walks
+// the key positions up to its last query's position in tiles of 32:
+//   * Tile t+2 is loaded into registers while tile t is computed and tile t+1 waits in
+//     LDS (two-deep prefetch; a tile is one cache block lookup, tiles start at
+//     multiples of 32).  K is stored row-major and V transposed (V^T[d][key]); both are
+//     XOR-swizzled in 16-byte slots, so the operand reads below are conflict-free.
+//   * Scores S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the key rows of score tile tt
+//     permuted: MFMA row i is key 8(i/4) + 4 tt + i%4.  Lane (j, h) then holds the
+//     scores of query column j for keys 8h .. 8h+7 (tile tt = 0 gives 8h..8h+3, tt = 1
+//     gives 8h+4..8h+7): exactly the k slots of its A operand in P V, and its V operand
+//     for output tile dt is V^T[16 dt + j][8h .. 8h+7], one 16-byte LDS read.  K and V
+//     operands are read once per wave and shared by the wave's column groups.
+//   * The causal mask is per column (key <= the column's position, key < the chunk
+//     end), the online softmax is base 2 per column (scores pre-scaled by
+//     log2(e)/sqrt(d)), P is split into bf16 hi + lo for the P V product.  Waves own
+//     distinct queries, so there is no merge: each wave normalises its columns and
+//     writes them.
+// Blocks are numbered kv head fastest: block b runs on XCD b % 8, so with 8 kv heads
+// every block of one head shares one XCD's L2 (the head's K/V is read from HBM once),
+// and the query blocks of a head are taken last-first (the longest causal ranges start
+// first).
+constexpr int kPreTile = 32;
 
-template <int D, int G>
-__global__ __launch_bounds__(kPreWaves * 64) void attention_prefill_kernel(AttnArgs p) {
-  constexpr int NW = kPreWaves, NT = NW * 64;
-  constexpr int QT = 16 / G;               // query positions per wave
-  constexpr int QB = NW * QT;              // query positions per block
+// 16-byte slot of K row `key` holding dims 8s .. 8s+7 (s ^ this): the 16 rows of one
+// score MFMA operand fall into 16 distinct slots.
+template <int D>
+__device__ __forceinline__ int kswz(int key) {
+  if constexpr (D == 128)
+    return (key & 3) | ((key >> 3) << 2);
+  else
+    return ((key >> 1) & 1) | ((key >> 3) << 1);
+}
+// 16-byte slot of V^T row d holding keys 8s .. 8s+7 (s ^ this)
+__device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
+
+template <int D, int G, int CG, int NW>
+__global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) {
+  constexpr int NT = NW * 64;
+  constexpr int QT = 16 / G;               // query positions per column group
+  constexpr int QB = NW * CG * QT;         // query positions per block
   constexpr int KK = D / 32;               // MFMA k steps of one score tile
   constexpr int DT = D / 16;               // 16-wide output tiles
-  constexpr int KR = D + 8;                // padded LDS row (bf16) of the K and V tiles
-  constexpr int TP = 32;                   // key positions per tile
+  constexpr int TP = kPreTile;             // key positions per tile
   constexpr int PR = D / 8;                // 16-byte pieces per cache row
   constexpr int PCH = TP * PR / NT;        // pieces per thread per tile (K and V each)
   static_assert(PCH >= 1 && TP * PR % NT == 0, "tile pieces must divide over the block");
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-  __shared__ __align__(16) uint16_t sk[2][TP * KR];
-  __shared__ __align__(16) uint16_t sv[2][TP * KR];
+  __shared__ __align__(16) uint16_t sk[2][TP * D];   // K[key][d], 16-byte slots swizzled
+  __shared__ __align__(16) uint16_t sv[2][D * TP];   // V^T[d][key], 16-byte slots swizzled
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, h = lane >> 4;
-  const int64_t b = blockIdx.z, g = blockIdx.y;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * QB;
+  // block -> (row, q block, kv head): kv head fastest, q blocks last-first
+  const int64_t nqb = (p.seq + QB - 1) / QB;
+  const int64_t L = blockIdx.x;
+  const int64_t g = L % p.hkv;
+  const int64_t rest = L / p.hkv;
+  const int64_t b = rest / nqb;
+  const int64_t s0 = (nqb - 1 - rest % nqb) * QB;
   const int64_t start = p.start_dev != nullptr ? p.start_dev[b] : p.start;
-  // this lane's query column j: position s, absolute position qpos (-1: no query)
-  const int64_t s = s0 + wave * QT + j / G;
-  const int64_t qpos = s < p.seq ? start + s : -1;
   const int64_t s_last = s0 + QB - 1 < p.seq - 1 ? s0 + QB - 1 : p.seq - 1;
   int64_t kend = start + s_last + 1;  // keys the block needs: [0, kend)
   if (kend > p.cap) kend = p.cap;
   const int64_t ntiles = (kend + TP - 1) / TP;
 
-  // B operand: query column j at d = 32 kk + 8 h .. +8 (zero for missing queries)
-  bf16x8_t qop[KK];
-  {
+  // column group c of this wave: positions s0 + (wave * CG + c) * QT + j / G; its score
+  // B operand (query column j at d = 32 kk + 8 h .. +8; zero for missing queries)
+  int64_t qpos[CG];
+  bf16x8_t qop[CG][KK];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int64_t s = s0 + (wave * CG + c) * QT + j / G;
+    qpos[c] = s < p.seq ? start + s : -1;
     const int64_t sq = s < p.seq ? s : p.seq - 1;
     const uint16_t* qp =
         static_cast<const uint16_t*>(p.q) + ((b * p.seq + sq) * p.hq + g * G + j % G) * D + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       uint4 v = *reinterpret_cast<const uint4*>(qp + 32 * kk);
-      if (qpos < 0) v = make_uint4(0, 0, 0, 0);
-      qop[kk] = __builtin_bit_cast(bf16x8_t, v);
+      if (qpos[c] < 0) v = make_uint4(0, 0, 0, 0);
+      qop[c][kk] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
   const uint16_t* kc0 = static_cast<const uint16_t*>(p.kc);
   const uint16_t* vc0 = static_cast<const uint16_t*>(p.vc);
   const int64_t last_row = kend - 1;
-  uint4 kr[PCH], vr[PCH];
-  // piece c of the thread: tile row tid / PR + c * NT / PR, 8 columns at 8 * (tid % PR);
+  // piece c of the thread: tile row (tid / PR + c * NT / PR), dims 8 (tid % PR) .. +8;
   // a tile's 32 rows are contiguous from its first row (one offset lookup per tile)
-  auto load_tile = [&](int64_t t) {
+  typedef uint4 Pieces[2][PCH];
+  Pieces ra, rb;
+  auto load_tile = [&](Pieces& r, int64_t t) {
     const int64_t off = p.kv.Row(b, g, t * TP);
     const uint32_t lim = static_cast<uint32_t>(min(last_row - t * TP, int64_t{TP - 1}));
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
-      const uint32_t r = min(static_cast<uint32_t>(tid / PR + c * (NT / PR)), lim);
-      kr[c] = *reinterpret_cast<const uint4*>(kc0 + off + (r * D + 8 * (tid % PR)));
-      vr[c] = *reinterpret_cast<const uint4*>(vc0 + off + (r * D + 8 * (tid % PR)));
+      const uint32_t row = min(static_cast<uint32_t>(tid / PR + c * (NT / PR)), lim);
+      r[0][c] = *reinterpret_cast<const uint4*>(kc0 + off + (row * D + 8 * (tid % PR)));
+      r[1][c] = *reinterpret_cast<const uint4*>(vc0 + off + (row * D + 8 * (tid % PR)));
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const Pieces& r, int buf) {
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
-      const int row = tid / PR + c * (NT / PR);
-      *reinterpret_cast<uint4*>(&sk[buf][row * KR + 8 * (tid % PR)]) = kr[c];
-      *reinterpret_cast<uint4*>(&sv[buf][row * KR + 8 * (tid % PR)]) = vr[c];
+      const int key = tid / PR + c * (NT / PR), sl = tid % PR;
+      *reinterpret_cast<uint4*>(&sk[buf][key * D + 8 * (sl ^ kswz<D>(key))]) = r[0][c];
+      const uint32_t w[4] = {r[1][c].x, r[1][c].y, r[1][c].z, r[1][c].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * sl + e;
+        sv[buf][d * TP + 8 * ((key >> 3) ^ vswz(d)) + (key & 7)] =
+            static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu));
+      }
     }
   };
 
-  float m_run = -INFINITY, l_run = 0.0f;
-  f32x4_t o[DT];  // O[column 4h + r][16 dt + j]
+  // the wave's columns: all present, and the smallest position among them
+  const int64_t wave_s0 = s0 + wave * CG * QT;
+  const bool wave_full = wave_s0 + CG * QT - 1 < p.seq;
+  const int64_t wave_qmin = start + wave_s0;
+  float m_run[CG], l_run[CG];
+  f32x4_t o[CG][DT];  // O[column 4h + r][16 dt + j]
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < CG; ++c) {
+    m_run[c] = -INFINITY;
+    l_run[c] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[c][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto compute = [&](int buf, int64_t t) {
     const uint16_t* kt = sk[buf];
     const uint16_t* vt = sv[buf];
-    float sc[2][4];
+    f32x4_t acc[CG][2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const int key = 8 * (j >> 2) + 4 * tt + (j & 3);  // this lane's A row
+#pragma unroll
+      for (int c = 0; c < CG; ++c) acc[c][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const uint4 a = *reinterpret_cast<const uint4*>(kt + (16 * tt + j) * KR + 32 * kk + 8 * h);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), qop[kk], acc, 0, 0, 0);
-      }
+        const uint4 a = *reinterpret_cast<const uint4*>(kt + key * D + 8 * ((4 * kk + h) ^ kswz<D>(key)));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = t * TP + 16 * tt + 4 * h + r;
-        sc[tt][r] = key <= qpos && key < kend ? acc[r] * p.scale : -INFINITY;
+        for (int c = 0; c < CG; ++c)
+          acc[c][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), qop[c][kk], acc[c][tt],
+                                                               0, 0, 0);
       }
     }
-    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-    bm = fmaxf(bm, xor_partner<16>(bm, lane));
-    bm = fmaxf(bm, xor_partner<32>(bm, lane));
-    const float mn = fmaxf(m_run, bm);
-    const float c = mn == -INFINITY ? 1.0f : exp2f(m_run - mn);
-    float pr[2][4];
-    float sum = 0.0f;
+    // Tiles wholly below every column's position and the chunk end need no mask (all
+    // but the last one or two tiles of a block); the test is wave-uniform.
+    const bool full = wave_full && t * TP + TP - 1 <= wave_qmin && t * TP + TP <= kend;
+    const int32_t tbase = static_cast<int32_t>(t * TP) + 8 * h;
+    bf16x8_t phi[CG], plo[CG];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int c = 0; c < CG; ++c) {
+      // lane (j, h), slot e = 4 tt + r: key 8h + e of query column j
+      float sc[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[tt][r] = sc[tt][r] == -INFINITY ? 0.0f : exp2f(sc[tt][r] - mn);
-        sum += pr[tt][r];
+      for (int e = 0; e < 8; ++e) sc[e] = acc[c][e >> 2][e & 3] * p.scale;
+      if (!full) {
+        const int32_t lim = static_cast<int32_t>(min(qpos[c], kend - 1));  // keys <= lim are live
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (tbase + e > lim) sc[e] = -INFINITY;
       }
-    l_run = fmaf(l_run, c, sum);
-    m_run = mn;
+      float bm = sc[0];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float cr = __shfl(c, 16 * h + 4 * h + r);
+      for (int e = 1; e < 8; ++e) bm = fmaxf(bm, sc[e]);
+      bm = fmaxf(bm, xor_partner<16>(bm, lane));
+      bm = fmaxf(bm, xor_partner<32>(bm, lane));
+      const float mn = fmaxf(m_run[c], bm);
+      // Rescale only when some column's maximum grew (multiplying by exp2(0) = 1 is
+      // exact, so skipping it changes nothing); after the first tiles this is rare.
+      if (__builtin_amdgcn_ballot_w64(mn > m_run[c]) != 0) {
+        const float cf = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[c] - mn);
+        l_run[c] *= cf;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][r] *= cr;
-    }
-    bf16x8_t phi, plo;
+        for (int r = 0; r < 4; ++r) {
+          const float cr = __shfl(cf, 16 * h + 4 * h + r);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = pr[e >> 2][e & 3];
-      const __bf16 hb = static_cast<__bf16>(v);
-      phi[e] = hb;
-      plo[e] = static_cast<__bf16>(v - static_cast<float>(hb));
+          for (int dt = 0; dt < DT; ++dt) o[c][dt][r] *= cr;
+        }
+      }
+      m_run[c] = mn;
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = sc[e] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[e] - mn);
+        sum += v;
+        const __bf16 hb = static_cast<__bf16>(v);
+        phi[c][e] = hb;
+        plo[c][e] = static_cast<__bf16>(v - static_cast<float>(hb));
+      }
+      l_run[c] += sum;
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      uint32_t w[4];
+      const int d = 16 * dt + j;
+      const bf16x8_t vop =
+          __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(vt + d * TP + 8 * (h ^ vswz(d))));
 #pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int e0 = 2 * e2, e1 = 2 * e2 + 1;
-        const int r0 = 16 * (e0 >> 2) + 4 * h + (e0 & 3), r1 = 16 * (e1 >> 2) + 4 * h + (e1 & 3);
-        w[e2] = static_cast<uint32_t>(vt[r0 * KR + 16 * dt + j]) | (static_cast<uint32_t>(vt[r1 * KR + 16 * dt + j]) << 16);
+      for (int c = 0; c < CG; ++c) {
+        o[c][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[c], vop, o[c][dt], 0, 0, 0);
+        o[c][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[c], vop, o[c][dt], 0, 0, 0);
       }
-      const bf16x8_t vop = __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop, o[dt], 0, 0, 0);
     }
   };
 
-  load_tile(0);
-  store_tile(0);
+  // tile t: in LDS buffer t & 1; its registers were loaded two iterations earlier
+  load_tile(ra, 0);
+  if (ntiles > 1) load_tile(rb, 1);
+  store_tile(ra, 0);
   __syncthreads();
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1);
-    compute(static_cast<int>(t & 1), t);
-    if (more) store_tile(static_cast<int>((t + 1) & 1));
+  int64_t t = 0;
+  for (; t + 1 < ntiles; t += 2) {
+    // even tile t in buffer 0; rb holds tile t + 1
+    if (t + 2 < ntiles) load_tile(ra, t + 2);
+    compute(0, t);
+    store_tile(rb, 1);
+    __syncthreads();
+    if (t + 3 < ntiles) load_tile(rb, t + 3);
+    compute(1, t + 1);
+    if (t + 2 < ntiles) store_tile(ra, 0);
     __syncthreads();
   }
+  if (t < ntiles) compute(0, t);
 
   // column j's sum over the four lane rows, then normalise and write
-  l_run += xor_partner<16>(l_run, lane);
-  l_run += xor_partner<32>(l_run, lane);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int q = 4 * h + r;  // this lane's output column
-    const float lq = __shfl(l_run, 16 * h + q);
-    const int64_t sq = s0 + wave * QT + q / G;
-    if (sq >= p.seq) continue;
-    uint16_t* out = static_cast<uint16_t*>(p.out) + ((b * p.seq + sq) * p.hq + g * G + q % G) * D;
+  for (int c = 0; c < CG; ++c) {
+    float lr = l_run[c];
+    lr += xor_partner<16>(lr, lane);
+    lr += xor_partner<32>(lr, lane);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) out[16 * dt + j] = f32_to_bf16_bits(lq > 0.0f ? o[dt][r] / lq : 0.0f);
+    for (int r = 0; r < 4; ++r) {
+      const int q = 4 * h + r;  // this lane's output column
+      const float lq = __shfl(lr, 16 * h + q);
+      const int64_t sq = s0 + (wave * CG + c) * QT + q / G;
+      if (sq >= p.seq) continue;
+      uint16_t* out = static_cast<uint16_t*>(p.out) + ((b * p.seq + sq) * p.hq + g * G + q % G) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) out[16 * dt + j] = f32_to_bf16_bits(lq > 0.0f ? o[c][dt][r] / lq : 0.0f);
+    }
   }
 }
 
@@ -871,14 +943,36 @@ void LaunchTimed(K kernel, dim3 grid, dim3 block, hipStream_t s, const AttnArgs&
   }
 }
 
+template <int D, int G, int CG, int NW>
+void LaunchPrefillShape(int64_t blocks, const AttnArgs& a, hipStream_t s) {
+  constexpr int QB = NW * CG * (16 / G);
+  RecordLaunch(blocks, NW * 64, 0, "attention_prefill<d=%d,g=%d,qb=%d>", D, G, QB);
+  LaunchTimed(attention_prefill_kernel<D, G, CG, NW>, dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), s, a);
+}
+
+// Query positions per block: the largest of 16/G x {4, 8, 16} that still gives every CU
+// a block (fewer re-reads of K/V per query), else the smallest.
+template <int D, int G>
+void LaunchPrefillG(const AttnArgs& a, int64_t batch, hipStream_t s) {
+  const int64_t per = a.hkv * batch, cus = DeviceCUs();
+  auto blocks = [&](int64_t qb) { return CeilDiv(a.seq, qb) * per; };
+  constexpr int QT = 16 / G;
+  // (a 512-thread block needs a whole 16-byte piece per thread per tile: D = 128)
+  if (D == 128 && blocks(16 * QT) >= cus)
+    LaunchPrefillShape<D, G, 2, D == 128 ? 8 : 4>(blocks(16 * QT), a, s);
+  else if (blocks(8 * QT) >= cus)
+    LaunchPrefillShape<D, G, 2, 4>(blocks(8 * QT), a, s);
+  else
+    LaunchPrefillShape<D, G, 1, 4>(blocks(4 * QT), a, s);
+}
+
 template <int D>
-am_status_code LaunchPrefill(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
-  RecordLaunch(GridBlocks(grid), kPreWaves * 64, 0, "attention_prefill<d=%d,g=%d>", D, static_cast<int>(G));
+am_status_code LaunchPrefill(int64_t G, int64_t batch, const AttnArgs& a, hipStream_t s) {
   switch (G) {
-    case 1: LaunchTimed(attention_prefill_kernel<D, 1>, grid, dim3(kPreWaves * 64), s, a); break;
-    case 2: LaunchTimed(attention_prefill_kernel<D, 2>, grid, dim3(kPreWaves * 64), s, a); break;
-    case 4: LaunchTimed(attention_prefill_kernel<D, 4>, grid, dim3(kPreWaves * 64), s, a); break;
-    case 8: LaunchTimed(attention_prefill_kernel<D, 8>, grid, dim3(kPreWaves * 64), s, a); break;
+    case 1: LaunchPrefillG<D, 1>(a, batch, s); break;
+    case 2: LaunchPrefillG<D, 2>(a, batch, s); break;
+    case 4: LaunchPrefillG<D, 4>(a, batch, s); break;
+    case 8: LaunchPrefillG<D, 8>(a, batch, s); break;
     default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
   }
   AM_RETURN_IF_LAUNCH_FAILED("attention");
@@ -1063,10 +1157,7 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
   if (a->dtype == AM_DT_BF16) {
     // prefill: MFMA kernel, one block per (16 query columns per wave) x kv head x row
     AM_CHECK_ARG(a->capacity * a->head_dim < (int64_t{1} << 31), "attention: cache too large for 32-bit offsets");
-    const int64_t qb = kPreWaves * (16 / G);
-    const dim3 grid(static_cast<unsigned>(CeilDiv(a->seq, qb)), static_cast<unsigned>(a->hkv),
-                    static_cast<unsigned>(batch));
-    return a->head_dim == 128 ? LaunchPrefill<128>(G, grid, p, s) : LaunchPrefill<64>(G, grid, p, s);
+    return a->head_dim == 128 ? LaunchPrefill<128>(G, batch, p, s) : LaunchPrefill<64>(G, batch, p, s);
   }
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   p.min_per_split = static_cast<int32_t>(kMinPerSplit);

@@ -272,7 +272,7 @@ def test_prefill_attention_chunk_2048_at_6144_cap_32768():
                         p(ws), nb)
     L.call("am_gfx950_attention", a, stream())
     k = launched()
-    assert k.startswith("attention_prefill<d=128,g=4>"), k
+    assert k == "attention_prefill<d=128,g=4,qb=64>", k  # 64 positions per block at 2048 rows
     got = rd(out)
     kf = np.zeros((HKV, cap, D), np.float32)
     vf = np.zeros((HKV, cap, D), np.float32)

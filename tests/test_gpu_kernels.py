@@ -434,6 +434,42 @@ def test_attention_prefill_mfma(d, heads, chunk):
         assert not bad.any(), (r, np.argwhere(bad)[:8])
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("g", [1, 2, 4, 8])
+@pytest.mark.parametrize("wide", [False, True])
+def test_attention_prefill_block_shapes(d, g, wide):
+    """Each prefill block shape (16/G positions x {4, 8, 16} column groups per block:
+    the launcher takes the largest that still gives every CU a block) against the
+    oracle, on sampled rows of two batch rows at their own start positions: rows at
+    both ends of a block, of the chunk and of a 32-key tile."""
+    hkv, B = 4, 2
+    hq = g * hkv
+    qt = 16 // g
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    m = 16 if wide else 8
+    S = -(-cus // (hkv * B)) * m * qt  # exactly enough blocks of m * qt positions
+    want_qb = 16 * qt if (wide and d == 128) else 8 * qt
+    starts = [40, 157]
+    cap = max(starts) + S + 16
+    rng = np.random.default_rng(300 + d + g + wide)
+    q = O.round_bf16(rng.standard_normal((B, S, hq * d), dtype=np.float32))
+    kc = O.round_bf16(rng.standard_normal((B, hkv, cap, d), dtype=np.float32))
+    vc = O.round_bf16(rng.standard_normal((B, hkv, cap, d), dtype=np.float32))
+    qd, kd, vd = bf16_dev(O.bf16_bits(q)), bf16_dev(O.bf16_bits(kc)), bf16_dev(O.bf16_bits(vc))
+    out = empty((B, S, hq * d), torch.int16)
+    posd = dev(np.array(starts, np.int64))
+    a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), S, hq, hkv, d, cap, 0, p(posd), B, hkv * cap * d, 1, 0, None, 0)
+    L.call("am_gfx950_attention", a, stream())
+    k = N.last_launch().kernel.decode()
+    assert k == f"attention_prefill<d={d},g={g},qb={want_qb}>", k
+    got = O.bf16_to_f32(bits_host(out))
+    rows = sorted({0, 1, 31, 32, want_qb - 1, want_qb, S // 2 + 5, S - want_qb, S - 2, S - 1})
+    for r in range(B):
+        for s_ in rows:
+            ref = O.attention(np.ascontiguousarray(q[r, s_:s_ + 1]), kc[r], vc[r], 1, hq, hkv, d, cap, starts[r] + s_)
+            close(got[r, s_], ref[0], TOL["bf16"], f"prefill row {r} position {s_} (qb {want_qb})")
+
+
 def test_attention_special_cases():
     # one position -> out = V row; identical keys -> out = mean of V over the window
     hq, hkv, d, cap = 4, 1, 64, 64
