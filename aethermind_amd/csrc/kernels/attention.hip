@@ -769,8 +769,12 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
   const uint16_t* kc0 = static_cast<const uint16_t*>(p.kc);
   const uint16_t* vc0 = static_cast<const uint16_t*>(p.vc);
   const int64_t last_row = kend - 1;
-  // piece c of the thread: tile row (tid / PR + c * NT / PR), dims 8 (tid % PR) .. +8;
-  // a tile's 32 rows are contiguous from its first row (one offset lookup per tile)
+  // K piece c of the thread: tile row (tid / PR + c * NT / PR), dims 8 (tid % PR) .. +8
+  // (a wave's lanes cover whole rows: row-major 16-byte LDS stores).  V piece c: key
+  // q % 32, dims 8 (q / 32) .. +8 for q = c * NT + tid (a wave's lanes cover all 32 keys
+  // of two 8-dim blocks, so the transposed 2-byte stores of one instruction fall into
+  // two V^T rows rather than sixteen).  A tile's 32 rows are contiguous from its first
+  // row (one offset lookup per tile).
   typedef uint4 Pieces[2][PCH];
   Pieces ra, rb;
   auto load_tile = [&](Pieces& r, int64_t t) {
@@ -780,7 +784,9 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
     for (int c = 0; c < PCH; ++c) {
       const uint32_t row = min(static_cast<uint32_t>(tid / PR + c * (NT / PR)), lim);
       r[0][c] = *reinterpret_cast<const uint4*>(kc0 + off + (row * D + 8 * (tid % PR)));
-      r[1][c] = *reinterpret_cast<const uint4*>(vc0 + off + (row * D + 8 * (tid % PR)));
+      const int q = c * NT + tid;
+      const uint32_t vrow = min(static_cast<uint32_t>(q % TP), lim);
+      r[1][c] = *reinterpret_cast<const uint4*>(vc0 + off + (vrow * D + 8 * (q / TP)));
     }
   };
   auto store_tile = [&](const Pieces& r, int buf) {
@@ -788,11 +794,12 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
     for (int c = 0; c < PCH; ++c) {
       const int key = tid / PR + c * (NT / PR), sl = tid % PR;
       *reinterpret_cast<uint4*>(&sk[buf][key * D + 8 * (sl ^ kswz<D>(key))]) = r[0][c];
+      const int q = c * NT + tid, vkey = q % TP, vsl = q / TP;
       const uint32_t w[4] = {r[1][c].x, r[1][c].y, r[1][c].z, r[1][c].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 8 * sl + e;
-        sv[buf][d * TP + 8 * ((key >> 3) ^ vswz(d)) + (key & 7)] =
+        const int d = 8 * vsl + e;
+        sv[buf][d * TP + 8 * ((vkey >> 3) ^ vswz(d)) + (vkey & 7)] =
             static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu));
       }
     }
