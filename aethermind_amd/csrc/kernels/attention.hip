@@ -431,9 +431,12 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
 
 // ---- decode: one query position per row, bf16 q and cache, both products on MFMA ----
 //
-// grid = (splits, kv_heads, batch).  A block of kDecWaves waves owns one (row, kv head)
-// and a slice of positions; wave w takes the 32-position steps w, w + kDecWaves, ...
-// of the slice, with the next step's K and V loads in flight while a step computes.
+// grid = (splits, kv_heads, batch).  A block of NW waves owns one (row, kv head) and a
+// slice of positions; wave w takes the 32-position steps w, w + NW, ... of the slice,
+// with the next step's K and V loads in flight while a step computes.  NW = 4 (one
+// wave per SIMD, 264 registers) unless the grid already gives every CU a block
+// (batched long contexts): then NW = 8 within 236 registers, two waves per SIMD and
+// twice the K/V loads in flight per CU, the extra waves merged in LDS.
 // No K or V byte is staged in LDS: their MFMA operands are built in the registers of
 // the lane that loaded them.
 //   * Scores: S^T = K Q^T on v_mfma_f32_16x16x32_bf16.  A = 16 cache rows (position
@@ -463,9 +466,10 @@ constexpr int kDecWaves = 4;
 constexpr int32_t kDecMinPerSplit = 128;
 constexpr int kDecMaxSplits = 8;
 
-template <int D, int G>
-__global__ __launch_bounds__(kDecWaves * 64) void attention_decode_kernel(AttnArgs p) {
-  constexpr int NW = kDecWaves;
+// NW = 8: two waves per SIMD (236 VGPRs, no spills, against 264 for the 4-wave block,
+// which holds one wave per SIMD), for grids that already give every CU a block.
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void attention_decode_kernel(AttnArgs p) {
   constexpr int KK = D / 32;  // MFMA k steps of one score tile
   constexpr int CW = D / 16;  // V columns per lane = output tiles
   constexpr int VW = CW / 2;  // 32-bit words of one lane's V row piece
@@ -995,16 +999,20 @@ int ChooseSplits(int64_t seq, int64_t cap, int32_t requested) {
   return static_cast<int>(s);
 }
 
-template <int D>
+template <int D, int NW>
 am_status_code LaunchDecode(int64_t G, dim3 grid, const AttnArgs& a, hipStream_t s) {
-  RecordLaunch(GridBlocks(grid), kDecWaves * 64, 0, "attention_decode<d=%d,g=%d,splits=%u>", D, static_cast<int>(G),
-               grid.x);
-  const dim3 block(kDecWaves * 64);
+  if constexpr (NW == kDecWaves)
+    RecordLaunch(GridBlocks(grid), NW * 64, 0, "attention_decode<d=%d,g=%d,splits=%u>", D, static_cast<int>(G),
+                 grid.x);
+  else
+    RecordLaunch(GridBlocks(grid), NW * 64, 0, "attention_decode<d=%d,g=%d,splits=%u,waves=%d>", D,
+                 static_cast<int>(G), grid.x, NW);
+  const dim3 block(NW * 64);
   switch (G) {
-    case 1: LaunchTimed(attention_decode_kernel<D, 1>, grid, block, s, a); break;
-    case 2: LaunchTimed(attention_decode_kernel<D, 2>, grid, block, s, a); break;
-    case 4: LaunchTimed(attention_decode_kernel<D, 4>, grid, block, s, a); break;
-    case 8: LaunchTimed(attention_decode_kernel<D, 8>, grid, block, s, a); break;
+    case 1: LaunchTimed(attention_decode_kernel<D, 1, NW>, grid, block, s, a); break;
+    case 2: LaunchTimed(attention_decode_kernel<D, 2, NW>, grid, block, s, a); break;
+    case 4: LaunchTimed(attention_decode_kernel<D, 4, NW>, grid, block, s, a); break;
+    case 8: LaunchTimed(attention_decode_kernel<D, 8, NW>, grid, block, s, a); break;
     default: return SetLastError(AM_STATUS_UNIMPLEMENTED, "attention: q heads per kv head must be 1, 2, 4 or 8");
   }
   AM_RETURN_IF_LAUNCH_FAILED("attention");
@@ -1159,7 +1167,12 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
     p.min_per_split = a->num_splits > 0 ? 32 : kDecMinPerSplit;
     if (a->num_splits <= 0 && p.splits > kDecMaxSplits) p.splits = kDecMaxSplits;
     const dim3 grid(static_cast<unsigned>(p.splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch));
-    return a->head_dim == 128 ? LaunchDecode<128>(G, grid, p, s) : LaunchDecode<64>(G, grid, p, s);
+    // Grids that give every CU a block (batched long contexts) run 8-wave blocks, two
+    // waves per SIMD: twice the K/V loads in flight per CU, merged in LDS.
+    if (a->num_splits <= 0 && GridBlocks(grid) >= DeviceCUs())
+      return a->head_dim == 128 ? LaunchDecode<128, 8>(G, grid, p, s) : LaunchDecode<64, 8>(G, grid, p, s);
+    return a->head_dim == 128 ? LaunchDecode<128, kDecWaves>(G, grid, p, s)
+                              : LaunchDecode<64, kDecWaves>(G, grid, p, s);
   }
   if (a->dtype == AM_DT_BF16) {
     // prefill: MFMA kernel, one block per (16 query columns per wave) x kv head x row

@@ -24,6 +24,7 @@ if not torch.cuda.is_available():  # pragma: no cover
 import aethermind_amd.native as N  # noqa: E402
 import oracle_lib as O  # noqa: E402
 from gpu_util import bf16_dev, bits_host, dev, empty, host, p, pack_weight, stream, zeros  # noqa: E402
+from test_gpu_decode_shapes import launched  # noqa: E402
 
 L = N.lib()
 TOL = 2e-2
@@ -220,11 +221,14 @@ def test_fused_lm_head_batched_argmax_and_state():
     assert not host(ws)[:256].any(), "argmax tickets must be left zero"
 
 
-def test_attention_decode_long_context_batch4():
+@pytest.mark.parametrize("B", [4, 2])
+def test_attention_decode_long_context_batch4(B):
     """The long-context decode of BASELINE configs[4]: four sequences at positions near
-    8k (and one at the last cache row) over their own cache planes, 8B head shape."""
-    B, hq, hkv, d, cap = 4, 32, 8, 128, 8448
-    starts = [8191, 8300, 5000, cap - 1]
+    8k (and one at the last cache row) over their own cache planes, 8B head shape.  A
+    grid that gives every CU a block (8 splits x 8 kv heads x 4 rows = 256) runs the
+    8-wave block (two waves per SIMD); batch 2 keeps the 4-wave block."""
+    hq, hkv, d, cap = 32, 8, 128, 8448
+    starts = [8191, 8300, 5000, cap - 1][:B]
     q = rbf(O.synth_f32(70, 1, B * hq * d, std=1.0).reshape(B, hq * d))
     kc = rbf(O.synth_f32(70, 2, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
     vc = rbf(O.synth_f32(70, 3, B * hkv * cap * d, std=1.0).reshape(B, hkv, cap, d))
@@ -236,6 +240,9 @@ def test_attention_decode_long_context_batch4():
     a = N.AttentionArgs(p(qd), p(kd), p(vd), p(out), 1, hq, hkv, d, cap, 0, p(posd), B, hkv * cap * d, 1, 0,
                         p(ws), wsb)
     L.call("am_gfx950_attention", a, stream())
+    name = launched()
+    wide = 8 * hkv * B >= torch.cuda.get_device_properties(0).multi_processor_count
+    assert name == f"attention_decode<d=128,g=4,splits=8{',waves=8' if wide else ''}>", name
     got = rd(out)
     for r in range(B):
         ref = O.attention(q[r:r + 1], kc[r], vc[r], 1, hq, hkv, d, cap, starts[r])[0]
