@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "am_gfx950.h"
+#include "hip_alloc.h"
 
 #include <algorithm>
 #include <cstdio>
@@ -367,10 +368,10 @@ Status KVCacheView::CommitUntil(size_t new_pos) noexcept {
 namespace {
 void* HipAlloc(size_t n, void*) {
   void* p = nullptr;
-  if (hipMalloc(&p, n == 0 ? 1 : n) != hipSuccess) return nullptr;
+  if (hip_alloc::DeviceMalloc(&p, n == 0 ? 1 : n) != hipSuccess) return nullptr;
   return p;
 }
-void HipFree(void* p, void*) { (void)hipFree(p); }
+void HipFree(void* p, void*) { (void)hip_alloc::DeviceFree(p); }
 void* HostAlloc(size_t n, void*) {
   void* p = nullptr;
   if (posix_memalign(&p, 256, n == 0 ? 1 : n) != 0) return nullptr;

@@ -36,6 +36,7 @@
 #include "gfx950_backend.h"
 #include "am_launch_timing.h"
 #include "hf_checkpoint.h"
+#include "hip_alloc.h"
 #include "packed_cache.h"
 
 namespace am {
@@ -112,7 +113,7 @@ class LlamaModel {
   int64_t linear_bytes = 0;
 
   ~LlamaModel() {
-    if (slab.base) (void)hipFree(slab.base);
+    if (slab.base) (void)hip_alloc::DeviceFree(slab.base);
   }
 
   int64_t KvRows() const { return static_cast<int64_t>(cfg.num_kv_heads) * cfg.head_dim; }
@@ -208,7 +209,7 @@ class LlamaModel {
     total += WBytes(V, H, fmt, g);
     total += 2 * (static_cast<int64_t>(c.max_tokens) * (d / 2) * 4 + 256);
     total += 4096;
-    AM_HIP_OK(hipMalloc(&slab.base, static_cast<size_t>(total)));
+    AM_HIP_OK(hip_alloc::DeviceMalloc(&slab.base, static_cast<size_t>(total)));
     slab.size = static_cast<size_t>(total);
 
     embed = slab.Take(static_cast<size_t>(V * H) * ab);
@@ -252,7 +253,7 @@ class LlamaModel {
     // scratch for one logical source matrix (largest: lm_head / embedding)
     const int64_t max_elems = std::max({V * H, F * H, QRows() * H});
     void* scratch = nullptr;
-    AM_HIP_OK(hipMalloc(&scratch, static_cast<size_t>(max_elems) * 4));
+    AM_HIP_OK(hip_alloc::DeviceMalloc(&scratch, static_cast<size_t>(max_elems) * 4));
     Status st = [&]() -> Status {
       am_gfx950_synth_args ea{seed, kEmbedId, 0.02, 0, V * H, embed, c.act_dtype};
       AM_C_OK(am_gfx950_synth_normal(&ea, stream));
@@ -272,7 +273,7 @@ class LlamaModel {
       AM_RETURN_IF_ERROR(SynthInto(seed, kLmHeadId, V, H, scratch, lm_head, 0));
       return FillRope();
     }();
-    (void)hipFree(scratch);
+    (void)hip_alloc::DeviceFree(scratch);
     return st;
   }
 
@@ -309,10 +310,10 @@ class LlamaModel {
     hipEvent_t ev[2] = {nullptr, nullptr};
     bool pending[2] = {false, false};
     Status st = [&]() -> Status {
-      AM_HIP_OK(hipMalloc(&dsrc, static_cast<size_t>(max_bytes)));
-      if (unpack_bytes > 0) AM_HIP_OK(hipMalloc(&dunpack, static_cast<size_t>(unpack_bytes)));
+      AM_HIP_OK(hip_alloc::DeviceMalloc(&dsrc, static_cast<size_t>(max_bytes)));
+      if (unpack_bytes > 0) AM_HIP_OK(hip_alloc::DeviceMalloc(&dunpack, static_cast<size_t>(unpack_bytes)));
       for (int i = 0; i < 2; ++i) {
-        AM_HIP_OK(hipHostMalloc(&pinned[i], kRing, hipHostMallocDefault));
+        AM_HIP_OK(hip_alloc::PinnedMalloc(&pinned[i], kRing));
         AM_HIP_OK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
       }
       int slot = 0;
@@ -431,10 +432,10 @@ class LlamaModel {
     (void)hipStreamSynchronize(stream);
     for (int i = 0; i < 2; ++i) {
       if (ev[i]) (void)hipEventDestroy(ev[i]);
-      if (pinned[i]) (void)hipHostFree(pinned[i]);
+      if (pinned[i]) (void)hip_alloc::PinnedFree(pinned[i]);
     }
-    if (dsrc) (void)hipFree(dsrc);
-    if (dunpack) (void)hipFree(dunpack);
+    if (dsrc) (void)hip_alloc::DeviceFree(dsrc);
+    if (dunpack) (void)hip_alloc::DeviceFree(dunpack);
     return st;
   }
 
@@ -452,7 +453,7 @@ class LlamaModel {
     hipEvent_t ev[2] = {nullptr, nullptr};
     Status Init() {
       for (int i = 0; i < 2; ++i) {
-        AM_HIP_OK(hipHostMalloc(&buf[i], kChunk, hipHostMallocDefault));
+        AM_HIP_OK(hip_alloc::PinnedMalloc(&buf[i], kChunk));
         AM_HIP_OK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
       }
       return Status::Ok();
@@ -460,7 +461,7 @@ class LlamaModel {
     ~Ring() {
       for (int i = 0; i < 2; ++i) {
         if (ev[i]) (void)hipEventSynchronize(ev[i]), (void)hipEventDestroy(ev[i]);
-        if (buf[i]) (void)hipHostFree(buf[i]);
+        if (buf[i]) (void)hip_alloc::PinnedFree(buf[i]);
       }
     }
   };
@@ -617,10 +618,10 @@ class LlamaSession {
     kv.reset();
     if (table_ev) (void)hipEventSynchronize(table_ev), (void)hipEventDestroy(table_ev);
     blocks.reset();
-    if (table_pinned) (void)hipHostFree(table_pinned);
-    if (act_slab) (void)hipFree(act_slab);
-    if (dl_table) (void)hipFree(dl_table);
-    if (dl_ws) (void)hipFree(dl_ws);
+    if (table_pinned) (void)hip_alloc::PinnedFree(table_pinned);
+    if (act_slab) (void)hip_alloc::DeviceFree(act_slab);
+    if (dl_table) (void)hip_alloc::DeviceFree(dl_table);
+    if (dl_ws) (void)hip_alloc::DeviceFree(dl_ws);
   }
 
   int64_t HistStride() const { return static_cast<int64_t>(m->cfg.max_tokens) + 1; }
@@ -704,8 +705,7 @@ class LlamaSession {
       AM_RETURN_IF_ERROR(blocks->Init(c.num_layers, c.num_kv_heads, c.head_dim, ActType(c.act_dtype),
                                       static_cast<size_t>(bs), static_cast<size_t>(nb), static_cast<size_t>(B),
                                       static_cast<size_t>(c.max_tokens)));
-      AM_HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&table_pinned), blocks->host_table().size() * 4,
-                              hipHostMallocDefault));
+      AM_HIP_OK(hip_alloc::PinnedMalloc(&table_pinned, blocks->host_table().size() * 4));
       AM_HIP_OK(hipEventCreateWithFlags(&table_ev, hipEventDisableTiming));
       AM_RETURN_IF_ERROR(SyncTable());
     } else {
@@ -758,7 +758,7 @@ class LlamaSession {
     constexpr int kParts = static_cast<int>(sizeof(sizes) / sizeof(sizes[0]));
     size_t total = 0;
     for (size_t s : sizes) total += (s + 255) & ~size_t{255};
-    AM_HIP_OK(hipMalloc(&act_slab, total));
+    AM_HIP_OK(hip_alloc::DeviceMalloc(&act_slab, total));
     AM_HIP_OK(hipMemsetAsync(act_slab, 0, total, stream));
     Slab sl{act_slab, total, 0};
     void* ptrs[kParts];
@@ -840,13 +840,13 @@ class LlamaSession {
       if (required) return Status::Unimplemented("persistent decode: unsupported head_dim or shape");
       return Status::Ok();
     }
-    AM_HIP_OK(hipMalloc(&dl_ws, static_cast<size_t>(dl_ws_bytes)));
-    AM_HIP_OK(hipMalloc(&dl_table, L * sizeof(am_gfx950_decode_layer)));
+    AM_HIP_OK(hip_alloc::DeviceMalloc(&dl_ws, static_cast<size_t>(dl_ws_bytes)));
+    AM_HIP_OK(hip_alloc::DeviceMalloc(&dl_table, L * sizeof(am_gfx950_decode_layer)));
     const am_gfx950_decode_layers_args a = DecodeLayersArgs();
     if (am_gfx950_decode_layers_validate(&a, host.data()) != AM_STATUS_OK) {
       const std::string why = am_last_error_message();
-      (void)hipFree(dl_ws);
-      (void)hipFree(dl_table);
+      (void)hip_alloc::DeviceFree(dl_ws);
+      (void)hip_alloc::DeviceFree(dl_table);
       dl_ws = dl_table = nullptr;
       dl_ws_bytes = 0;
       if (required) return Status::Unimplemented("persistent decode: " + why);
@@ -1220,7 +1220,7 @@ class LlamaSession {
         }
         if (e != hipSuccess) return Status::Internal(std::string("graph capture failed: ") + hipGetErrorString(e));
         graph = g;
-        AM_HIP_OK(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
+        AM_HIP_OK(hip_alloc::GraphInstantiate(&graph_exec, graph));
       }
       for (int64_t i = 0; i < n; ++i) AM_HIP_OK(hipGraphLaunch(graph_exec, stream));
     } else {

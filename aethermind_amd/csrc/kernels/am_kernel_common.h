@@ -29,12 +29,15 @@ inline int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // (table == nullptr): sequence b's planes start b * cbs elements in and head g's rows
 // g * cap * d after that.  Paged: the cache is a pool of blocks [hkv][1 << shift][d]
 // and table[b * stride + (pos >> shift)] names the block holding position pos of
-// sequence b (clamped into [0, num_blocks) so a bad table cannot address outside the
-// pool).  A run of positions that starts at a multiple of 32 and stays inside 32
-// positions lies in one block (blocks are at least 32 positions), so kernels look up
-// one block per 32-position step.
+// sequence b.  Readers clamp an entry outside [0, num_blocks) into the pool (Row), so a
+// bad table cannot address outside it; writers (WriteRow) skip the row instead and set
+// err, so a position whose block is unassigned (-1) never overwrites another
+// sequence's block.  A run of positions that starts at a multiple of 32 and stays
+// inside 32 positions lies in one block (blocks are at least 32 positions), so kernels
+// look up one block per 32-position step.
 struct KvRows {
   const int32_t* table = nullptr;
+  int32_t* err = nullptr;  // writers: set to 1 on an entry outside the pool (optional)
   int64_t cbs = 0, cap = 0;
   int64_t num_blocks = 0;
   int32_t shift = 0, stride = 0;
@@ -44,6 +47,18 @@ struct KvRows {
     if (table == nullptr) return b * cbs + (g * cap + pos) * d;
     int64_t blk = table[b * stride + (pos >> shift)];
     blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);
+    return (((blk * hkv + g) << shift) + (pos & ((int64_t{1} << shift) - 1))) * d;
+  }
+
+  // The row a writer stores position pos of (b, g) to, or -1 (row skipped, err set)
+  // when the table entry lies outside [0, num_blocks).
+  __device__ __forceinline__ int64_t WriteRow(int64_t b, int64_t g, int64_t pos) const {
+    if (table == nullptr) return b * cbs + (g * cap + pos) * d;
+    const int64_t blk = table[b * stride + (pos >> shift)];
+    if (blk < 0 || blk >= num_blocks) {
+      if (err != nullptr) *err = 1;
+      return -1;
+    }
     return (((blk * hkv + g) << shift) + (pos & ((int64_t{1} << shift) - 1))) * d;
   }
 };

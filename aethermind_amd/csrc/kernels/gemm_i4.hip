@@ -405,9 +405,12 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
       } else if (ok) {
         const bool isk = gn < p.c2;
         const int32_t hc = isk ? gn - p.c1 : gn - p.c2;
-        uint16_t* dst = (isk ? p.kc : p.vc) + p.kv.Row(0, hc / d, pos) + i0;
-        *reinterpret_cast<uint4*>(dst) = o1;
-        *reinterpret_cast<uint4*>(dst + half) = o2;
+        const int64_t row = p.kv.WriteRow(0, hc / d, pos);
+        if (row >= 0) {
+          uint16_t* dst = (isk ? p.kc : p.vc) + row + i0;
+          *reinterpret_cast<uint4*>(dst) = o1;
+          *reinterpret_cast<uint4*>(dst + half) = o2;
+        }
       }
     }
     return;
@@ -648,6 +651,7 @@ am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight&
   p.cap = static_cast<int32_t>(r.capacity);
   p.err = r.err_flag;
   if (auto st = MakeKvRows(r.pages, 0, r.capacity, r.hkv, r.head_dim, &p.kv); st != AM_STATUS_OK) return st;
+  if (p.kv.err == nullptr) p.kv.err = r.err_flag;
   return LaunchI4Any<kI4QkvRope>(p, ws, ws_bytes, s);
 }
 

@@ -610,15 +610,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
           A::store(q, head * p.d + i + half, o1);
         } else if (posv < p.cap) {
           T* kc = static_cast<T*>(p.k_cache);
-          const int64_t base = p.kv.Row(0, head - p.hq, posv);
-          A::store(kc, base + i, o0);
-          A::store(kc, base + i + half, o1);
+          const int64_t base = p.kv.WriteRow(0, head - p.hq, posv);
+          if (base >= 0) {
+            A::store(kc, base + i, o0);
+            A::store(kc, base + i + half, o1);
+          }
         }
       } else if (posv < p.cap) {
         T* vc = static_cast<T*>(p.v_cache);
-        const int64_t base = p.kv.Row(0, head - p.hq - p.hkv, posv);
-        A::store(vc, base + i, y0);
-        A::store(vc, base + i + half, y1);
+        const int64_t base = p.kv.WriteRow(0, head - p.hq - p.hkv, posv);
+        if (base >= 0) {
+          A::store(vc, base + i, y0);
+          A::store(vc, base + i + half, y1);
+        }
       }
     }
   };

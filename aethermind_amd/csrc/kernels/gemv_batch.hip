@@ -423,14 +423,20 @@ __global__ __launch_bounds__(kBWaves * 64) void gemv_batch_kernel(BatchArgs p) {
             q[i] = f32_to_bf16_bits(o0);
             q[i + half] = f32_to_bf16_bits(o1);
           } else if (in_cache) {
-            uint16_t* kc = p.k_cache + p.kv.Row(p.row0 + b, head - p.hq, pos);
-            kc[i] = f32_to_bf16_bits(o0);
-            kc[i + half] = f32_to_bf16_bits(o1);
+            const int64_t row = p.kv.WriteRow(p.row0 + b, head - p.hq, pos);
+            if (row >= 0) {
+              uint16_t* kc = p.k_cache + row;
+              kc[i] = f32_to_bf16_bits(o0);
+              kc[i + half] = f32_to_bf16_bits(o1);
+            }
           }
         } else if (in_cache) {
-          uint16_t* vc = p.v_cache + p.kv.Row(p.row0 + b, head - p.hq - p.hkv, pos);
-          vc[i] = f32_to_bf16_bits(y0);
-          vc[i + half] = f32_to_bf16_bits(y1);
+          const int64_t row = p.kv.WriteRow(p.row0 + b, head - p.hq - p.hkv, pos);
+          if (row >= 0) {
+            uint16_t* vc = p.v_cache + row;
+            vc[i] = f32_to_bf16_bits(y0);
+            vc[i + half] = f32_to_bf16_bits(y1);
+          }
         }
       }
     }

@@ -156,7 +156,9 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const uint8_t* k, const 
       continue;
     }
     const int64_t src = (s * hkv + h) * row_bytes + c * 16;
-    const int64_t dst = kv.Row(0, h, p) * esz + c * 16;
+    const int64_t row = kv.WriteRow(0, h, p);
+    if (row < 0) continue;
+    const int64_t dst = row * esz + c * 16;
     *reinterpret_cast<uint4*>(kc + dst) = *reinterpret_cast<const uint4*>(k + src);
     *reinterpret_cast<uint4*>(vc + dst) = *reinterpret_cast<const uint4*>(v + src);
   }
@@ -455,6 +457,7 @@ am_status_code MakeKvRows(const am_gfx950_kv_pages* pages, int64_t cbs, int64_t 
     r.num_blocks = pages->num_blocks;
     r.stride = pages->table_stride;
     r.shift = __builtin_ctz(static_cast<unsigned>(pages->block_size));
+    r.err = pages->err_flag;
   }
   *out = r;
   return AM_STATUS_OK;
@@ -475,6 +478,7 @@ extern "C" am_status_code am_gfx950_kv_update(const am_gfx950_kv_update_args* a,
   }
   KvRows kv;
   if (auto st = MakeKvRows(a->pages, 0, a->capacity, a->hkv, a->head_dim, &kv); st != AM_STATUS_OK) return st;
+  if (kv.err == nullptr) kv.err = a->err_flag;
   const int grid = GridFor(a->seq * a->hkv * (row_bytes / 16));
   hipLaunchKernelGGL(kv_update_kernel, dim3(grid), dim3(256), 0, AsStream(stream),
                      static_cast<const uint8_t*>(a->k), static_cast<const uint8_t*>(a->v),

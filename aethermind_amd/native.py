@@ -50,7 +50,8 @@ class LinearArgs(C.Structure):
 
 
 class KvPages(C.Structure):
-    _fields_ = [("block_table", vp), ("block_size", i32), ("table_stride", i32), ("num_blocks", i64)]
+    _fields_ = [("block_table", vp), ("block_size", i32), ("table_stride", i32), ("num_blocks", i64),
+                ("err_flag", vp)]
 
 
 class PrefillRopeKv(C.Structure):
@@ -177,6 +178,14 @@ class SessionConfig(C.Structure):
     _fields_ = [("struct_size", C.c_uint32), ("max_tokens", C.c_uint32), ("eos_token_id", i64), ("use_graph", i32)]
 
 
+class AllocStats(C.Structure):
+    _fields_ = [("device_allocs", i64), ("device_frees", i64), ("device_bytes_live", i64), ("pinned_allocs", i64),
+                ("pinned_frees", i64), ("pinned_bytes_live", i64), ("graph_instantiations", i64)]
+
+    def as_dict(self):
+        return {n: int(getattr(self, n)) for n, _ in self._fields_}
+
+
 class SessionOptions(C.Structure):
     _fields_ = [("fused_decode", i32), ("use_graph", i32), ("batch", i32), ("persistent_decode", i32),
                 ("kv_block_size", i32), ("kv_pool_blocks", i32)]
@@ -246,6 +255,7 @@ _SIGS = {
     "am_model_load_packed_cache": (i32, [vp, C.c_char_p, C.POINTER(ModelLoadOptions), C.POINTER(vp)]),
     "am_model_buffer": (i32, [vp, i32, i32, C.POINTER(vp), C.POINTER(i64)]),
     "am_model_weight_bytes_total": (i64, [vp]),
+    "am_debug_alloc_stats": (i32, [C.POINTER(AllocStats)]),
     "am_session_open": (i32, [vp, C.POINTER(SessionOptions), C.POINTER(vp)]),
     "am_session_destroy": (None, [vp]),
     "am_session_prefill": (i32, [vp, vp, i64, C.POINTER(i64)]),

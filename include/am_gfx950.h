@@ -215,6 +215,13 @@ typedef struct am_gfx950_kv_pages {
   int32_t block_size;         /* positions per block: a power of two, at least 32 */
   int32_t table_stride;       /* table entries per sequence */
   int64_t num_blocks;         /* blocks in each pool */
+  /* grown at the end (zero-initialise the struct): optional device flag the KV writers
+   * (kv_update, the fused q/k/v decode epilogues, the prefill q|k|v RoPE+KV epilogue)
+   * set to 1 when the table entry of a position they write lies outside
+   * [0, num_blocks), e.g. an unassigned block (-1); that row is then not written.
+   * Readers clamp such an entry into the pool.  kv_update and the prefill epilogue
+   * also report into their own err_flag when this one is NULL. */
+  int32_t* err_flag;
 } am_gfx950_kv_pages;
 
 /* OpType::kKVCacheUpdate (kvcache_update_op.cpp:50-138): writes k/v [seq][hkv*d]

@@ -210,6 +210,20 @@ int32_t am_session_persistent_decode(am_session* s);
  * count_by_op. */
 am_status_code am_session_profile_decode(am_session* s, int64_t n, double* ms_by_op, int64_t* count_by_op);
 
+/* Process-wide counts of the device memory (hipMalloc / hipFree) and pinned host
+ * memory (hipHostMalloc / hipHostFree) this library has taken and returned, and of the
+ * HIP graphs it has instantiated (an instantiation takes device memory of its own).
+ * A debug query with no counterpart in the reference: it shows that steady-state
+ * decode allocates nothing, the PRD's "zero allocations in steady state"
+ * (docs/products/aethermind_prd.md:152).  Memory torch or a caller allocates is not
+ * counted. */
+typedef struct am_alloc_stats {
+  int64_t device_allocs, device_frees, device_bytes_live;
+  int64_t pinned_allocs, pinned_frees, pinned_bytes_live;
+  int64_t graph_instantiations;
+} am_alloc_stats;
+am_status_code am_debug_alloc_stats(am_alloc_stats* out);
+
 /* ---------------- the PRD's Phase-1 C ABI (aethermind_prd.md:298-320) ----------------
  * Token ids are the only data boundary and are uint32 (prd.md:158-185).  Config structs
  * start with struct_size and only grow at the end (the PRD's ABI v1.x rules,

@@ -128,9 +128,16 @@ enum {
   ORC_SLIP_RESIDUAL_NORMED = 1, /* attention residual added to the normed input, not h */
   ORC_SLIP_ROPE_AFTER_KV = 2,   /* keys written to the cache without RoPE */
   ORC_SLIP_GQA_MODULO = 3,      /* q head h reads kv head h % hkv instead of h / group */
-  ORC_SLIP_NO_FINAL_NORM = 4    /* final RMSNorm skipped before the head */
+  ORC_SLIP_NO_FINAL_NORM = 4,   /* final RMSNorm skipped before the head */
+  ORC_SLIP_SWAP_NORM_GAINS = 5, /* each layer's input and post-attention gains swapped */
+  ORC_SLIP_FINAL_GAIN_FROM_LAYER = 6, /* final norm applies the last layer's post-attention gain */
+  ORC_SLIP_DROP_INPUT_GAIN = 7  /* input norms applied without their gain */
 };
 void orc_model_set_slip(orc_model* m, int32_t slip);
+/* Replace a norm gain vector (hidden floats): kind 0 = input norm of `layer`, 1 =
+ * post-attention norm of `layer`, 2 = final norm (layer ignored).  Synthetic models
+ * start with every gain 1.0.  Returns 3 for a bad kind or layer. */
+int orc_model_set_norm_gain(orc_model* m, int32_t kind, int32_t layer, const float* gain);
 /* OpenMP threads used by the oracle's parallel loops (cpu_baseline uses 1). */
 void orc_set_threads(int32_t n);
 

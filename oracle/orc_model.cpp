@@ -103,6 +103,7 @@ struct orc_model {
   std::vector<float> embed;  // [vocab][hidden] (bf16 values for bf16 models)
   std::vector<Layer> layers;
   std::vector<float> final_norm;
+  std::vector<float> unit_gain;  // all 1.0 (ORC_SLIP_DROP_INPUT_GAIN)
   QWeight lm_head;
   std::vector<float> cos_tab, sin_tab;
   int fast = 0;
@@ -195,6 +196,7 @@ orc_model* orc_model_create_synthetic(const orc_model_config* cfg, uint64_t seed
     L.vc.assign(static_cast<size_t>(hkv * cfg->max_tokens * d), 0.0f);
   }
   m->final_norm.assign(static_cast<size_t>(H), 1.0f);
+  m->unit_gain.assign(static_cast<size_t>(H), 1.0f);
   m->lm_head = MakeWeight(seed, kLmHeadId, V, H, fmt, g);
   m->cos_tab.resize(static_cast<size_t>(cfg->max_tokens * (d / 2)));
   m->sin_tab.resize(m->cos_tab.size());
@@ -207,6 +209,19 @@ void orc_model_destroy(orc_model* m) { delete m; }
 void orc_model_set_fast(orc_model* m, int32_t fast) { m->fast = fast; }
 
 void orc_model_set_slip(orc_model* m, int32_t slip) { m->slip = slip; }
+
+int orc_model_set_norm_gain(orc_model* m, int32_t kind, int32_t layer, const float* gain) {
+  std::vector<float>* dst = nullptr;
+  if (kind == 2) {
+    dst = &m->final_norm;
+  } else if ((kind == 0 || kind == 1) && layer >= 0 && layer < m->cfg.num_layers) {
+    Layer& L = m->layers[static_cast<size_t>(layer)];
+    dst = kind == 0 ? &L.in_norm : &L.post_norm;
+  }
+  if (dst == nullptr || gain == nullptr) return 3;
+  std::memcpy(dst->data(), gain, sizeof(float) * dst->size());
+  return 0;
+}
 
 void orc_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : 1); }
 
@@ -225,7 +240,13 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
   if (int rc = orc_embedding_i64(ids, n, m->embed.data(), c.vocab, H, h.data()); rc != 0) return rc;
 
   for (Layer& L : m->layers) {
-    Norm(m, h.data(), L.in_norm.data(), n, xn.data());
+    {
+      // which gain the input norm applies (the slips are planted composition mistakes)
+      const std::vector<float>& g = m->slip == ORC_SLIP_SWAP_NORM_GAINS ? L.post_norm
+                                    : m->slip == ORC_SLIP_DROP_INPUT_GAIN ? m->unit_gain
+                                                                          : L.in_norm;
+      Norm(m, h.data(), g.data(), n, xn.data());
+    }
     Linear(m, xn.data(), n, L.q, q.data());
     MaybeRound(m, q.data(), n * hq * d);
     Linear(m, xn.data(), n, L.k, k.data());
@@ -272,7 +293,7 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
       for (size_t i = 0; i < h.size(); ++i) h[i] += tmp[i];
     MaybeRound(m, h.data(), n * H);
 
-    Norm(m, h.data(), L.post_norm.data(), n, xn.data());
+    Norm(m, h.data(), (m->slip == ORC_SLIP_SWAP_NORM_GAINS ? L.in_norm : L.post_norm).data(), n, xn.data());
     Linear(m, xn.data(), n, L.gate, gt.data());
     MaybeRound(m, gt.data(), n * F);
     Linear(m, xn.data(), n, L.up, up.data());
@@ -288,7 +309,9 @@ int orc_model_forward(orc_model* m, const int64_t* ids, int64_t n, int64_t pos, 
   if (m->slip == ORC_SLIP_NO_FINAL_NORM)
     std::memcpy(xn.data(), h.data() + (n - 1) * H, sizeof(float) * static_cast<size_t>(H));
   else
-    Norm(m, h.data() + (n - 1) * H, m->final_norm.data(), 1, xn.data());
+    Norm(m, h.data() + (n - 1) * H,
+         (m->slip == ORC_SLIP_FINAL_GAIN_FROM_LAYER ? m->layers.back().post_norm : m->final_norm).data(), 1,
+         xn.data());
   Linear(m, xn.data(), 1, m->lm_head, logits);
   return 0;
 }

@@ -13,8 +13,16 @@ tests/test_oracle.py disagree with this file.
 
 Stored: the prompt, the 33 greedy tokens (prefill token + 32 decode steps), the full
 logits of the prefill step, and per step the top-16 (index, value) pairs plus the
-logits at every 97th vocabulary index.  Runs on the CPU in a few seconds:
-    python tests/golden/make_hf_tiny_golden.py
+logits at every 97th vocabulary index.
+
+With `gains`, writes tests/golden/hf_tiny_gains_fp32_seed0.npz instead: the same model
+with non-unit RMSNorm gains, 1 + N(0, 0.1) from the synthetic stream, a different vector
+for every norm (oracle_lib.norm_gains).  Unit gains cannot show which gain buffer a
+norm applies; these pin the wiring (input vs post-attention gain of each layer, the
+final norm's own gain).
+
+Runs on the CPU in a few seconds:
+    python tests/golden/make_hf_tiny_golden.py [gains]
 """
 import os
 import sys
@@ -34,7 +42,7 @@ ROLES = {"self_attn.q_proj": 1, "self_attn.k_proj": 2, "self_attn.v_proj": 3, "s
          "mlp.gate_proj": 5, "mlp.up_proj": 6, "mlp.down_proj": 7}
 
 
-def build_model(cfg, seed):
+def build_model(cfg, seed, gains=None):
     import torch
     from transformers import LlamaConfig, LlamaForCausalLM
 
@@ -50,14 +58,18 @@ def build_model(cfg, seed):
     H, V = cfg["hidden"], cfg["vocab"]
     sd["model.embed_tokens.weight"] = O.synth_f32(seed, 0x01, V * H).reshape(V, H)
     sd["lm_head.weight"] = O.synth_f32(seed, 0x02, V * H).reshape(V, H)
-    sd["model.norm.weight"] = np.ones(H, np.float32)
+    sd["model.norm.weight"] = np.ones(H, np.float32) if gains is None else gains["final"].astype(np.float32)
     for l in range(cfg["num_layers"]):
         for name, role in ROLES.items():
             shape = tuple(model.state_dict()[f"model.layers.{l}.{name}.weight"].shape)
             sd[f"model.layers.{l}.{name}.weight"] = O.synth_f32(seed, ((l + 1) << 8) | role,
                                                                shape[0] * shape[1]).reshape(shape)
-        sd[f"model.layers.{l}.input_layernorm.weight"] = np.ones(H, np.float32)
-        sd[f"model.layers.{l}.post_attention_layernorm.weight"] = np.ones(H, np.float32)
+        if gains is None:
+            sd[f"model.layers.{l}.input_layernorm.weight"] = np.ones(H, np.float32)
+            sd[f"model.layers.{l}.post_attention_layernorm.weight"] = np.ones(H, np.float32)
+        else:
+            sd[f"model.layers.{l}.input_layernorm.weight"] = gains["input"][l].astype(np.float32)
+            sd[f"model.layers.{l}.post_attention_layernorm.weight"] = gains["post"][l].astype(np.float32)
     missing, unexpected = model.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=False)
     # rotary inv_freq buffers are not weights
     assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
@@ -82,23 +94,25 @@ def hf_greedy(model, prompt, n_new):
     return np.array(toks, np.int64), steps
 
 
-def main():
+def main(with_gains=False):
     import torch
 
     torch.manual_seed(0)
     cfg = dict(O.TINY)
     prompt = O.token_ids(0, 0, cfg["vocab"], 16)
-    model = build_model(cfg, 0)
+    gains = O.norm_gains(0, cfg["num_layers"], cfg["hidden"]) if with_gains else None
+    model = build_model(cfg, 0, gains)
     toks, steps = hf_greedy(model, prompt, N_TOKENS)
     top_idx = np.stack([np.argsort(-s, kind="stable")[:TOPK] for s in steps]).astype(np.int64)
     top_val = np.stack([s[i] for s, i in zip(steps, top_idx)]).astype(np.float32)
     sample = np.stack([s[::SAMPLE_STRIDE] for s in steps]).astype(np.float32)
     gap = np.array([np.sort(s)[-1] - np.sort(s)[-2] for s in steps], np.float32)
-    np.savez(os.path.join(HERE, "hf_tiny_fp32_seed0.npz"), prompt=prompt, tokens=toks, prefill_logits=steps[0],
+    name = "hf_tiny_gains_fp32_seed0.npz" if with_gains else "hf_tiny_fp32_seed0.npz"
+    np.savez(os.path.join(HERE, name), prompt=prompt, tokens=toks, prefill_logits=steps[0],
              top_idx=top_idx, top_val=top_val, sample=sample, sample_stride=np.int64(SAMPLE_STRIDE), top2_gap=gap)
     print("tokens", toks.tolist())
     print("min top-2 gap", float(gap.min()))
 
 
 if __name__ == "__main__":
-    main()
+    main("gains" in sys.argv[1:])

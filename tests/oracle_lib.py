@@ -56,6 +56,7 @@ _SIGS = {
     "orc_model_forward": (i32, [vp, vp, i64, i64, vp]),
     "orc_model_set_fast": (None, [vp, i32]),
     "orc_model_set_slip": (None, [vp, i32]),
+    "orc_model_set_norm_gain": (i32, [vp, i32, i32, vp]),
     "orc_set_threads": (None, [i32]),
 }
 
@@ -223,6 +224,19 @@ class OracleModel:
     def set_slip(self, slip: int):
         lib().orc_model_set_slip(self.h, slip)
 
+    def set_norm_gain(self, kind: int, layer: int, gain: np.ndarray):
+        """kind 0 = input norm of `layer`, 1 = post-attention norm, 2 = final norm."""
+        g = np.ascontiguousarray(gain, np.float32)
+        assert g.size == self.cfg["hidden"]
+        assert lib().orc_model_set_norm_gain(self.h, kind, layer, ptr(g)) == 0
+
+    def set_gains(self, gains: dict):
+        """gains: {"input": [L][H], "post": [L][H], "final": [H]} (norm_gains())."""
+        for l in range(self.cfg["num_layers"]):
+            self.set_norm_gain(0, l, gains["input"][l])
+            self.set_norm_gain(1, l, gains["post"][l])
+        self.set_norm_gain(2, 0, gains["final"])
+
     def generate(self, prompt: np.ndarray, n_new: int):
         prompt = np.ascontiguousarray(prompt, np.int64)
         toks = np.empty(n_new, np.int64)
@@ -248,6 +262,15 @@ class OracleModel:
             self.close()
         except Exception:
             pass
+
+
+def norm_gains(seed: int, num_layers: int, hidden: int, std: float = 0.1) -> dict:
+    """Non-unit RMSNorm gains of the synthetic-data SPEC's stream: 1 + N(0, std) with
+    tensor id ((layer + 1) << 8) | 8 for the input norm, | 9 for the post-attention norm
+    and 0x03 for the final norm, so every gain vector differs from every other."""
+    return {"input": np.stack([1.0 + synth_f32(seed, ((l + 1) << 8) | 8, hidden, std=std) for l in range(num_layers)]),
+            "post": np.stack([1.0 + synth_f32(seed, ((l + 1) << 8) | 9, hidden, std=std) for l in range(num_layers)]),
+            "final": 1.0 + synth_f32(seed, 0x03, hidden, std=std)}
 
 
 TINY = dict(num_layers=4, hidden=512, num_q_heads=8, num_kv_heads=2, head_dim=64, ffn=1376, vocab=32000,

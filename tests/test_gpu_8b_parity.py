@@ -6,19 +6,23 @@ decode plan replayed as a HIP graph) against fixtures the CPU oracle wrote on it
 AVX2 path (tests/golden/make_8b_golden.py): the 512 prompt ids of stream 0, the
 prefill token and the next 32 greedy tokens.
 
-Bars.  Greedy token ids identical to the oracle's, except at near-ties: a token may
-differ only at a step where the oracle's own top-two gap (recorded in the fixture) is
-within twice the logit error measured at that step, so the error explains the flip;
-the test then continues from the oracle's token by prefilling prompt + the oracle's
-tokens so far, and every later step is held to the same bars.
+Bars.  Greedy token ids identical to the oracle's, except at steps the oracle itself
+cannot rank: a token may differ only at a step where the oracle's own top-two gap
+(recorded in the fixture) is within the oracle's own measured error at that step; the
+test then continues from the oracle's token by prefilling prompt + the oracle's tokens
+so far, and every later step is held to the same bars.
 
-The logit bar is calibrated by the oracle itself.  The fixture also holds the same 33
+The bars are calibrated by the oracle itself.  The fixture also holds the same 33
 steps recomputed on the oracle's fp64-accumulation path: two valid summation orders of
-the same bf16 composition, 32 layers deep, differ by 2-5% of the largest |logit| and
-pick different greedy tokens at some near-ties (self_err, self_flip).  The GPU must
-stay within twice the oracle's own largest step error, and its divergences within
-twice the oracle's own flips plus two.  The per-op 2e-2 bf16 bar of the north star
-holds op by op (test_gpu_decode_shapes.py); it does not compose over 32 layers."""
+the same bf16 composition, 32 layers deep, differ by 2-5% of the largest |logit|
+(self_err, per step) and pick different greedy tokens at some near-ties (self_flip).
+The GPU's summation order is a third one.  Its logit error may exceed the oracle's
+largest self error by at most 25% at any step, and it may diverge at most once more
+than the oracle's own two paths do.  Measured on the MI355X (divergences / oracle flips,
+largest error / oracle's largest): int4 4 / 3, 4.05e-2 / 3.65e-2; int8 2 / 3, 4.53e-2 /
+4.33e-2; bf16 3 / 5, 4.44e-2 / 4.32e-2, every divergence at a step the oracle cannot
+rank.  The per-op 2e-2 bf16 bar of the north star holds op by op
+(test_gpu_decode_shapes.py); it does not compose over 32 layers."""
 
 import ctypes as C
 import os
@@ -39,7 +43,7 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 SHAPE = dict(num_layers=32, hidden=4096, num_q_heads=32, num_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
              rms_eps=1e-5, rope_theta=500000.0)
 FORMATS = {"int4": N.AM_WF_INT4, "int8": N.AM_WF_INT8, "bf16": N.AM_WF_BF16}
-TOL = 1e-1  # sanity cap per step; the calibrated bar is applied at the end
+ERR_FACTOR = 1.25  # GPU logit error / the oracle's largest self error, per step
 
 
 def _fixture(fmt):
@@ -70,6 +74,9 @@ def test_8b_greedy_tokens_match_oracle(fmt):
     m = N.vp()
     L.call("am_model_create_synthetic", rt, C.byref(mc), 1, C.byref(m))
     logits = np.zeros(SHAPE["vocab"], np.float32)
+    self_err = g["self_err"].astype(np.float64)
+    self_flips = int(np.sum(g["self_flip"]))
+    tol = ERR_FACTOR * float(np.max(self_err))
     report = []
     try:
         step = 0
@@ -86,14 +93,17 @@ def test_8b_greedy_tokens_match_oracle(fmt):
             while True:
                 L.call("am_session_logits", s, logits.ctypes.data)
                 err, scale = _logit_errors(logits, g, step)
-                report.append((step, got, int(want[step]), round(err, 5), float(g["top2_gap"][step]) / scale))
-                assert err <= TOL, f"{fmt} step {step}: logits off by {err:.3e} of max |logit| ({report})"  # sanity cap
+                gap = float(g["top2_gap"][step]) / scale
+                report.append((step, got, int(want[step]), round(err, 5), round(gap, 5)))
+                assert err <= tol, (f"{fmt} step {step}: logits off by {err:.3e} of max |logit|, above "
+                                    f"{ERR_FACTOR} x the oracle's own {float(np.max(self_err)):.3e} ({report})")
                 if got != int(want[step]):
-                    gap = float(g["top2_gap"][step]) / scale
-                    assert gap <= 2 * err, (f"{fmt} step {step}: token {got} != oracle {int(want[step])} with the "
-                                            f"oracle's top-2 gap {gap:.3e} above twice the logit error {err:.3e} "
-                                            f"({report})")
+                    assert gap <= self_err[step], (
+                        f"{fmt} step {step}: token {got} != oracle {int(want[step])} where the oracle's top-2 gap "
+                        f"{gap:.3e} exceeds its own error {self_err[step]:.3e} at that step ({report})")
                     divergences += 1
+                    print(f"[8b parity {fmt}] divergence at step {step}: gap {gap:.4f}, gpu error {err:.4f}, "
+                          f"oracle self error {self_err[step]:.4f}", flush=True)
                     step += 1
                     restarted = True
                     break
@@ -107,15 +117,10 @@ def test_8b_greedy_tokens_match_oracle(fmt):
             if not restarted:
                 break
         worst = max(r[3] for r in report)
-        self_err = float(np.max(g["self_err"])) if "self_err" in g else None
-        self_flips = int(np.sum(g["self_flip"])) if "self_flip" in g else None
-        print(f"[8b parity {fmt}] steps {n_steps}, near-tie divergences {divergences} (oracle fp64 vs AVX2: "
-              f"{self_flips}), max logit error {worst:.3e} (oracle fp64 vs AVX2: {self_err})", flush=True)
-        if self_err is not None:
-            assert worst <= 2 * self_err, (worst, self_err, report)
-            assert divergences <= 2 * self_flips + 2, (divergences, self_flips, report)
-        else:
-            assert divergences <= 2, report
+        summary = (f"[8b parity {fmt}] steps {n_steps}: near-tie divergences {divergences} (oracle fp64 vs AVX2: "
+                   f"{self_flips}), max logit error {worst:.3e} (oracle fp64 vs AVX2: {float(np.max(self_err)):.3e})")
+        print(summary, flush=True)
+        assert divergences <= self_flips + 1, f"{summary}: {report}"
     finally:
         L.am_model_destroy(m)
         L.am_runtime_destroy(rt)

@@ -24,7 +24,7 @@ if not torch.cuda.is_available():  # pragma: no cover
 
 import aethermind_amd.native as N  # noqa: E402
 import oracle_lib as O  # noqa: E402
-from gpu_util import bf16_dev, bits_host, dev, empty, p, pack_weight, stream, zeros  # noqa: E402
+from gpu_util import bf16_dev, bits_host, dev, empty, host, p, pack_weight, stream, zeros  # noqa: E402
 
 L = N.lib()
 NAN_BF16 = 0x7FC0
@@ -137,6 +137,72 @@ def test_kv_update_paged_writes_the_mapped_rows_only():
         for blk in range(pg.nb):
             if blk not in used:
                 assert (raw[blk] == NAN_BF16).all()
+
+
+def test_kv_update_skips_unassigned_blocks():
+    """A table entry outside [0, num_blocks) (an unassigned block, -1, or past the pool)
+    is never written through: the rows of those positions are skipped, the pages'
+    err_flag is set, and every block of the pool other than the mapped ones keeps its
+    contents (the reader's clamp would have sent the rows to block 0 or the last
+    block)."""
+    rng = np.random.default_rng(4)
+    hkv, d, cap, bs, S, start = 2, 64, 256, 32, 96, 32
+    cache = np.full((1, hkv, cap, d), 0x3F80, np.uint16)
+    pg = Paged(rng, cache, bs)
+    pg.table[0, 2] = -1  # positions 64..95
+    pg.table[0, 3] = pg.nb + 5  # positions 96..127
+    pg.dtable = dev(pg.table)
+    err = zeros((1,), torch.int32)
+    pages = N.KvPages(p(pg.dtable), bs, pg.per, pg.nb, p(err))
+    pool_k, pool_v = bf16_dev(pg.pool), bf16_dev(pg.pool)
+    k, v = rand_bits(rng, (S, hkv * d)), rand_bits(rng, (S, hkv * d))
+    kd, vd = bf16_dev(k), bf16_dev(v)
+    a = N.KvUpdateArgs(p(kd), p(vd), p(pool_k), p(pool_v), S, hkv, d, cap, start, None, N.AM_DT_BF16, None,
+                       C.pointer(pages))
+    L.call("am_gfx950_kv_update", C.byref(a), stream())
+    assert int(host(err)[0]) == 1
+    for pool, src in ((pool_k, k), (pool_v, v)):
+        raw = bits_host(pool).reshape(pg.pool.shape)
+        want = pg.pool.copy()
+        src3 = src.reshape(S, hkv, d)
+        for pos in range(start, start + S):
+            j = pos // bs
+            if j in (2, 3):
+                continue
+            want[pg.table[0, j], :, pos % bs, :] = src3[pos - start]
+        assert np.array_equal(raw, want)
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_fused_qkv_skips_unassigned_blocks(rows):
+    """The fused q/k/v decode epilogue (batch-1 and batched kernels) writes no K/V row
+    for a position whose block is unassigned: the pool is left as it was, the err flag
+    is set, and q is still produced."""
+    rng = np.random.default_rng(11 + rows)
+    H, hq, hkv, d, cap, bs = 512, 8, 2, 64, 256, 32
+    n = (hq + 2 * hkv) * d
+    bits = O.synth_bf16(9, 0x21, n * H).reshape(n, H)
+    dw, keep = pack_weight(O.bf16_to_f32(bits).copy(), N.AM_WF_INT4, 128, src_bf16_bits=bits)
+    h = bf16_dev(rand_bits(rng, (rows, H)))
+    nw = bf16_dev(rand_bits(rng, (H,)))
+    pos = np.array([5, 130, 255][:rows], np.int64)
+    ct, st = O.rope_tables(cap, d, 10000.0)
+    pd, ctd, std_ = dev(pos), dev(ct), dev(st)
+    pg = Paged(rng, np.zeros((rows, hkv, cap, d), np.uint16), bs)
+    for r in range(rows):
+        pg.table[r, pos[r] // bs] = -1
+    pg.dtable = dev(pg.table)
+    err = zeros((1,), torch.int32)
+    pages = N.KvPages(p(pg.dtable), bs, pg.per, pg.nb, p(err))
+    pk, pv = bf16_dev(pg.pool), bf16_dev(pg.pool)
+    qo = zeros((rows, hq * d), torch.int16)
+    a = N.FusedQkvArgs(p(h), p(nw), 1e-5, dw, p(ctd), p(std_), p(pd), p(qo), p(pk), p(pv), hq, hkv, d, cap,
+                       N.AM_DT_BF16, rows, 0, C.pointer(pages))
+    L.call("am_gfx950_fused_qkv", C.byref(a), stream())
+    assert int(host(err)[0]) == 1
+    for pool in (pk, pv):
+        assert np.array_equal(bits_host(pool).reshape(pg.pool.shape), pg.pool)
+    assert np.any(bits_host(qo) != 0)
 
 
 @pytest.mark.parametrize("rows", [1, 3])

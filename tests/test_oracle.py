@@ -288,11 +288,11 @@ def test_tiny_model_matches_committed_golden():
 
 
 # ---------------------------------------------------------------- composition vs HF
-def _hf_golden_errors(m):
+def _hf_golden_errors(m, name="hf_tiny_fp32_seed0.npz"):
     """Walks the oracle model through the golden's 33 steps (prefill, then KV-cached
     decode steps fed with the golden's tokens) and returns the largest logit error
     relative to the step's largest |logit| and the steps whose greedy token differs."""
-    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "hf_tiny_fp32_seed0.npz"))
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", name))
     prompt = g["prompt"]
     stride = int(g["sample_stride"])
     worst, bad_steps = 0.0, []
@@ -335,3 +335,50 @@ def test_hf_golden_rejects_planted_composition_slips(slip):
     m.set_slip(slip)
     worst, bad = _hf_golden_errors(m)
     assert worst > 1e-2, (slip, worst)
+
+
+# ---------------------------------------------------------------- norm gain wiring vs HF
+GAINS_GOLDEN = "hf_tiny_gains_fp32_seed0.npz"
+
+
+def _gains_model(slip=0, fast=False):
+    m = O.OracleModel(O.TINY, 0)
+    m.set_gains(O.norm_gains(0, O.TINY["num_layers"], O.TINY["hidden"]))
+    m.set_fast(fast)
+    m.set_slip(slip)
+    return m
+
+
+def test_norm_gains_are_distinct_and_non_unit():
+    g = O.norm_gains(0, O.TINY["num_layers"], O.TINY["hidden"])
+    vecs = list(g["input"]) + list(g["post"]) + [g["final"]]
+    for i, a in enumerate(vecs):
+        assert 0.05 < float(np.std(a)) < 0.2 and abs(float(np.mean(a)) - 1.0) < 0.02
+        for b in vecs[i + 1:]:
+            assert float(np.max(np.abs(a - b))) > 0.1
+
+
+def test_oracle_gain_wiring_matches_hf_transformers_golden():
+    """With a different non-unit gain on every RMSNorm (1 + N(0, 0.1);
+    tests/golden/make_hf_tiny_golden.py gains), the oracle's composition still equals
+    transformers' LlamaForCausalLM: identical greedy tokens at all 33 steps and logits
+    within 1e-4 of the largest |logit|.  The unit-gain golden cannot tell which gain a
+    norm applies; this one can (see the slips below)."""
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", GAINS_GOLDEN))
+    assert np.array_equal(O.token_ids(0, 0, 32000, 16), g["prompt"])
+    for fast in (False, True):
+        worst, bad = _hf_golden_errors(_gains_model(fast=fast), GAINS_GOLDEN)
+        assert worst <= 1e-4 and not bad, (fast, worst, bad)
+
+
+@pytest.mark.parametrize("slip", [5, 6, 7])
+def test_gains_golden_rejects_planted_gain_wiring_slips(slip):
+    """Swapping each layer's input and post-attention gains, giving the final norm the
+    last layer's post-attention gain, or dropping the input norms' gain each fails the
+    gains pin, while the unit-gain pin cannot see any of them."""
+    worst, bad = _hf_golden_errors(_gains_model(slip), GAINS_GOLDEN)
+    assert worst > 1e-3, (slip, worst)
+    m = O.OracleModel(O.TINY, 0)
+    m.set_slip(slip)
+    worst_unit, bad_unit = _hf_golden_errors(m)
+    assert worst_unit <= 1e-4 and not bad_unit, (slip, worst_unit)
