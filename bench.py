@@ -83,15 +83,7 @@ def cpu_baseline(weight_format: int, seconds_budget: float = 20.0, pos: int = 51
     t_layer = max(res[2] - res[1], 1e-9)
     t_rest = max(res[1] - t_layer, 0.0)
     t_token = t_rest + SHAPE["num_layers"] * t_layer
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu = _cpu_model_name()
     return {
         "value": round(1.0 / t_token, 4),
         "unit": "tokens/s",
@@ -103,6 +95,92 @@ def cpu_baseline(weight_format: int, seconds_budget: float = 20.0, pos: int = 51
                    (f"; {sequences} sequences decode one after another, so the aggregate rate is the same"
                     if sequences > 1 else "")),
     }
+
+
+GEMV_SHAPES = [(4096, 4096, "q/o"), (1024, 4096, "k/v"), (14336, 4096, "gate or up"), (4096, 14336, "down"),
+               (128256, 4096, "lm_head")]
+
+
+def _cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_plan(all_cores: int):
+    """The rest of the CPU-baseline plan, on the same oracle restatement of the
+    reference CPU path (AVX2 dot product and RMSNorm, rows dequantized on the fly):
+    - the tiny fp32 config end to end (prefill 16, greedy
+      decode 32) on one thread, with its tokens checked against the committed golden;
+    - the decode GEMV of each 8B shape in bf16, INT8 and INT4 (the reference's
+      benchmark harness pattern: benchmark_cpu_dot_product_avx2.cpp:21-36, timed
+      repeats of one kernel), one thread, and again on `all_cores` threads, labelled
+      apart (the reference's OpenMP pragmas are inert in its build, so one thread is
+      the reference's own figure)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+
+    import oracle_lib as O
+
+    L = O.lib()
+    out = {"cpu": _cpu_model_name(), "nproc": os.cpu_count()}
+    # tiny end to end
+    L.orc_set_threads(1)
+    m = O.OracleModel(O.TINY, 0)
+    m.set_fast(True)
+    prompt = O.token_ids(0, 0, O.TINY["vocab"], 16)
+    t0 = time.perf_counter()
+    logits = m.forward(prompt, 0)
+    t_prefill = time.perf_counter() - t0
+    toks = [O.argmax(logits)]
+    t0 = time.perf_counter()
+    for i in range(32):
+        logits = m.forward(np.array([toks[-1]], np.int64), 16 + i)
+        toks.append(O.argmax(logits))
+    t_decode = time.perf_counter() - t0
+    m.close()
+    golden = None
+    try:
+        g = np.load(os.path.join(ROOT, "tests", "golden", "tiny_fp32_seed0.npz"))
+        golden = bool(np.array_equal(np.array(toks, np.int64), g["tokens"]))
+    except OSError:
+        pass
+    out["tiny_end_to_end"] = {"threads": 1, "prefill_tokens": 16, "prefill_ms": round(t_prefill * 1e3, 2),
+                              "decode_tokens": 32, "decode_tokens_per_s": round(32 / t_decode, 2),
+                              "tokens": toks, "tokens_equal_committed_golden": golden}
+
+    def sweep(threads):
+        L.orc_set_threads(threads)
+        rows = []
+        for n, k, role in GEMV_SHAPES:
+            x = np.random.default_rng(n + k).standard_normal(k).astype(np.float32)
+            y = np.empty(n, np.float32)
+            for fmt, fname in ((1, "bf16"), (2, "int8"), (3, "int4")):
+                q = L.orc_qweight_create(n, k, fmt, 128, 1)
+                if not q:
+                    raise RuntimeError("orc_qweight_create failed")
+                L.orc_qweight_gemv(q, O.ptr(x), O.ptr(y))  # first touch
+                best = 1e9
+                for _ in range(2):
+                    t0 = time.perf_counter()
+                    L.orc_qweight_gemv(q, O.ptr(x), O.ptr(y))
+                    best = min(best, time.perf_counter() - t0)
+                nb = int(L.orc_qweight_bytes(q))
+                L.orc_qweight_destroy(q)
+                rows.append({"n": n, "k": k, "role": role, "format": fname, "bytes": nb, "ms": round(best * 1e3, 3),
+                             "gbs": round(nb / best / 1e9, 3)})
+        return rows
+
+    out["gemv_1_thread"] = sweep(1)
+    out["gemv_all_cores"] = {"threads": all_cores, "label": "all cores (not the reference's configuration)",
+                             "results": sweep(all_cores)}
+    L.orc_set_threads(1)
+    return out
 
 
 def calibrate_copy(mib: int) -> None:
@@ -378,6 +456,18 @@ def main():
             log(f"cpu baseline: {cpu['value']} tok/s ({cpu['sample']})")
         except Exception as e:  # the GPU figures stand without it
             log(f"cpu baseline failed: {e}")
+        if cpu is not None:
+            try:
+                t0 = time.perf_counter()
+                cpu["plan"] = cpu_baseline_plan(min(16, os.cpu_count() or 1))
+                te = cpu["plan"]["tiny_end_to_end"]
+                log(f"cpu tiny end to end (1 thread): prefill 16 in {te['prefill_ms']} ms, decode "
+                    f"{te['decode_tokens_per_s']} tok/s, tokens equal golden: {te['tokens_equal_committed_golden']}")
+                for r in cpu["plan"]["gemv_1_thread"]:
+                    log(f"cpu gemv 1 thread {r['n']}x{r['k']} {r['format']}: {r['ms']} ms, {r['gbs']} GB/s")
+                log(f"cpu baseline plan took {time.perf_counter() - t0:.1f} s")
+            except Exception as e:
+                log(f"cpu baseline plan failed: {e}")
 
     pmc, prov = measured_traffic(f"gemv_{args.config}_decode_traffic")
     out = {

@@ -138,6 +138,16 @@ void orc_model_set_slip(orc_model* m, int32_t slip);
  * post-attention norm of `layer`, 2 = final norm (layer ignored).  Synthetic models
  * start with every gain 1.0.  Returns 3 for a bad kind or layer. */
 int orc_model_set_norm_gain(orc_model* m, int32_t kind, int32_t layer, const float* gain);
+/* Per-shape decode GEMV of the CPU baseline: an n x k weight in format fmt (1 bf16,
+ * 2 int8 per-channel, 3 int4 of `group`) filled with cheap deterministic bytes (timing
+ * only: the values are not the synthetic-data SPEC's), and y = W x through the model's
+ * Linear path (rows dequantized on the fly, AVX2 dot product), on the OpenMP threads
+ * set by orc_set_threads.  orc_qweight_bytes: weight + scale bytes. */
+typedef struct orc_qweight orc_qweight;
+orc_qweight* orc_qweight_create(int64_t n, int64_t k, int32_t fmt, int64_t group, uint64_t seed);
+void orc_qweight_destroy(orc_qweight* q);
+int64_t orc_qweight_bytes(const orc_qweight* q);
+void orc_qweight_gemv(const orc_qweight* q, const float* x, float* y);
 /* OpenMP threads used by the oracle's parallel loops (cpu_baseline uses 1). */
 void orc_set_threads(int32_t n);
 

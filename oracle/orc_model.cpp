@@ -112,7 +112,7 @@ struct orc_model {
 
 namespace {
 
-void Linear(const orc_model* m, const float* x, int64_t rows, const QWeight& w, float* out) {
+void LinearImpl(bool fast, const float* x, int64_t rows, const QWeight& w, float* out) {
   // Output columns in blocks of 16 dequantized rows: each token row is then read once
   // per block instead of once per column (the same dot per output either way).
   const int64_t n = w.n, k = w.k;
@@ -128,7 +128,7 @@ void Linear(const orc_model* m, const float* x, int64_t rows, const QWeight& w, 
         const float* xr = x + r * k;
         for (int64_t j = 0; j < nb; ++j) {
           const float* wr = buf.data() + j * k;
-          if (m->fast) {
+          if (fast) {
             out[r * n + c0 + j] = orc_dot_avx2(xr, wr, k);
           } else {
             double acc = 0.0;
@@ -139,6 +139,10 @@ void Linear(const orc_model* m, const float* x, int64_t rows, const QWeight& w, 
       }
     }
   }
+}
+
+void Linear(const orc_model* m, const float* x, int64_t rows, const QWeight& w, float* out) {
+  LinearImpl(m->fast != 0, x, rows, w, out);
 }
 
 void MaybeRound(const orc_model* m, float* x, int64_t n) {
@@ -334,5 +338,60 @@ int orc_model_generate(orc_model* m, const int64_t* prompt, int64_t n_prompt, in
     std::memcpy(last_logits, logits.data(), sizeof(float) * logits.size());
   return 0;
 }
+
+// ---------------- per-shape GEMV of the CPU baseline ----------------
+// A weight of one format filled with cheap deterministic bytes (the timing does not
+// depend on the values, and the seeded normal generator would cost seconds per GB),
+// multiplied by one activation row through the model's own Linear path: rows
+// dequantized on the fly in blocks of 16, each dotted with the AVX2 kernel.
+struct orc_qweight {
+  QWeight w;
+};
+
+orc_qweight* orc_qweight_create(int64_t n, int64_t k, int32_t fmt, int64_t group, uint64_t seed) {
+  if (n <= 0 || k <= 0 || fmt < 1 || fmt > 3 || (fmt == 3 && (group <= 0 || k % group != 0))) return nullptr;
+  auto* q = new orc_qweight();
+  QWeight& w = q->w;
+  w.n = n;
+  w.k = k;
+  w.fmt = fmt;
+  w.group = group;
+  const size_t count = static_cast<size_t>(n * k);
+  auto bits = [seed](uint64_t i) { return orc_splitmix64(seed ^ (i * 0x9E3779B97F4A7C15ull)); };
+  if (fmt == 1) {
+    w.bf16.resize(count);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i) {
+      // 2^-7 <= |value| < 2^-4: exponent 0x78..0x7A, random sign and mantissa
+      const uint64_t b = bits(static_cast<uint64_t>(i));
+      w.bf16[static_cast<size_t>(i)] =
+          static_cast<uint16_t>(((b >> 8) & 0x8000u) | ((0x78u + (b & 1u) + ((b >> 1) & 1u)) << 7) | ((b >> 16) & 0x7Fu));
+    }
+  } else if (fmt == 2) {
+    w.q8.resize(count);
+    w.s8.assign(static_cast<size_t>(n), 0.02f / 127.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count); ++i)
+      w.q8[static_cast<size_t>(i)] = static_cast<int8_t>(static_cast<int>(bits(static_cast<uint64_t>(i)) % 255u) - 127);
+  } else {
+    w.q4.resize(count / 2);
+    w.s4.assign(static_cast<size_t>(n * (k / group)), orc_f32_to_f16(0.02f / 7.0f));
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < static_cast<int64_t>(count / 2); ++i)
+      w.q4[static_cast<size_t>(i)] = static_cast<uint8_t>(bits(static_cast<uint64_t>(i)));
+  }
+  return q;
+}
+
+void orc_qweight_destroy(orc_qweight* q) { delete q; }
+
+int64_t orc_qweight_bytes(const orc_qweight* q) {
+  const QWeight& w = q->w;
+  if (w.fmt == 1) return w.n * w.k * 2;
+  if (w.fmt == 2) return w.n * w.k + w.n * 4;
+  return w.n * w.k / 2 + w.n * (w.k / w.group) * 2;
+}
+
+void orc_qweight_gemv(const orc_qweight* q, const float* x, float* y) { LinearImpl(true, x, 1, q->w, y); }
 
 }  // extern "C"

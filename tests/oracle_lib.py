@@ -58,6 +58,10 @@ _SIGS = {
     "orc_model_set_slip": (None, [vp, i32]),
     "orc_model_set_norm_gain": (i32, [vp, i32, i32, vp]),
     "orc_set_threads": (None, [i32]),
+    "orc_qweight_create": (vp, [i64, i64, i32, i64, u64]),
+    "orc_qweight_destroy": (None, [vp]),
+    "orc_qweight_bytes": (i64, [vp]),
+    "orc_qweight_gemv": (None, [vp, vp, vp]),
 }
 
 _lib = None

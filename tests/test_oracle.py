@@ -382,3 +382,32 @@ def test_gains_golden_rejects_planted_gain_wiring_slips(slip):
     m.set_slip(slip)
     worst_unit, bad_unit = _hf_golden_errors(m)
     assert worst_unit <= 1e-4 and not bad_unit, (slip, worst_unit)
+
+
+# ---------------------------------------------------------------- CPU-baseline GEMV helper
+@pytest.mark.parametrize("fmt", [1, 2, 3])
+def test_qweight_gemv_is_the_linear_map_of_its_weight(fmt):
+    """The per-shape GEMV the bench's CPU baseline times (orc_qweight_gemv) is a linear
+    map: doubling x doubles y exactly, y(x1 + x2) = y(x1) + y(x2) to fp32 rounding,
+    and one-hot inputs pick single columns whose values are bounded by the fill."""
+    L = O.lib()
+    n, k = 37, 256
+    q = L.orc_qweight_create(n, k, fmt, 128, 5)
+    assert q
+    try:
+        rng = np.random.default_rng(fmt)
+        x1, x2 = rng.standard_normal(k).astype(np.float32), rng.standard_normal(k).astype(np.float32)
+
+        def y(x):
+            x = np.ascontiguousarray(x, np.float32)
+            out = np.empty(n, np.float32)
+            L.orc_qweight_gemv(q, O.ptr(x), O.ptr(out))
+            return out
+
+        assert np.array_equal(y(2 * x1), 2 * y(x1))
+        np.testing.assert_allclose(y(x1 + x2), y(x1) + y(x2), rtol=1e-4, atol=1e-5)
+        cols = np.stack([y(np.eye(k, dtype=np.float32)[j]) for j in range(0, k, 17)])
+        assert np.all(np.isfinite(cols)) and np.any(cols != 0) and float(np.max(np.abs(cols))) < 0.07
+        assert L.orc_qweight_bytes(q) == {1: n * k * 2, 2: n * k + 4 * n, 3: n * k // 2 + n * (k // 128) * 2}[fmt]
+    finally:
+        L.orc_qweight_destroy(q)
