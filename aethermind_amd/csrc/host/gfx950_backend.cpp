@@ -590,6 +590,18 @@ AM_REGISTER_KERNEL(HipPreQkvRopeBF16I4, Desc(OpType::kFusedLinearRoPEKVUpdate, H
                                              &FusedLinearRoPEKVKernel, "gfx950::gemm_qkv_rope_kv_bf16_int4"))
 AM_REGISTER_KERNEL(HipPreSiluBF16I4, Desc(OpType::kFusedLinearSiluMul, HipSelector(kBF16, kI4, WF::kQuantizedInt4, EP::kPrefill),
                                           &FusedLinearSiluMulKernel, "gfx950::gemm_silu_mul_bf16_int4"))
+// the same prefill fusions for INT8 per-channel and bf16 weights (one GEMM kernel template)
+#define AM_PREFILL_REGS(TAG, WT, FMT)                                                                                  \
+  AM_REGISTER_KERNEL(HipPreLinAdd##TAG, Desc(OpType::kFusedLinearAdd, HipSelector(kBF16, WT, FMT, EP::kPrefill),        \
+                                             &PrefillLinearAddKernel, "gfx950::gemm_add_" #TAG))                      \
+  AM_REGISTER_KERNEL(HipPreSplit##TAG, Desc(OpType::kFusedLinearSplit, HipSelector(kBF16, WT, FMT, EP::kPrefill),       \
+                                            &FusedLinearSplitKernel, "gfx950::gemm_split_" #TAG))                     \
+  AM_REGISTER_KERNEL(HipPreQkvRope##TAG, Desc(OpType::kFusedLinearRoPEKVUpdate, HipSelector(kBF16, WT, FMT, EP::kPrefill), \
+                                              &FusedLinearRoPEKVKernel, "gfx950::gemm_qkv_rope_kv_" #TAG))            \
+  AM_REGISTER_KERNEL(HipPreSilu##TAG, Desc(OpType::kFusedLinearSiluMul, HipSelector(kBF16, WT, FMT, EP::kPrefill),      \
+                                           &FusedLinearSiluMulKernel, "gfx950::gemm_silu_mul_" #TAG))
+AM_PREFILL_REGS(bf16_int8, kI8, WF::kQuantizedInt8)
+AM_PREFILL_REGS(bf16_bf16, kBF16, WF::kPlain)
 }  // namespace
 
 }  // namespace aethermind::gfx950

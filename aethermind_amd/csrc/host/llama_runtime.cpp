@@ -729,8 +729,8 @@ class LlamaSession {
         am_gfx950_attention_workspace_bytes(1, S, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0),
         am_gfx950_attention_workspace_bytes(B, 1, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_tokens, 0)));
     am_ws_bytes = am_gfx950_argmax_workspace_bytes(1);
-    if (c.weight_format == AM_WF_INT4) {
-      const int64_t g = c.group_size;
+    if (c.weight_format == AM_WF_INT4 || c.weight_format == AM_WF_INT8 || c.weight_format == AM_WF_BF16) {
+      const int64_t g = c.weight_format == AM_WF_INT4 ? c.group_size : 128;
       for (auto nk : {std::pair<int64_t, int64_t>{m->QRows() + 2 * m->KvRows(), H}, {H, m->QRows()}, {2 * F, H}, {H, F}})
         gemm_ws_bytes = std::max(gemm_ws_bytes, static_cast<size_t>(am_gfx950_gemm_workspace_bytes(S, nk.first, nk.second, g)));
     }
@@ -910,11 +910,14 @@ class LlamaSession {
     const gfx950::NormAttrs na{c.rms_eps};
     auto& W = s_views[static_cast<size_t>(l)];
     const TensorView hv(h, A, {S, H}), xnv(xn, A, {S, H});
-    // Prefill with INT4 weights on the MFMA GEMM fuses each Linear with its neighbour:
-    // q|k|v as one GEMM over the concatenated weight, o and down with their residual
-    // Add, gate|up with the SiluMul (the same op-boundary roundings).
-    const bool fuse = ph == ExecPhase::kPrefill && c.act_dtype == AM_DT_BF16 && c.weight_format == AM_WF_INT4 &&
-                      c.group_size % 64 == 0 && c.ffn % 64 == 0;
+    // Prefill on the MFMA GEMM fuses each Linear with its neighbour: q|k|v as one GEMM
+    // over the concatenated weight, o and down with their residual Add, gate|up with
+    // the SiluMul (the same op-boundary roundings).  INT4 (group a multiple of 64), INT8
+    // and bf16 weights; INT8 and bf16 need every k a multiple of 128.
+    const bool k128 = H % 128 == 0 && F % 128 == 0 && Q % 128 == 0;
+    const bool fuse = ph == ExecPhase::kPrefill && c.act_dtype == AM_DT_BF16 && c.ffn % 64 == 0 &&
+                      ((c.weight_format == AM_WF_INT4 && c.group_size % 64 == 0) ||
+                       ((c.weight_format == AM_WF_INT8 || c.weight_format == AM_WF_BF16) && k128));
     AM_RETURN_IF_ERROR(b.Add(OpType::kRmsNorm, PackAttrs(na), Sel(false, ph), nullptr,
                              {hv, TensorView(m->in_norm[l], A, {H})}, {MutableTensorView(xn, A, {S, H})}));
     // the prefill GEMMs' inputs, with the split-K workspace when the session has one

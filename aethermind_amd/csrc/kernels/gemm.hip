@@ -339,7 +339,8 @@ extern "C" am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linea
   AM_CHECK_ARG(a->m > 0 && a->x != nullptr && a->out[0] != nullptr, "prefill_linear: bad rows or pointers");
   if (!GemmI4Eligible(a->w, a->m, a->x))
     return SetLastError(AM_STATUS_UNIMPLEMENTED,
-                        "prefill_linear: needs INT4 weights (group a multiple of 64), bf16 rows 16-byte aligned");
+                        "prefill_linear: needs INT4 (group a multiple of 64), INT8 or bf16 weights (k a multiple of "
+                        "128) and bf16 rows 16-byte aligned");
   switch (a->epilogue) {
     case AM_PREFILL_SPLIT:
       return GemmI4(a->x, a->m, a->w, 2, a->out[0], a->out[1], a->out[2], a->split[0], a->split[1], nullptr,

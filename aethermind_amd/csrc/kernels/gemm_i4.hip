@@ -1,41 +1,49 @@
-// Prefill GEMM for INT4 weights on gfx950: out[M,N] = X[M,K] (bf16) @ W[N,K]^T on
-// bf16 MFMA (v_mfma_f32_16x16x32_bf16), with the prefill plan's fused epilogues.
+// Prefill GEMM on gfx950: out[M,N] = X[M,K] (bf16) @ W[N,K]^T on bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16) for INT4 g128, INT8 per-channel and bf16 weights, with the
+// prefill plan's fused epilogues.
 //
 //   * Block tile 128 x 128 (M x N), k step 64, 256 threads = 2 x 2 waves of 64 x 64
-//     (4 x 4 MFMA tiles each); two blocks per CU.
+//     (4 x 4 MFMA tiles each), or 128 x 256 with 8 waves when that still gives every
+//     CU a tile.
 //   * Operands move global -> LDS by DMA (global_load_lds_dwordx4): no registers and no
-//     LDS store instructions, so three k steps are in flight while one is computed (a
-//     step's 20 KB arrive ~1-2 us after issue; one step of MFMAs takes ~0.4 us).  The
-//     ring holds three stages of X (128 rows x 128 B) and W (128 rows x 32 B raw INT4),
-//     plus a four-slot ring of the fp16 group scales.
+//     LDS store instructions, so two or three k steps are in flight while one is
+//     computed.  The ring holds the stages of X (128 rows x 128 B) and W (rows of 32 B
+//     INT4, 64 B INT8 or 128 B bf16 per k step), plus for INT4 a four-slot ring of the
+//     fp16 group scales.
 //   * DMA writes a wave's 64 lanes to 1 KB of consecutive LDS, so the bank layout is
-//     set by which global chunk each lane fetches: 16-byte chunk c of X row r sits at
-//     slot c ^ ((r >> 1) & 7) of the row, and chunk c of W row n at slot c ^ ((n >> 3)
-//     & 1).  The 16 rows read by one MFMA operand fetch then fall into distinct banks.
-//   * The weight stays INT4 in LDS: a lane's B operand (8 k values) is one 32-bit LDS
-//     read, unpacked in registers right before the MFMA with one shift and one AND-OR
-//     per bf16 pair (nibble q+8 in the low mantissa bits of bf16 128.0 reads 136+q).
-//   * The 136 * sum(x) that 136+q adds is taken out on the MFMA: the A operand times an
-//     all -136 B operand gives -136 * (row sum) in exactly the accumulator layout of the
-//     output tiles.  Each group's sum is scaled by its fp16 scale when the group (two k
-//     steps) completes.  Products are exact and accumulation is fp32.
+//     set by which global chunk each lane fetches: 16-byte chunk c of X row r (and of a
+//     bf16 W row) sits at slot c ^ ((r >> 1) & 7) of the row, chunk c of an INT8 W row n
+//     at slot c ^ ((n >> 2) & 3), chunk c of an INT4 W row n at slot c ^ ((n >> 3) & 1).
+//     The 16 rows read by one MFMA operand fetch then fall into distinct banks.
+//   * The weight stays in its storage format in LDS and becomes the bf16 B operand in
+//     registers right before the MFMA.  INT4: one 32-bit read of 8 nibbles, one shift
+//     and one AND-OR per bf16 pair (nibble q+8 in the low mantissa bits of bf16 128.0
+//     reads 136+q).  INT8: one 64-bit read of 8 bytes q+128, each converted exactly
+//     (integers below 256 are exact in bf16).  bf16: one 128-bit read, no conversion.
+//   * The offset the stored codes carry (136 * sum(x) for INT4, 128 * sum(x) for INT8)
+//     is taken out on the MFMA: the A operand times an all -136 (-128) B operand gives
+//     -136 * (row sum) in exactly the accumulator layout of the output tiles.  INT4
+//     scales each group's sum by its fp16 scale when the group (two k steps) completes;
+//     INT8 scales the whole sum by the row's fp32 scale after the split-K merge.
+//     Products are exact and accumulation is fp32.
 //   * Rows past the M or N edge read row 0 and are never stored.
-//   * The k loop runs one INT4 group per iteration: the group's first MFMAs start from
+//   * The INT4 k loop runs one group per iteration: the group's first MFMAs start from
 //     a zero accumulator, so closing a group is one fma per output and no clearing.
 //   * Split-K (tiles that would leave CUs idle): split s of a tile owns a contiguous
-//     range of whole groups.  Each split block stores its fp32 accumulators with
-//     device-scope stores, waits for them, and takes a ticket; the last block of the
-//     tile reads the other partials back with device-scope loads and sums all of them
-//     in split order (the same order whichever block is last, so results do not depend
-//     on scheduling), resets the ticket and runs the epilogue.
+//     range of whole groups (128 k values for INT8 and bf16).  Each split block stores
+//     its fp32 accumulators with device-scope stores, waits for them, and takes a ticket;
+//     the last block of the tile reads the other partials back with device-scope loads
+//     and sums all of them in split order (the same order whichever block is last, so
+//     results do not depend on scheduling), resets the ticket and runs the epilogue.
 //   * Epilogues (the op boundaries of the reference graph, model_graph_builder.cpp:
 //     133-290) go through LDS: the block writes round(acc) as a bf16 tile, then every
 //     thread moves 16-byte row chunks (one load of residual, one store per chunk).
 //     Store; residual (out = round(res + round(acc)), Linear then Add); column split
 //     (one q|k|v weight, three outputs); SiLU-Mul (tile columns [0, BN/2) are gate
 //     features u, [BN/2, BN) the up rows of the same u: act = round(silu(round(gate))
-//     * round(up))).  Chunks that cross the N edge or a split column, or outputs whose
-//     rows are not 16-byte aligned, take the per-element path.
+//     * round(up))); q|k|v with RoPE and the KV cache write.  Chunks that cross the N
+//     edge or a split column, or outputs whose rows are not 16-byte aligned, take the
+//     per-element path.
 
 #include <algorithm>
 #include <type_traits>
@@ -54,23 +62,43 @@ typedef __attribute__((address_space(3))) void lvoid;
 constexpr int QBM = 128, QBK = 64;
 constexpr int XST = QBM * QBK * 2;  // 16 KB of X per stage
 
+// Bytes of one weight row per k step of 64, and the 16-byte chunks they make.
+template <int WF> struct WRow;
+template <> struct WRow<AM_WF_INT4> { static constexpr int kBytes = 32; };
+template <> struct WRow<AM_WF_INT8> { static constexpr int kBytes = 64; };
+template <> struct WRow<AM_WF_BF16> { static constexpr int kBytes = 128; };
+
 // Block shapes: NWN waves along N (64 columns each) by 2 along M.
-//   NWN = 2: 256 threads, 128 x 128 tile, 3 stages (62 KB of LDS, two blocks per CU)
-//   NWN = 4: 512 threads, 128 x 256 tile, 4 stages (100 KB, one block per CU): half
-//            the X bytes per MFMA, which moves most of the traffic.
-template <int NWN>
+//   NWN = 2: 256 threads, 128 x 128 tile, 3 stages (INT4 62 KB of LDS and INT8 72 KB:
+//            two blocks per CU; bf16 96 KB: one)
+//   NWN = 4: 512 threads, 128 x 256 tile, 4 stages (3 for bf16; INT4 100 KB, INT8
+//            128 KB, bf16 144 KB, one block per CU): half the X bytes per MFMA, which
+//            moves most of the traffic.
+template <int WF, int NWN>
 struct Shape {
+  static constexpr bool kI4 = WF == AM_WF_INT4;
   static constexpr int kWaves = 2 * NWN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kBN = 64 * NWN;
-  static constexpr int kStages = NWN == 2 ? 3 : 4;
-  static constexpr int kWSt = kBN * QBK / 2;       // W bytes per stage
+  static constexpr int kStages = NWN == 2 ? 3 : (WF == AM_WF_BF16 ? 3 : 4);
+  static constexpr int kRowB = WRow<WF>::kBytes;   // W row bytes per k step
+  static constexpr int kWSt = kBN * kRowB;         // W bytes per stage
   static constexpr int kStg = XST + kWSt;
-  static constexpr int kScSlot = kBN * 4;          // one dword per weight row
-  static constexpr int kLds = kStages * kStg + 4 * kScSlot;
+  static constexpr int kScSlot = kBN * 4;          // INT4: one dword per weight row
+  static constexpr int kLds = kStages * kStg + (kI4 ? 4 * kScSlot : 0);
   static constexpr int kXi = 16 / kWaves;          // X DMA instructions per wave per step
-  static constexpr int kLoads = kXi + 2;           // + W + scales
+  static constexpr int kWi = kWSt / 1024 / kWaves; // W DMA instructions per wave per step
+  static constexpr int kLoads = kXi + kWi + (kI4 ? 1 : 0);  // + the INT4 scale dword
+  static_assert(kWi >= 1 && kWi * kWaves * 1024 == kWSt, "W stage must be whole DMA instructions per wave");
 };
+
+// Slot of 16-byte chunk c of weight row n within the row's k-step bytes.
+template <int WF>
+__device__ __forceinline__ int wslot(int n, int c) {
+  if constexpr (WF == AM_WF_INT4) return c ^ ((n >> 3) & 1);
+  else if constexpr (WF == AM_WF_INT8) return c ^ ((n >> 2) & 3);
+  else return c ^ ((n & 7) ^ ((n >> 3) & 1));
+}
 
 // X row r's 16-byte chunk c sits at slot c ^ xsw(r) of the row: 8 consecutive rows, and
 // 16 rows taken as two parity classes, land in distinct LDS banks.
@@ -80,9 +108,9 @@ enum I4Epi { kI4Store = 0, kI4Residual = 1, kI4Split = 2, kI4SiluMul = 3, kI4Qkv
 
 struct I4Args {
   const uint16_t* x;  // bf16 [M][K]
-  const uint8_t* w;   // INT4 device tile order, [N][K/2]
-  const uint16_t* s;  // fp16 scales [N][K/group]
-  int32_t M, N, K, group;
+  const uint8_t* w;   // [N][K]: INT4 device order (K/2 bytes a row), INT8 q+128 bytes, or bf16
+  const void* s;      // INT4: fp16 scales [N][K/group]; INT8: fp32 row scales [N]; bf16: unused
+  int32_t M, N, K, group;  // group: the INT4 group; 128 (the split-K unit) for INT8 and bf16
   int32_t ffn;  // SiLU-Mul: rows [0, ffn) gate, [ffn, 2 ffn) up
   uint16_t* out0;
   uint16_t* out1;
@@ -104,6 +132,21 @@ struct I4Args {
   int32_t hd, cap;
   int32_t* err;               // optional: set when a row's position is outside [0, cap)
 };
+
+// 8 bytes q+128 -> 8 exact bf16 values 0..255, in byte order
+__device__ __forceinline__ bf16x8_t bytes8(uint2 v) {
+  const uint32_t w[2] = {v.x, v.y};
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = w[i >> 1];
+    const int sh = 16 * (i & 1);
+    const float lo = static_cast<float>((word >> sh) & 0xFFu), hi = static_cast<float>((word >> (sh + 8)) & 0xFFu);
+    const bf16x2_t h = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    d[i] = __builtin_bit_cast(uint32_t, h);
+  }
+  return __builtin_bit_cast(bf16x8_t, make_uint4(d[0], d[1], d[2], d[3]));
+}
 
 __device__ __forceinline__ bf16x8_t unpack8(uint32_t word, uint32_t mask, uint32_t magic) {
   uint32_t d[4];
@@ -140,9 +183,9 @@ __device__ __forceinline__ void wait_barrier(int ahead) {
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int EPI, int NWN>
-__global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i4_kernel(I4Args p) {
-  using S = Shape<NWN>;
+template <int WF, int EPI, int NWN>
+__global__ __launch_bounds__((Shape<WF, NWN>::kThreads), NWN == 2 ? 2 : 1) void gemm_mfma_kernel(I4Args p) {
+  using S = Shape<WF, NWN>;
   constexpr int BN = S::kBN, NST = S::kStages, STG = S::kStg;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x;
@@ -178,25 +221,42 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
     const int32_t gr = m0 + r < p.M ? m0 + r : 0;
     xsrc[i] = reinterpret_cast<const uint8_t*>(p.x) + (static_cast<int64_t>(gr) * p.K + 8 * c) * 2;
   }
-  // W: wave w moves rows 32w .. 32w+31, two 16-byte chunks per row
-  const int wr = wave * 32 + (lane >> 1);
-  const uint8_t* wsrc =
-      p.w + static_cast<int64_t>(wrow<EPI, BN>(p, tn, wr)) * (p.K / 2) + 16 * ((lane & 1) ^ ((wr >> 3) & 1));
-  // scales: lane -> weight row (wave % NWN) * 64 + lane (waves past NWN repeat the
+  // INT8: the fp32 scales of this lane's four output columns, loaded ahead of every DMA
+  float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if constexpr (WF == AM_WF_INT8) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      rs[nt] = static_cast<const float*>(p.s)[wrow<EPI, BN>(p, tn, wn * 64 + nt * 16 + (lane & 15))];
+  }
+  // W: instruction i of wave w fills 1 KB of the stage's W rows; lane L's 16 bytes land
+  // at row (1024 (w kWi + i) + 16 L) / kRowB, slot ((16 L) mod kRowB) / 16, so it fetches
+  // the chunk whose slot that is (the slot map is an XOR, its own inverse)
+  const int64_t wrow_bytes = static_cast<int64_t>(p.K) / QBK * S::kRowB;
+  const uint8_t* wsrc[S::kWi];
+#pragma unroll
+  for (int i = 0; i < S::kWi; ++i) {
+    const int o = (wave * S::kWi + i) * 1024 + 16 * lane;
+    const int r = o / S::kRowB, slot = (o % S::kRowB) / 16;
+    wsrc[i] = p.w + static_cast<int64_t>(wrow<EPI, BN>(p, tn, r)) * wrow_bytes + 16 * wslot<WF>(r, slot);
+  }
+  // INT4 scales: lane -> weight row (wave % NWN) * 64 + lane (waves past NWN repeat the
   // same rows); the dword holding its fp16
   const int sr = (wave % NWN) * 64 + lane;
-  const int64_t sbase = static_cast<int64_t>(wrow<EPI, BN>(p, tn, sr)) * ng;
+  const int64_t sbase = S::kI4 ? static_cast<int64_t>(wrow<EPI, BN>(p, tn, sr)) * ng : 0;
 
   auto issue = [&](int32_t j) {  // local step j = k step k0 + j
     const int32_t ks = k0 + j;
     uint8_t* st = lds + (j % NST) * STG;
 #pragma unroll
     for (int i = 0; i < S::kXi; ++i) dma16(xsrc[i] + ks * (QBK * 2), st + (wave * S::kXi + i) * 1024);
-    dma16(wsrc + ks * (QBK / 2), st + XST + wave * 1024);
-    const int32_t g = ks / spg;
-    const int64_t se = sbase + g;  // fp16 element; its dword, aligned down
-    dma4(reinterpret_cast<const uint8_t*>(p.s) + ((se * 2) & ~int64_t{3}),
-         lds + NST * STG + (g & 3) * S::kScSlot + (wave % NWN) * 256);
+#pragma unroll
+    for (int i = 0; i < S::kWi; ++i) dma16(wsrc[i] + ks * S::kRowB, st + XST + (wave * S::kWi + i) * 1024);
+    if constexpr (S::kI4) {
+      const int32_t g = ks / spg;
+      const int64_t se = sbase + g;  // fp16 element; its dword, aligned down
+      dma4(reinterpret_cast<const uint8_t*>(p.s) + ((se * 2) & ~int64_t{3}),
+           lds + NST * STG + (g & 3) * S::kScSlot + (wave % NWN) * 256);
+    }
   };
 
   f32x4_t acc[4][4], part[4][4], corr[4];
@@ -211,7 +271,10 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   }
   uint32_t mask = 0x000F000Fu, magic = 0x43004300u;
   asm volatile("" : "+v"(mask), "+v"(magic));
-  const bf16x8_t bneg = __builtin_bit_cast(bf16x8_t, make_uint4(0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u));
+  // the code offset times -1 (INT4 -136, INT8 -128) as an all-equal B operand
+  constexpr uint32_t kNeg = S::kI4 ? 0xC308C308u : 0xC300C300u;
+  constexpr bool kOff = WF != AM_WF_BF16;
+  const bf16x8_t bneg = __builtin_bit_cast(bf16x8_t, make_uint4(kNeg, kNeg, kNeg, kNeg));
 
   // LDS read offsets of this lane (within a stage)
   int aoff[4][2], boff[4][2];
@@ -224,8 +287,16 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int n = wn * 64 + nt * 16 + (lane & 15);
+    const int kb = lane >> 4;  // 8-value k block of this lane's B operand
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) boff[nt][kk] = XST + n * 32 + 16 * (kk ^ ((n >> 3) & 1)) + 4 * (lane >> 4);
+    for (int kk = 0; kk < 2; ++kk) {
+      if constexpr (WF == AM_WF_INT4)
+        boff[nt][kk] = XST + n * 32 + 16 * wslot<WF>(n, kk) + 4 * kb;
+      else if constexpr (WF == AM_WF_INT8)
+        boff[nt][kk] = XST + n * 64 + 16 * wslot<WF>(n, 2 * kk + (kb >> 1)) + 8 * (kb & 1);
+      else
+        boff[nt][kk] = XST + n * 128 + 16 * wslot<WF>(n, 4 * kk + kb);
+    }
   }
   // scale of this lane's column of tile nt in group g: the half of the slot dword that
   // holds element (row * ng + g)
@@ -234,7 +305,7 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
   for (int nt = 0; nt < 4; ++nt) {
     const int n = wn * 64 + nt * 16 + (lane & 15);
     soff[nt] = NST * STG + n * 4;
-    shalf_base[nt] = static_cast<int>(static_cast<int64_t>(wrow<EPI, BN>(p, tn, n)) * ng & 1);
+    shalf_base[nt] = S::kI4 ? static_cast<int>(static_cast<int64_t>(wrow<EPI, BN>(p, tn, n)) * ng & 1) : 0;
   }
 
   // prologue: steps 0 .. NST-2 in flight
@@ -258,11 +329,18 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) af[mt] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + aoff[mt][kk]));
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        bfr[nt] = unpack8(*reinterpret_cast<const uint32_t*>(st + boff[nt][kk]), mask, magic);
+      for (int nt = 0; nt < 4; ++nt) {
+        if constexpr (WF == AM_WF_INT4)
+          bfr[nt] = unpack8(*reinterpret_cast<const uint32_t*>(st + boff[nt][kk]), mask, magic);
+        else if constexpr (WF == AM_WF_INT8)
+          bfr[nt] = bytes8(*reinterpret_cast<const uint2*>(st + boff[nt][kk]));
+        else
+          bfr[nt] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(st + boff[nt][kk]));
+      }
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        corr[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bneg, (FIRST && kk == 0) ? zero4 : corr[mt], 0, 0, 0);
+        if constexpr (kOff)
+          corr[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bneg, (FIRST && kk == 0) ? zero4 : corr[mt], 0, 0, 0);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)
           part[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], (FIRST && kk == 0) ? zero4 : part[mt][nt],
@@ -271,20 +349,32 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
     }
   };
   int32_t j = 0;
-  for (int32_t g = g0; g < g1; ++g) {
-    step(j++, std::true_type{});
-    for (int32_t t = 1; t < spg; ++t) step(j++, std::false_type{});
-    // the group closes: scale and fold into acc
+  if constexpr (S::kI4) {
+    for (int32_t g = g0; g < g1; ++g) {
+      step(j++, std::true_type{});
+      for (int32_t t = 1; t < spg; ++t) step(j++, std::false_type{});
+      // the group closes: scale and fold into acc
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + soff[nt] + (g & 3) * S::kScSlot);
-      const uint32_t bits = ((shalf_base[nt] + g) & 1) ? (sw >> 16) : (sw & 0xFFFFu);
-      const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+      for (int nt = 0; nt < 4; ++nt) {
+        const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + soff[nt] + (g & 3) * S::kScSlot);
+        const uint32_t bits = ((shalf_base[nt] + g) & 1) ? (sw >> 16) : (sw & 0xFFFFu);
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(sc, part[mt][nt][r] + corr[mt][r], acc[mt][nt][r]);
+          for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(sc, part[mt][nt][r] + corr[mt][r], acc[mt][nt][r]);
+      }
     }
+  } else {
+    // one running sum over the split's k range (the row scale comes after the merge)
+    step(j++, std::true_type{});
+    while (j < nk) step(j++, std::false_type{});
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = kOff ? part[mt][nt][r] + corr[mt][r] : part[mt][nt][r];
   }
 
   if (p.splits > 1) {
@@ -334,6 +424,14 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i / 4][i % 4] = sum[i];
     if (tid == 0) __hip_atomic_store(&p.tickets[bid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if constexpr (WF == AM_WF_INT8) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] *= rs[nt];
   }
   // ---- epilogue: round(acc) as a bf16 tile in LDS (lane holds D[4*(lane/16)+r][lane%16]
   // of each 16x16 tile), then 16-byte row chunks ----
@@ -523,7 +621,8 @@ __global__ __launch_bounds__(Shape<NWN>::kThreads, NWN == 2 ? 2 : 1) void gemm_i
 template <int EPI, int NWN>
 int64_t TilesOf(const I4Args& p) {
   const int64_t tiles_m = CeilDiv(p.M, QBM);
-  return tiles_m * (EPI == kI4SiluMul ? p.ffn / (Shape<NWN>::kBN / 2) : CeilDiv(p.N, Shape<NWN>::kBN));
+  constexpr int64_t BN = 64 * NWN;
+  return tiles_m * (EPI == kI4SiluMul ? p.ffn / (BN / 2) : CeilDiv(p.N, BN));
 }
 
 constexpr int64_t kTicketRegion = 4096;               // bytes at the start of the workspace
@@ -549,14 +648,14 @@ int SplitsFor(int64_t tiles, int64_t groups, int64_t cus) {
 int64_t TicketBytes(int64_t) { return kTicketRegion; }
 template <int NWN>
 int64_t PartialBytes(int64_t tiles, int splits) {
-  return splits > 1 ? tiles * splits * Shape<NWN>::kWaves * (16 * 64 * 16) : 0;
+  return splits > 1 ? tiles * splits * (2 * NWN) * (16 * 64 * 16) : 0;
 }
 
-template <int EPI, int NWN>
-am_status_code LaunchI4(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
-  using S = Shape<NWN>;
+template <int WF, int EPI, int NWN>
+am_status_code LaunchMfma(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
+  using S = Shape<WF, NWN>;
   static const bool lds_ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_i4_kernel<EPI, NWN>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_mfma_kernel<WF, EPI, NWN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds) == hipSuccess;
   if (!lds_ok) return SetLastError(AM_STATUS_INTERNAL, "gemm_i4: could not set the dynamic LDS size");
   const int64_t tiles = TilesOf<EPI, NWN>(p);
@@ -569,8 +668,10 @@ am_status_code LaunchI4(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
   }
   const int64_t blocks = tiles * splits;
   static const char* const names[] = {"store", "residual", "split", "silu_mul", "qkv_rope_kv"};
-  RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_i4<%s,bn=%d,splits=%d>", names[EPI], S::kBN, splits);
-  hipLaunchKernelGGL((gemm_i4_kernel<EPI, NWN>), dim3(static_cast<unsigned>(blocks)), dim3(S::kThreads), S::kLds, s, p);
+  const char* fmt = WF == AM_WF_INT4 ? "i4" : WF == AM_WF_INT8 ? "i8" : "bf16";
+  RecordLaunch(blocks, S::kThreads, S::kLds, "gemm_%s<%s,bn=%d,splits=%d>", fmt, names[EPI], S::kBN, splits);
+  hipLaunchKernelGGL((gemm_mfma_kernel<WF, EPI, NWN>), dim3(static_cast<unsigned>(blocks)), dim3(S::kThreads), S::kLds,
+                     s, p);
   AM_RETURN_IF_LAUNCH_FAILED("gemm_i4");
   return AM_STATUS_OK;
 }
@@ -583,19 +684,44 @@ bool WideI4(const I4Args& p) {
   return (EPI != kI4SiluMul || p.ffn % 128 == 0) && tiles_m * CeilDiv(cols, 256) >= DeviceCUs();
 }
 
-template <int EPI>
-am_status_code LaunchI4Any(const I4Args& p, void* ws, int64_t ws_bytes, hipStream_t s) {
-  return WideI4<EPI>(p) ? LaunchI4<EPI, 4>(p, ws, ws_bytes, s) : LaunchI4<EPI, 2>(p, ws, ws_bytes, s);
+template <int WF, int EPI>
+am_status_code LaunchWF(const I4Args& p, void* ws, int64_t ws_bytes, hipStream_t s) {
+  return WideI4<EPI>(p) ? LaunchMfma<WF, EPI, 4>(p, ws, ws_bytes, s) : LaunchMfma<WF, EPI, 2>(p, ws, ws_bytes, s);
 }
+
+// The weight format picks the kernel (p.group: the INT4 group, 128 otherwise).
+template <int EPI>
+am_status_code LaunchI4Any(const I4Args& p, int32_t fmt, void* ws, int64_t ws_bytes, hipStream_t s) {
+  switch (fmt) {
+    case AM_WF_INT4: return LaunchWF<AM_WF_INT4, EPI>(p, ws, ws_bytes, s);
+    case AM_WF_INT8: return LaunchWF<AM_WF_INT8, EPI>(p, ws, ws_bytes, s);
+    default: return LaunchWF<AM_WF_BF16, EPI>(p, ws, ws_bytes, s);
+  }
+}
+
+// Split-K unit along k: the INT4 group, 128 values for INT8 and bf16 weights.
+int32_t SplitUnit(const am_gfx950_weight& w) { return w.format == AM_WF_INT4 ? w.group_size : 2 * QBK; }
 
 bool Aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 }  // namespace
 
-// INT4 weights with group % 64 == 0 and K % group == 0, bf16 activations.
+// bf16 activations with INT4 weights (group % 64 == 0 and K % group == 0), INT8
+// per-channel weights (K % 128 == 0) or bf16 weights (K % 128 == 0).
 bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x) {
-  return w.format == AM_WF_INT4 && w.scales != nullptr && w.group_size > 0 && w.group_size % QBK == 0 &&
-         w.k % w.group_size == 0 && m > 0 && m * w.k < (int64_t{1} << 31) && w.n * (w.k / 2) < (int64_t{1} << 31) &&
+  bool fmt = false;
+  int64_t row_bytes = 0;
+  if (w.format == AM_WF_INT4) {
+    fmt = w.scales != nullptr && w.group_size > 0 && w.group_size % QBK == 0 && w.k % w.group_size == 0;
+    row_bytes = w.k / 2;
+  } else if (w.format == AM_WF_INT8) {
+    fmt = w.scales != nullptr && w.k % (2 * QBK) == 0;
+    row_bytes = w.k;
+  } else if (w.format == AM_WF_BF16) {
+    fmt = w.k % (2 * QBK) == 0;
+    row_bytes = 2 * w.k;
+  }
+  return fmt && m > 0 && m * w.k < (int64_t{1} << 31) && w.n * row_bytes < (int64_t{1} << 31) &&
          m * w.n < (int64_t{1} << 31) && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
@@ -617,8 +743,8 @@ int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group) {
 // q|k|v GEMM with the RoPE and KVCacheUpdate nodes in the epilogue (one sequence).
 am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight& w, const am_gfx950_prefill_rope_kv& r,
                                void* q_out, void* ws, int64_t ws_bytes, hipStream_t s) {
-  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unsupported shape or weight");
-  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm_i4: workspace must be 16-byte aligned");
+  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm: unsupported shape or weight");
+  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm: workspace must be 16-byte aligned");
   AM_CHECK_ARG(r.head_dim == 64 || r.head_dim == 128, "prefill q|k|v RoPE: head_dim must be 64 or 128");
   AM_CHECK_ARG(r.hq > 0 && r.hkv > 0 && r.hq % r.hkv == 0 && w.n == (r.hq + 2 * r.hkv) * r.head_dim,
                "prefill q|k|v RoPE: the weight rows must be hq + 2 hkv heads");
@@ -632,11 +758,11 @@ am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight&
   I4Args p{};
   p.x = static_cast<const uint16_t*>(x);
   p.w = static_cast<const uint8_t*>(w.data);
-  p.s = static_cast<const uint16_t*>(w.scales);
+  p.s = w.scales;
   p.M = static_cast<int32_t>(m);
   p.N = static_cast<int32_t>(w.n);
   p.K = static_cast<int32_t>(w.k);
-  p.group = w.group_size;
+  p.group = SplitUnit(w);
   p.out0 = static_cast<uint16_t*>(q_out);
   p.c1 = static_cast<int32_t>(r.hq * r.head_dim);
   p.c2 = static_cast<int32_t>((r.hq + r.hkv) * r.head_dim);
@@ -652,22 +778,22 @@ am_status_code GemmI4QkvRopeKv(const void* x, int64_t m, const am_gfx950_weight&
   p.err = r.err_flag;
   if (auto st = MakeKvRows(r.pages, 0, r.capacity, r.hkv, r.head_dim, &p.kv); st != AM_STATUS_OK) return st;
   if (p.kv.err == nullptr) p.kv.err = r.err_flag;
-  return LaunchI4Any<kI4QkvRope>(p, ws, ws_bytes, s);
+  return LaunchI4Any<kI4QkvRope>(p, w.format, ws, ws_bytes, s);
 }
 
 am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32_t epi, void* out0, void* out1,
                       void* out2, int64_t c1, int64_t c2, const void* residual, void* ws, int64_t ws_bytes,
                       hipStream_t s) {
-  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unsupported shape or weight");
-  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm_i4: workspace must be 16-byte aligned");
+  if (!GemmI4Eligible(w, m, x)) return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm: unsupported shape or weight");
+  AM_CHECK_ARG(ws == nullptr || (Aligned16(ws) && ws_bytes >= 0), "gemm: workspace must be 16-byte aligned");
   I4Args p{};
   p.x = static_cast<const uint16_t*>(x);
   p.w = static_cast<const uint8_t*>(w.data);
-  p.s = static_cast<const uint16_t*>(w.scales);
+  p.s = w.scales;
   p.M = static_cast<int32_t>(m);
   p.N = static_cast<int32_t>(w.n);
   p.K = static_cast<int32_t>(w.k);
-  p.group = w.group_size;
+  p.group = SplitUnit(w);
   p.out0 = static_cast<uint16_t*>(out0);
   p.out1 = static_cast<uint16_t*>(out1);
   p.out2 = static_cast<uint16_t*>(out2);
@@ -688,19 +814,19 @@ am_status_code GemmI4(const void* x, int64_t m, const am_gfx950_weight& w, int32
   }
   p.vec = vec ? 1 : 0;
   switch (epi) {
-    case kI4Store: return LaunchI4Any<kI4Store>(p, ws, ws_bytes, s);
+    case kI4Store: return LaunchI4Any<kI4Store>(p, w.format, ws, ws_bytes, s);
     case kI4Residual:
-      AM_CHECK_ARG(residual != nullptr, "gemm_i4: residual epilogue without a residual");
-      return LaunchI4Any<kI4Residual>(p, ws, ws_bytes, s);
+      AM_CHECK_ARG(residual != nullptr, "gemm: residual epilogue without a residual");
+      return LaunchI4Any<kI4Residual>(p, w.format, ws, ws_bytes, s);
     case kI4Split:
       AM_CHECK_ARG(0 < c1 && c1 <= c2 && c2 <= w.n && out0 && (c2 == c1 || out1) && (c2 == w.n || out2),
-                   "gemm_i4: bad column split");
-      return LaunchI4Any<kI4Split>(p, ws, ws_bytes, s);
+                   "gemm: bad column split");
+      return LaunchI4Any<kI4Split>(p, w.format, ws, ws_bytes, s);
     case kI4SiluMul:
-      AM_CHECK_ARG(w.n % 128 == 0, "gemm_i4: SiLU-Mul needs 2*ffn rows with ffn a multiple of 64");
+      AM_CHECK_ARG(w.n % 128 == 0, "gemm: SiLU-Mul needs 2*ffn rows with ffn a multiple of 64");
       p.ffn = static_cast<int32_t>(w.n / 2);
-      return LaunchI4Any<kI4SiluMul>(p, ws, ws_bytes, s);
-    default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm_i4: unknown epilogue");
+      return LaunchI4Any<kI4SiluMul>(p, w.format, ws, ws_bytes, s);
+    default: return SetLastError(AM_STATUS_INVALID_ARGUMENT, "gemm: unknown epilogue");
   }
 }
 

@@ -117,14 +117,15 @@ typedef struct am_gfx950_linear_args {
   int32_t mode;
   void* workspace;      /* optional (NULL): am_gfx950_gemm_workspace_bytes(m, n, k, group) bytes,
                            16-byte aligned, zero before the first call (left zero); lets the
-                           INT4 MFMA GEMM split K when its tiles alone leave CUs idle */
+                           MFMA GEMM split K when its tiles alone leave CUs idle */
   int64_t workspace_bytes;
 } am_gfx950_linear_args;
 am_status_code am_gfx950_linear(const am_gfx950_linear_args* args, void* hip_stream);
 
 /* Prefill fusions of Linear with the next reference node, on the MFMA GEMM (m rows of
- * bf16 activations, INT4 weights with group a multiple of 64; other formats return
- * AM_STATUS_UNIMPLEMENTED and take am_gfx950_linear per node):
+ * bf16 activations; INT4 weights with group a multiple of 64, INT8 per-channel or bf16
+ * weights with k a multiple of 128; fp32 weights return AM_STATUS_UNIMPLEMENTED and
+ * take am_gfx950_linear per node):
  *   AM_PREFILL_SPLIT     one weight whose row ranges are several Linears (q|k|v):
  *                        columns [0, split[0]) -> out[0] [m][split[0]], [split[0],
  *                        split[1]) -> out[1], [split[1], n) -> out[2]; each rounded
@@ -168,9 +169,10 @@ typedef struct am_gfx950_prefill_linear_args {
 } am_gfx950_prefill_linear_args;
 am_status_code am_gfx950_prefill_linear(const am_gfx950_prefill_linear_args* args, void* hip_stream);
 
-/* Workspace bytes with which the INT4 prefill GEMM of an m x n x k product (INT4
- * group size group_size) may split K: split s of an output tile sums a contiguous
- * range of whole groups, and the tile's last split block adds the fp32 partials in
+/* Workspace bytes with which the prefill GEMM of an m x n x k product may split K
+ * (group_size: the INT4 group; 128 for INT8 and bf16 weights, whose splits are whole
+ * 128-value ranges of k): split s of an output tile sums a contiguous range of whole
+ * groups, and the tile's last split block adds the fp32 partials in
  * split order (results are independent of block scheduling).  0: the shape never
  * splits (its tiles already fill the device).  The first 4096 bytes are the tickets
  * (one u32 per tile of the launch), which must be zero before the first call and are

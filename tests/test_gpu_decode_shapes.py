@@ -240,7 +240,7 @@ def test_prefill_gemm_8b(fmt, shape):
     out = empty((m, n), torch.int16)
     L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2), stream())
     k = launched()
-    assert k.startswith("gemm_i4<store," if wf == N.AM_WF_INT4 else "gemm<"), k
+    assert k.startswith({N.AM_WF_INT4: "gemm_i4", N.AM_WF_INT8: "gemm_i8", N.AM_WF_BF16: "gemm_bf16"}[wf] + "<store,"), k
     got = rd(out)
     rows = [0, 1, 127, 128, 200, 255, 256, 300, 383, 384, 450, 511]
     ref = O.linear(np.ascontiguousarray(x[rows]), w)

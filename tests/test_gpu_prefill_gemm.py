@@ -1,5 +1,5 @@
-"""The prefill GEMM for INT4 weights (gemm_i4.hip) and its fused epilogues, through
-the C ABI, against the CPU oracle: am_gfx950_linear (store, residual) and
+"""The prefill GEMM (gemm_i4.hip: INT4 g128, INT8 per-channel and bf16 weights on one
+kernel template) and its fused epilogues, through the C ABI, against the CPU oracle: am_gfx950_linear (store, residual) and
 am_gfx950_prefill_linear (q|k|v column split, gate|up SiLU-Mul) at the 8B prefill
 shapes (512 rows; q|k|v 6144x4096, gate|up 28672x4096, down 4096x14336) and at ragged
 shapes (rows and columns that are not tile multiples, a k of one group, groups of 256).
@@ -30,13 +30,32 @@ L = N.lib()
 TOL = 2e-2
 
 
-def int4_weight(n, k, seed, group=128):
+FMTS = [N.AM_WF_INT4, N.AM_WF_INT8, N.AM_WF_BF16]
+PRE = {N.AM_WF_INT4: "gemm_i4", N.AM_WF_INT8: "gemm_i8", N.AM_WF_BF16: "gemm_bf16"}
+
+
+def weight(n, k, seed, group=128, fmt=N.AM_WF_INT4):
+    """A device weight of format fmt repacked from seeded bf16 values, and the oracle's
+    dequantized fp32 matrix of the same weight (the build SPEC's quantization)."""
     rng = np.random.default_rng(seed)
     bits = bf16_rne_bits(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
     w = bits_f32(bits)
-    dw, keep = pack_weight(w, N.AM_WF_INT4, group, src_bf16_bits=bits)
-    pk, sc = O.quant_int4(w, group)
-    return O.dequant_int4(pk, sc, k, group), dw, keep[:2]
+    dw, keep = pack_weight(w, fmt, group, src_bf16_bits=bits)
+    if fmt == N.AM_WF_INT4:
+        pk, sc = O.quant_int4(w, group)
+        w = O.dequant_int4(pk, sc, k, group)
+    elif fmt == N.AM_WF_INT8:
+        w = O.dequant_int8(*O.quant_int8(w))
+    return w, dw, keep[:2]
+
+
+def int4_weight(n, k, seed, group=128):
+    return weight(n, k, seed, group, N.AM_WF_INT4)
+
+
+def unit(fmt, group=128):
+    """the split-K unit along k: the INT4 group, 128 for INT8 and bf16"""
+    return group if fmt == N.AM_WF_INT4 else 128
 
 
 def sample_rows(m):
@@ -48,17 +67,18 @@ def rd(t):
     return O.bf16_to_f32(bits_host(t))
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("m", [512, 200, 17])
-def test_split_qkv(m):
+def test_split_qkv(m, fmt):
     n_q, n_kv, k = 4096, 1024, 4096
-    w, dw, keep = int4_weight(n_q + 2 * n_kv, k, seed=201)
+    w, dw, keep = weight(n_q + 2 * n_kv, k, seed=201, fmt=fmt)
     x = act_rows(202, m, k)
     xd = bf16_dev(bf16_rne_bits(x))
     outs = [empty((m, n), torch.int16) for n in (n_q, n_kv, n_kv)]
     a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SPLIT, (N.vp * 3)(*[p(o) for o in outs]),
                             (N.i64 * 2)(n_q, n_q + n_kv))
     L.call("am_gfx950_prefill_linear", a, stream())
-    assert launched().startswith("gemm_i4<split,"), launched()
+    assert launched().startswith(PRE[fmt] + "<split,"), launched()
     rows = sample_rows(m)
     ref = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
     got = np.concatenate([rd(o) for o in outs], axis=1)
@@ -68,16 +88,17 @@ def test_split_qkv(m):
             close(got[r, c0:c1], ref[i, c0:c1], TOL, f"row {r} cols {c0}:{c1}")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("m", [512, 77])
-def test_silu_mul_gate_up(m):
+def test_silu_mul_gate_up(m, fmt):
     F, k = 14336, 4096
-    w, dw, keep = int4_weight(2 * F, k, seed=211)
+    w, dw, keep = weight(2 * F, k, seed=211, fmt=fmt)
     x = act_rows(212, m, k)
     xd = bf16_dev(bf16_rne_bits(x))
     out = empty((m, F), torch.int16)
     a = N.PrefillLinearArgs(p(xd), m, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0))
     L.call("am_gfx950_prefill_linear", a, stream())
-    assert launched() == ("gemm_i4<silu_mul,bn=256,splits=1>" if m >= 256 else "gemm_i4<silu_mul,bn=128,splits=1>"), \
+    assert launched() == (PRE[fmt] + ("<silu_mul,bn=256,splits=1>" if m >= 256 else "<silu_mul,bn=128,splits=1>")), \
         launched()
     rows = sample_rows(m)
     gu = rbf(O.linear(np.ascontiguousarray(x[rows]), w))
@@ -91,15 +112,16 @@ def test_silu_mul_gate_up(m):
 
 @pytest.mark.parametrize("shape", [(512, 4096, 14336, 128), (200, 4096, 4096, 128), (130, 260, 512, 256),
                                    (33, 130, 128, 128), (512, 16384, 512, 64)])
-def test_linear_store_and_residual(shape):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_linear_store_and_residual(shape, fmt):
     m, n, k, group = shape
-    w, dw, keep = int4_weight(n, k, seed=221 + n, group=group)
+    w, dw, keep = weight(n, k, seed=221 + n, group=group, fmt=fmt)
     x = act_rows(222, m, k)
     res = act_rows(223, m, n)
     xd, rdv = bf16_dev(bf16_rne_bits(x)), bf16_dev(bf16_rne_bits(res))
     out = empty((m, n), torch.int16)
     L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2), stream())
-    assert launched().startswith("gemm_i4<store,"), launched()
+    assert launched().startswith(PRE[fmt] + "<store,"), launched()
     rows = sample_rows(m)
     ref = O.linear(np.ascontiguousarray(x[rows]), w)
     got = rd(out)
@@ -107,7 +129,7 @@ def test_linear_store_and_residual(shape):
         close(got[r], rbf(ref[i]), TOL, f"store row {r} {shape}")
     # Linear then Add, in place on the residual (out aliases residual)
     L.call("am_gfx950_linear", N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(rdv), N.AM_DT_BF16, p(rdv), 2), stream())
-    assert launched().startswith("gemm_i4<residual,"), launched()
+    assert launched().startswith(PRE[fmt] + "<residual,"), launched()
     got = rd(rdv)
     for i, r in enumerate(rows):
         close(got[r], rbf(res[r] + rbf(ref[i])), TOL, f"residual row {r} {shape}")
@@ -133,13 +155,14 @@ SPLIT_SHAPES = [(512, 4096, 4096, 128, 2), (512, 4096, 14336, 128, 4), (100, 520
 
 
 @pytest.mark.parametrize("shape", SPLIT_SHAPES)
-def test_split_k_residual(shape):
+@pytest.mark.parametrize("fmt", FMTS)
+def test_split_k_residual(shape, fmt):
     m, n, k, group, want = shape
-    w, dw, keep = int4_weight(n, k, seed=241 + n, group=group)
+    w, dw, keep = weight(n, k, seed=241 + n, group=group, fmt=fmt)
     x = act_rows(242, m, k)
     res = act_rows(243, m, n)
     xd = bf16_dev(bf16_rne_bits(x))
-    nbytes, ws = workspace(m, n, k, group)
+    nbytes, ws = workspace(m, n, k, unit(fmt, group))
     assert nbytes > 0
     rows = sample_rows(m)
     ref = O.linear(np.ascontiguousarray(x[rows]), w)
@@ -149,7 +172,7 @@ def test_split_k_residual(shape):
         args = N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(rdv), N.AM_DT_BF16, p(rdv), 2)
         args.workspace, args.workspace_bytes = p(ws), nbytes
         L.call("am_gfx950_linear", args, stream())
-        assert launched().startswith("gemm_i4<residual,") and splits_of(launched()) == want, launched()
+        assert launched().startswith(PRE[fmt] + "<residual,") and splits_of(launched()) == want, launched()
         got = rd(rdv)
         for i, r in enumerate(rows):
             close(got[r], rbf(res[r] + rbf(ref[i])), TOL, f"split residual row {r} {shape} call {rep}")
@@ -161,7 +184,7 @@ def test_split_k_residual(shape):
     args = N.LinearArgs(p(xd), N.AM_DT_BF16, m, dw, p(out), N.AM_DT_BF16, None, 2)
     args.workspace, args.workspace_bytes = p(ws), nbytes
     L.call("am_gfx950_linear", args, stream())
-    assert launched().startswith("gemm_i4<store,") and splits_of(launched()) == want, launched()
+    assert launched().startswith(PRE[fmt] + "<store,") and splits_of(launched()) == want, launched()
     got = rd(out)
     for i, r in enumerate(rows):
         close(got[r], rbf(ref[i]), TOL, f"split store row {r} {shape}")
@@ -200,7 +223,8 @@ def test_split_k_qkv_and_silu_few_rows():
     assert tickets_zero(ws, F // 64), "tickets not left at zero"
 
 
-def test_split_k_shapes_share_one_workspace():
+@pytest.mark.parametrize("fmt", FMTS)
+def test_split_k_shapes_share_one_workspace(fmt):
     """A session's prefill runs q|k|v, o, gate|up and down on one workspace: a launch
     with few tiles leaves its partials where a launch with more tiles keeps tickets
     unless the ticket region is the same for every shape.  2048-wide layer at 24 rows:
@@ -210,9 +234,9 @@ def test_split_k_shapes_share_one_workspace():
     nbytes = max(L.am_gfx950_gemm_workspace_bytes(m, n, k, 128) for n, k in shapes)
     ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
     # the third value keeps the device tensors the weight structs point into alive
-    wq, dq, kq = int4_weight(nq + 2 * nkv, H, seed=271)
-    wg, dg, kg = int4_weight(2 * F, H, seed=272)
-    wd, dd, kd = int4_weight(H, F, seed=273)
+    wq, dq, kq = weight(nq + 2 * nkv, H, seed=271, fmt=fmt)
+    wg, dg, kg = weight(2 * F, H, seed=272, fmt=fmt)
+    wd, dd, kd = weight(H, F, seed=273, fmt=fmt)
     x = act_rows(274, m, H)
     xd = bf16_dev(bf16_rne_bits(x))
     rows = sample_rows(m)
@@ -221,7 +245,7 @@ def test_split_k_shapes_share_one_workspace():
         a = N.PrefillLinearArgs(p(xd), m, dq, N.AM_PREFILL_SPLIT, (N.vp * 3)(*[p(o) for o in outs]),
                                 (N.i64 * 2)(nq, nq + nkv), p(ws), nbytes)
         L.call("am_gfx950_prefill_linear", a, stream())
-        assert launched().startswith("gemm_i4<split,") and splits_of(launched()) > 1, launched()
+        assert launched().startswith(PRE[fmt] + "<split,") and splits_of(launched()) > 1, launched()
         got = np.concatenate([rd(o) for o in outs], axis=1)
         ref = rbf(O.linear(np.ascontiguousarray(x[rows]), wq))
         for i, r in enumerate(rows):
@@ -230,7 +254,7 @@ def test_split_k_shapes_share_one_workspace():
         a = N.PrefillLinearArgs(p(xd), m, dg, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(act), None, None),
                                 (N.i64 * 2)(0, 0), p(ws), nbytes)
         L.call("am_gfx950_prefill_linear", a, stream())
-        assert launched().startswith("gemm_i4<silu_mul,") and splits_of(launched()) > 1, launched()
+        assert launched().startswith(PRE[fmt] + "<silu_mul,") and splits_of(launched()) > 1, launched()
         gu = rbf(O.linear(np.ascontiguousarray(x[rows]), wg))
         ref = rbf(O.silu_mul(gu[:, :F], gu[:, F:]))
         got = rd(act)
@@ -241,7 +265,7 @@ def test_split_k_shapes_share_one_workspace():
         args = N.LinearArgs(p(act), N.AM_DT_BF16, m, dd, p(out), N.AM_DT_BF16, None, 2)
         args.workspace, args.workspace_bytes = p(ws), nbytes
         L.call("am_gfx950_linear", args, stream())
-        assert launched().startswith("gemm_i4<store,") and splits_of(launched()) > 1, launched()
+        assert launched().startswith(PRE[fmt] + "<store,") and splits_of(launched()) > 1, launched()
         ref = rbf(O.linear(np.ascontiguousarray(a_host[rows]), wd))
         got = rd(out)
         for i, r in enumerate(rows):
@@ -250,12 +274,12 @@ def test_split_k_shapes_share_one_workspace():
     del kq, kg, kd
 
 
-def qkv_rope_run(m, start, hq=16, hkv=4, d=128, H=2048, cap=256, with_ws=True, seed=281):
+def qkv_rope_run(m, start, hq=16, hkv=4, d=128, H=2048, cap=256, with_ws=True, seed=281, fmt=N.AM_WF_INT4):
     """One AM_PREFILL_QKV_ROPE_KV launch on fresh zeroed cache planes; returns the
     oracle inputs and the device outputs."""
     import ctypes as C
     n = (hq + 2 * hkv) * d
-    w, dw, keep = int4_weight(n, H, seed=seed)
+    w, dw, keep = weight(n, H, seed=seed, fmt=fmt)
     x = act_rows(seed + 1, m, H)
     xd = bf16_dev(bf16_rne_bits(x))
     ctab, stab = O.rope_tables(cap, d, 10000.0)
@@ -276,14 +300,15 @@ def qkv_rope_run(m, start, hq=16, hkv=4, d=128, H=2048, cap=256, with_ws=True, s
     return x, w, ctab, stab, out, name
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("m,start", [(200, 37), (24, 100), (1, 255)])
-def test_qkv_rope_kv_epilogue(m, start):
+def test_qkv_rope_kv_epilogue(m, start, fmt):
     """q|k|v GEMM with RoPE and the KV cache write in the epilogue, against the
     oracle's Linear -> bf16 -> RoPE -> bf16 (q, k) and Linear -> bf16 (v) at positions
     start + i; cache rows outside [start, start + m) stay untouched.  24 rows split K."""
     hq, hkv, d, cap = 16, 4, 128, 256
-    x, w, ctab, stab, out, name = qkv_rope_run(m, start)
-    assert name.startswith("gemm_i4<qkv_rope_kv,"), name
+    x, w, ctab, stab, out, name = qkv_rope_run(m, start, fmt=fmt)
+    assert name.startswith(PRE[fmt] + "<qkv_rope_kv,"), name
     if m == 24:
         assert splits_of(name) > 1, name
     rows = sample_rows(m)
@@ -366,9 +391,10 @@ def test_workspace_too_small_runs_unsplit():
 
 
 def test_prefill_linear_rejects_other_formats():
+    """fp32 weights have no MFMA prefill kernel: the fused entry point refuses them
+    (the plan takes one node per Linear instead)."""
     rng = np.random.default_rng(3)
-    bits = bf16_rne_bits(rng.standard_normal((256, 512), dtype=np.float32))
-    dw, keep = pack_weight(bits_f32(bits), N.AM_WF_BF16, 128, src_bf16_bits=bits)
+    dw, keep = pack_weight(rng.standard_normal((256, 512), dtype=np.float32), N.AM_WF_F32, 128)
     x = bf16_dev(bf16_rne_bits(act_rows(4, 64, 512)))
     out = empty((64, 128), torch.int16)
     a = N.PrefillLinearArgs(p(x), 64, dw, N.AM_PREFILL_SILU_MUL, (N.vp * 3)(p(out), None, None), (N.i64 * 2)(0, 0))
