@@ -130,6 +130,39 @@ def test_embedding_bf16_large_exact():
     assert np.array_equal(bits_host(out), bits[ids])
 
 
+def _bf16_special_table(H=64):
+    """fp32 bit patterns that exercise every branch of float -> bf16: NaN payloads of
+    both signs, +-inf, +-0, fp32 subnormals, exact round-half-even ties both ways,
+    values that round up across an exponent and into inf, plus random normals."""
+    pats = [0x7FC00000, 0x7F800001, 0xFFC00000, 0xFF800001, 0x7FFFFFFF, 0xFFFFFFFF, 0x7FA00000,  # NaN
+            0x7F800000, 0xFF800000, 0x00000000, 0x80000000,                                     # inf, zero
+            0x00000001, 0x807FFFFF, 0x00400000, 0x00008000, 0x00018000,                         # subnormal
+            0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000,                                     # ties
+            0x3F808001, 0x3F807FFF, 0x3FFF8000, 0x477F8000, 0x7F7F8000, 0x7F7FFFFF, 0xFF7FFFFF]  # carries
+    rng = np.random.default_rng(5)
+    rest = rng.standard_normal(4 * H - len(pats)).astype(np.float32).view(np.uint32)
+    return np.concatenate([np.array(pats, np.uint32), rest]).view(np.float32).reshape(4, H)
+
+
+def test_f32_to_bf16_conversion_special_values_bitexact():
+    """The device conversion (RNE, every NaN -> 0x7FC0: the reference's
+    bfloat16.cpp:20-32) through the embedding gather of an fp32 table into bf16 rows,
+    bit for bit against the oracle's conversion (pinned to the reference's patterns in
+    tests/test_oracle.py)."""
+    table = _bf16_special_table()
+    want = O.bf16_bits(table)
+    assert np.all(want[0, :7] == 0x7FC0) and want[0, 7] == 0x7F80 and want[0, 8] == 0xFF80
+    ids = dev(np.array([0, 1, 2, 3], np.int64))
+    t = dev(table)
+    out = empty((4, table.shape[1]), torch.int16)
+    L.call("am_gfx950_embedding", N.EmbeddingArgs(p(ids), N.AM_DT_I64, 4, p(t), N.AM_DT_F32, 4, table.shape[1], p(out),
+                                                  N.AM_DT_BF16, None, 0), stream())
+    got = bits_host(out)
+    bad = np.flatnonzero(got.reshape(-1) != want.reshape(-1))
+    assert bad.size == 0, [(hex(int(table.reshape(-1).view(np.uint32)[i])), hex(int(got.reshape(-1)[i])),
+                            hex(int(want.reshape(-1)[i]))) for i in bad[:8]]
+
+
 # ---------------------------------------------------------------- rmsnorm
 def test_rmsnorm_reference_kats():
     x = dev(np.array([[1, 2, 3, 4], [0.5, 1, 1.5, 2], [4, 3, 2, 1]], np.float32))
