@@ -9,11 +9,11 @@ slots, once with a paged cache of 64-position blocks.
 
 Bars, per sequence and step: logits within the north star's bf16 bar, 2e-2 of the
 step's largest |logit| (the top-16 entries and every 257th vocabulary entry the
-fixture holds); greedy tokens identical to the oracle's, except where the oracle's own
-top-2 gap is within twice the measured logit error (a near-tie the error explains): that
-sequence is then no longer compared (its context has left the fixture's), and the count
-of such divergences may not exceed the flips between the oracle's own fp64 and AVX2
-paths on this workload (self_flip)."""
+fixture holds); greedy tokens identical to the oracle's, except at a step the oracle
+itself cannot rank (its own top-2 gap within its own fp64-vs-AVX2 error at that step,
+self_err): that sequence is then no longer compared (its context has left the
+fixture's), and such divergences may number at most twice the oracle's own flips on
+this workload (self_flip; 2 of 68 steps, at 2 of the 8 steps it cannot rank)."""
 
 import ctypes as C
 import os
@@ -81,8 +81,9 @@ def test_long_context_batch4_session_matches_oracle(kv_block):
             report.append((r, step, token, want, round(err, 5), round(gap, 5)))
             assert err <= TOL, f"seq {r} step {step}: logits off by {err:.3e} of max |logit| ({report[-8:]})"
             if token != want:
-                assert gap <= 2 * err, (f"seq {r} step {step}: token {token} != oracle {want} with the oracle's "
-                                        f"top-2 gap {gap:.3e} above twice the logit error {err:.3e}")
+                own = float(g["self_err"][r, step])
+                assert gap <= own, (f"seq {r} step {step}: token {token} != oracle {want} where the oracle's top-2 "
+                                    f"gap {gap:.3e} exceeds its own error {own:.3e} at that step (GPU error {err:.3e})")
                 divergences += 1
                 live[r] = False
 
@@ -104,8 +105,8 @@ def test_long_context_batch4_session_matches_oracle(kv_block):
         print(f"[long context kv_block={kv_block}] {B} sequences x {steps} steps: max logit error {worst:.3e} "
               f"(oracle fp64 vs AVX2: {float(np.max(g['self_err'])):.3e}), near-tie divergences {divergences} "
               f"(oracle fp64 vs AVX2 flips: {self_flips})", flush=True)
-        assert divergences <= self_flips, (f"{divergences} divergences, oracle's own flips {self_flips}, max error "
-                                           f"{worst:.3e}: {report}")
+        assert divergences <= 2 * self_flips, (f"{divergences} divergences, oracle's own flips {self_flips}, max "
+                                               f"error {worst:.3e}: {report}")
     finally:
         L.am_session_destroy(s)
         L.am_model_destroy(m)
