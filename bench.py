@@ -26,6 +26,9 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 
+FORMAT_LABEL = {"int4": "INT4", "int8": "INT8", "bf16": "bf16"}
+GEMV_KIND = {"int4": "weight-only INT4 g128 dequant", "int8": "weight-only INT8 per-channel dequant",
+             "bf16": "bf16-weight"}
 CONFIGS = {
     "int4": dict(weight_format=3, name="llama3-8b-shape-int4-g128", decode=256),
     "int8": dict(weight_format=2, name="llama3-8b-shape-int8-perchannel", decode=128),
@@ -471,7 +474,8 @@ def main():
 
     pmc, prov = measured_traffic(f"gemv_{args.config}_decode_traffic")
     out = {
-        "metric": "batch-1 decode tokens/sec, Llama-3-8B-shape INT4; GEMV HBM GB/s vs peak",
+        "metric": (f"batch-1 decode tokens/sec, Llama-3-8B-shape {FORMAT_LABEL[args.config]}; "
+                   "GEMV HBM GB/s vs peak"),
         "value": round(tok_s, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -494,7 +498,7 @@ def main():
                      "traffic": pmc.get("hbm_bytes_per_token") if pmc else None,
                      "traffic_unit": "HBM bytes per token over the GEMV launches (rocprofv3 PMC, copy-scaled)",
                      "traffic_provenance": prov, "attention_pmc": attention_pmc(pmc),
-                     "kernel": "gemv_kernel (weight-only INT4 dequant GEMV, all 4 fused epilogues)",
+                     "kernel": f"gemv_kernel ({GEMV_KIND[args.config]} GEMV, all 4 fused epilogues)",
                      "bytes_per_token": weight_bytes, "gemv_ms_per_token": round(gemv_ms, 4),
                      "launches_per_token": gemv_launches},
         "breakdown": breakdown,
