@@ -60,6 +60,15 @@ typedef __attribute__((address_space(1))) void gvoid;
 typedef __attribute__((address_space(3))) void lvoid;
 
 constexpr int QBM = 128, QBK = 64;
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Split-K partials move as 16-byte buffer loads and stores carrying the sc1 cache
+// policy (bit 4 of the builtins' aux operand on gfx950): the device-coherent accesses
+// the relaxed agent-scope atomics compile to, four words at a time.  The descriptor's
+// last dword is the raw-buffer format word (32-bit data, no swizzle); a wave's region
+// is 16 tiles x 64 lanes x 16 bytes.
+constexpr int kCpolSc1 = 16;
+constexpr int kRawBufferFlags = 0x00020000;
+constexpr int kPartWaveBytes = 16 * 64 * 16;
 constexpr int XST = QBM * QBK * 2;  // 16 KB of X per stage
 
 // Bytes of one weight row per k step of 64, and the 16-byte chunks they make.
@@ -378,17 +387,14 @@ __global__ __launch_bounds__((Shape<WF, NWN>::kThreads), NWN == 2 ? 2 : 1) void 
   }
 
   if (p.splits > 1) {
-    // partial of this split: device-scope stores, acknowledged before the ticket
+    // partial of this split: device-scope (sc1) 16-byte buffer stores of the wave's
+    // 16 KB region, acknowledged before the ticket
     float* mine = p.part + ((static_cast<int64_t>(bid) * p.splits + split) * S::kWaves + wave) * (16 * 64 * 4);
+    const __amdgpu_buffer_rsrc_t rmine = __builtin_amdgcn_make_buffer_rsrc(mine, 0, kPartWaveBytes, kRawBufferFlags);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const f32x4_t v = acc[i / 4][i % 4];
-      uint64_t* d = reinterpret_cast<uint64_t*>(mine + (i * 64 + lane) * 4);
-      __hip_atomic_store(d, (static_cast<uint64_t>(__float_as_uint(v[1])) << 32) | __float_as_uint(v[0]),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(d + 1, (static_cast<uint64_t>(__float_as_uint(v[3])) << 32) | __float_as_uint(v[2]),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int i = 0; i < 16; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[i / 4][i % 4]), rmine, (i * 64 + lane) * 16, 0,
+                                             kCpolSc1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __shared__ unsigned last;
@@ -408,18 +414,13 @@ __global__ __launch_bounds__((Shape<WF, NWN>::kThreads), NWN == 2 ? 2 : 1) void 
         continue;
       }
       const float* src = p.part + ((static_cast<int64_t>(bid) * p.splits + sp) * S::kWaves + wave) * (16 * 64 * 4);
-      uint64_t v[32];
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), 0, kPartWaveBytes, kRawBufferFlags);
+      u32x4_t v[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint64_t* d = reinterpret_cast<const uint64_t*>(src + (i * 64 + lane) * 4);
-        v[2 * i] = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        v[2 * i + 1] = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int i = 0; i < 16; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (i * 64 + lane) * 16, 0, kCpolSc1);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        sum[i] += f32x4_t{__uint_as_float(static_cast<uint32_t>(v[2 * i])), __uint_as_float(static_cast<uint32_t>(v[2 * i] >> 32)),
-                          __uint_as_float(static_cast<uint32_t>(v[2 * i + 1])),
-                          __uint_as_float(static_cast<uint32_t>(v[2 * i + 1] >> 32))};
+      for (int i = 0; i < 16; ++i) sum[i] += __builtin_bit_cast(f32x4_t, v[i]);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i / 4][i % 4] = sum[i];
