@@ -19,9 +19,10 @@
 //     swaps / DPP; the 8 waves through LDS, one (head, dim) per thread.
 //   * The split count follows the live context (at least kMinPerSplit positions per
 //     split); with one split the block writes the output.  Otherwise every block
-//     writes a partial record (m, l, o) with device-scope stores, waits for them to
-//     complete and takes a ticket; the last block of the (row, kv head) reads the
-//     records back with device-scope loads, merges them and resets the ticket.  Only
+//     writes a partial record (per head m, l, two pad words, o[D]) with device-coherent
+//     8- and 16-byte buffer stores, waits for them to complete and takes a ticket; the
+//     last block of the (row, kv head) reads the records back with device-coherent
+//     buffer loads, merges them and resets the ticket.  Only
 //     the records and the ticket are device-coherent accesses: no cache-wide
 //     writeback or invalidate, and no second launch.
 
@@ -54,6 +55,14 @@ struct AttnArgs {
 };
 
 constexpr int kWaves = 8;
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Split records move as 8- and 16-byte buffer loads and stores carrying the sc1 cache
+// policy (bit 4 of the builtins' aux operand on gfx950): the device-coherent accesses
+// the relaxed agent-scope atomics compile to, several words at a time.  The
+// descriptor's last dword is the raw-buffer format word (32-bit data, no swizzle).
+constexpr int kCpolSc1 = 16;
+constexpr int kRawBufferFlags = 0x00020000;
 // Fewest cache positions one split block handles (contexts up to this length use a
 // single block per (row, kv head) and need no cross-block merge), and the most
 // splits: measured on MI355X, 128 positions per block and at most 16 blocks per
@@ -172,36 +181,54 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
                                             const float (*sm_o)[G][D], bool& last, int64_t qr, int64_t g, int split,
                                             int64_t nsplit) {
   constexpr int NT = NW * 64;
+  constexpr int RH = D + 4;  // floats per head in a partial record: m, l, 2 pad, o[D]
   using T = typename A::T;
-  // Merge the waves: thread t owns (head, dim) pairs t, t + NT, ...; with one split it
-  // writes the output, otherwise the block's partial record (device-scope stores).
-  float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * (D + 2);
-  for (int t = threadIdx.x; t < G * D; t += NT) {
-    const int hh = t / D, dd = t % D;
-    float mx = -INFINITY;
+  // Merge the waves of (head hh, dims d0 .. d0 + NE): the running maximum, the
+  // rescaled denominator and output sums, in wave order.
+  auto wave_merge = [&]<int NE>(int hh, int d0, float& mx, float& den, float (&acc)[NE]) {
+    mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm_m[w][hh]);
-    float den = 0.0f, acc = 0.0f;
+    den = 0.0f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
     if (mx != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const float c = exp2f(sm_m[w][hh] - mx);
         den = fmaf(sm_l[w][hh], c, den);
-        acc = fmaf(sm_o[w][hh][dd], c, acc);
+#pragma unroll
+        for (int e = 0; e < NE; ++e) acc[e] = fmaf(sm_o[w][hh][d0 + e], c, acc[e]);
       }
     }
-    if (nsplit == 1) {
+  };
+  if (nsplit == 1) {
+    // one split: thread t owns (head, dim) pairs t, t + NT, ... and writes the output
+    for (int t = threadIdx.x; t < G * D; t += NT) {
+      const int hh = t / D, dd = t % D;
+      float mx, den, acc[1];
+      wave_merge(hh, dd, mx, den, acc);
       T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
-      A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
-    } else {
-      if (dd == 0) {
-        __hip_atomic_store(&rec[hh * (D + 2)], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&rec[hh * (D + 2) + 1], den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __hip_atomic_store(&rec[hh * (D + 2) + 2 + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      A::store(out, dd, den > 0.0f ? acc[0] / den : 0.0f);
     }
+    return;
   }
-  if (nsplit == 1) return;
+  // The block's partial record, published with device-coherent (sc1) buffer stores:
+  // thread t owns dims 4t .. 4t + 3 of one head (one 16-byte store; the head's first
+  // thread also stores m and l as one 8-byte store).
+  float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * RH;
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(rec, 0, G * RH * 4, kRawBufferFlags);
+  for (int t = threadIdx.x; t < G * D / 4; t += NT) {
+    const int hh = 4 * t / D, d0 = 4 * t % D;
+    float mx, den, acc[4];
+    wave_merge(hh, d0, mx, den, acc);
+    if (d0 == 0)
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(mx), __float_as_uint(den)}, rrec, hh * RH * 4, 0,
+                                            kCpolSc1);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4_t{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])}, rrec,
+        (hh * RH + 4 + d0) * 4, 0, kCpolSc1);
+  }
   // every thread's record stores have completed before the block takes its ticket
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -212,46 +239,50 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
   }
   __syncthreads();
   if (!last) return;
-  // Merge the splits: thread t owns (head, dim) pairs t, t + NT, ...; the records are
-  // read with device-scope loads, kMergeBatch splits at a time with all of a batch's
-  // loads in flight together (slots past the last split reread it and are skipped).
-  // Each batch rescales the running sums to the batch's new maximum.
+  // Merge the splits: thread t owns dims 4t .. 4t + 3 of one head; the records are read
+  // with device-coherent (sc1) buffer loads, kMergeBatch splits at a time with all of a
+  // batch's loads in flight together (slots past the last split reread it and are
+  // skipped).  Each batch rescales the running sums to the batch's new maximum.
   constexpr int kMergeBatch = 8;
-  const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * (D + 2);
-  const int64_t rs = G * (D + 2);  // record stride between splits
-  for (int t = threadIdx.x; t < G * D; t += NT) {
-    const int hh = t / D, dd = t % D;
-    const float* base = base0 + hh * (D + 2);
-    float mx = -INFINITY, den = 0.0f, acc = 0.0f;
+  const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * RH;
+  const __amdgpu_buffer_rsrc_t rall = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(base0), 0, static_cast<int>(nsplit * G * RH * 4), kRawBufferFlags);
+  for (int t = threadIdx.x; t < G * D / 4; t += NT) {
+    const int hh = 4 * t / D, d0 = 4 * t % D;
+    float mx = -INFINITY, den = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int64_t s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
-      float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+      u32x2_t ml[kMergeBatch];
+      u32x4_t ov[kMergeBatch];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
-        const float* r = base + (s0 + u < nsplit ? s0 + u : nsplit - 1) * rs;
-        mv[u] = __hip_atomic_load(&r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lv[u] = __hip_atomic_load(&r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ov[u] = __hip_atomic_load(&r[2 + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int r = static_cast<int>(s0 + u < nsplit ? s0 + u : nsplit - 1);
+        const int off = (r * G * RH + hh * RH) * 4;
+        ml[u] = __builtin_amdgcn_raw_buffer_load_b64(rall, off, 0, kCpolSc1);
+        ov[u] = __builtin_amdgcn_raw_buffer_load_b128(rall, off + (4 + d0) * 4, 0, kCpolSc1);
       }
       float bm = mx;
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u)
-        if (s0 + u < nsplit) bm = fmaxf(bm, mv[u]);
+        if (s0 + u < nsplit) bm = fmaxf(bm, __uint_as_float(ml[u][0]));
       if (bm == -INFINITY) continue;
       const float c0 = exp2f(mx - bm);  // 0 while nothing has been summed
       den *= c0;
-      acc *= c0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] *= c0;
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         if (s0 + u < nsplit) {
-          const float c = exp2f(mv[u] - bm);
-          den = fmaf(lv[u], c, den);
-          acc = fmaf(ov[u], c, acc);
+          const float c = exp2f(__uint_as_float(ml[u][0]) - bm);
+          den = fmaf(__uint_as_float(ml[u][1]), c, den);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] = fmaf(__uint_as_float(ov[u][e]), c, acc[e]);
         }
       }
       mx = bm;
     }
     T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
-    A::store(out, dd, den > 0.0f ? acc / den : 0.0f);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) A::store(out, d0 + e, den > 0.0f ? acc[e] / den : 0.0f);
   }
   if (threadIdx.x == 0) __hip_atomic_store(&p.tickets[qr * p.hkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1044,7 +1075,7 @@ extern "C" int64_t am_gfx950_attention_workspace_bytes(int64_t batch, int64_t se
   const int splits = ChooseSplits(seq, capacity, num_splits);
   if (splits == 1) return 0;
   const int64_t tickets = 256 * CeilDiv(batch * seq * hkv * 4, 256);
-  return tickets + batch * seq * hq * splits * (head_dim + 2) * 4;
+  return tickets + batch * seq * hq * splits * (head_dim + 4) * 4;
 }
 
 // ---- zero-allocation variant -----------------------------------------------------
