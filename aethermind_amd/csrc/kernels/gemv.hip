@@ -688,15 +688,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
       int64_t bi = -1;
       for (int w = 0; w < NW; ++w)
         if (bi_s[w] >= 0 && argmax_better(bv_s[w], bi_s[w], bv, bi)) { bv = bv_s[w]; bi = bi_s[w]; }
-      p.pv[blockIdx.x] = bv;
-      p.pi[blockIdx.x] = bi;
-      __threadfence();
-      const unsigned t = atomicAdd(p.ticket, 1u);
+      // device-coherent (sc1) stores, acknowledged before the relaxed ticket: the
+      // last block's device-coherent loads then see every block's partial
+      __hip_atomic_store(&p.pv[blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.pi[blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      const unsigned t = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = (t == gridDim.x - 1);
     }
     __syncthreads();
     if (last) {
-      __threadfence();
       float bv = 0.0f;
       int64_t bi = -1;
       for (int64_t b = threadIdx.x; b < gridDim.x; b += NT) {

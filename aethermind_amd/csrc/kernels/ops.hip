@@ -238,15 +238,16 @@ __global__ __launch_bounds__(256) void argmax_kernel(const typename A::T* x, int
         bv = sv[w];
         bi = si[w];
       }
-    pv[r * ArgmaxWs::kMaxBlocks + blockIdx.x] = bv;
-    pi[r * ArgmaxWs::kMaxBlocks + blockIdx.x] = bi;
-    __threadfence();
-    const unsigned t = atomicAdd(&tickets[r], 1u);
+    // device-coherent (sc1) stores, acknowledged before the relaxed ticket: the last
+    // block's device-coherent loads then see every block's partial
+    __hip_atomic_store(&pv[r * ArgmaxWs::kMaxBlocks + blockIdx.x], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&pi[r * ArgmaxWs::kMaxBlocks + blockIdx.x], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    const unsigned t = __hip_atomic_fetch_add(&tickets[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = (t == static_cast<unsigned>(nb - 1));
   }
   __syncthreads();
   if (last && threadIdx.x == 0) {
-    __threadfence();
     float fv = 0.0f;
     int64_t fi = -1;
     for (int b = 0; b < nb; ++b) {
