@@ -490,11 +490,11 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs p) {
 //     records and ticket as the general kernel.
 constexpr int kDecWaves = 4;
 // Split policy of the decode kernel, measured on MI355X with a cold cache (the layer's
-// K/V evicted by the weight stream, as in decode): at least 128 positions per split
-// block and at most 8 split blocks per (row, kv head) minimise the kernel time from
-// 128 to 4096 positions.  A split block costs a cross-block merge, so short contexts
-// keep a single block.
-constexpr int32_t kDecMinPerSplit = 128;
+// K/V evicted by the weight stream, as in decode) and in the replayed decode graph: at
+// least 64 positions per split block and at most 8 split blocks per (row, kv head)
+// minimise the kernel time from 64 to 4096 positions.  A split block costs a
+// cross-block merge, so short contexts keep a single block.
+constexpr int32_t kDecMinPerSplit = 64;
 constexpr int kDecMaxSplits = 8;
 
 // NW = 8: two waves per SIMD (236 VGPRs, no spills, against 264 for the 4-wave block,
