@@ -20,11 +20,10 @@
 //   * The split count follows the live context (at least kMinPerSplit positions per
 //     split); with one split the block writes the output.  Otherwise every block
 //     writes a partial record (per head m, l, two pad words, o[D]) with device-coherent
-//     8- and 16-byte buffer stores, waits for them to complete and takes a ticket; the
-//     last block of the (row, kv head) reads the records back with device-coherent
-//     buffer loads, merges them and resets the ticket.  Only
-//     the records and the ticket are device-coherent accesses: no cache-wide
-//     writeback or invalidate, and no second launch.
+//     stores, waits for them to complete and takes a ticket; the last block of the
+//     (row, kv head) reads the records back with device-coherent loads, merges them
+//     and resets the ticket.  Only the records and the ticket are device-coherent
+//     accesses: no cache-wide writeback or invalidate, and no second launch.
 
 #include <hip/hip_ext.h>
 
@@ -213,21 +212,33 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
     }
     return;
   }
-  // The block's partial record, published with device-coherent (sc1) buffer stores:
-  // thread t owns dims 4t .. 4t + 3 of one head (one 16-byte store; the head's first
-  // thread also stores m and l as one 8-byte store).
+  // The block's partial record, published with device-coherent (sc1) stores: in 4-wave
+  // blocks thread t owns 4 consecutive dims of one head (one 16-byte buffer store, and
+  // the head's first thread stores m and l as one 8-byte store); 8-wave blocks have a
+  // thread for every (head, dim) pair and keep 4-byte relaxed agent-scope stores (as
+  // fast there in same-box A/B runs at batch 4; the wider accesses were about 1% slower).
+  constexpr int DPT = NW >= 8 ? 1 : 4;
+  static_assert(D % DPT == 0, "dims per thread must divide the head dimension");
   float* rec = p.part + (((qr * p.hkv + g) * p.splits + split) * G) * RH;
   const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(rec, 0, G * RH * 4, kRawBufferFlags);
-  for (int t = threadIdx.x; t < G * D / 4; t += NT) {
-    const int hh = 4 * t / D, d0 = 4 * t % D;
-    float mx, den, acc[4];
+  for (int t = threadIdx.x; t < G * D / DPT; t += NT) {
+    const int hh = DPT * t / D, d0 = DPT * t % D;
+    float mx, den, acc[DPT];
     wave_merge(hh, d0, mx, den, acc);
-    if (d0 == 0)
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(mx), __float_as_uint(den)}, rrec, hh * RH * 4, 0,
-                                            kCpolSc1);
-    __builtin_amdgcn_raw_buffer_store_b128(
-        u32x4_t{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])}, rrec,
-        (hh * RH + 4 + d0) * 4, 0, kCpolSc1);
+    if constexpr (DPT == 4) {
+      if (d0 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{__float_as_uint(mx), __float_as_uint(den)}, rrec, hh * RH * 4, 0,
+                                              kCpolSc1);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4_t{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])},
+          rrec, (hh * RH + 4 + d0) * 4, 0, kCpolSc1);
+    } else {
+      if (d0 == 0) {
+        __hip_atomic_store(&rec[hh * RH], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&rec[hh * RH + 1], den, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __hip_atomic_store(&rec[hh * RH + 4 + d0], acc[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   // every thread's record stores have completed before the block takes its ticket
   __builtin_amdgcn_s_waitcnt(0);
@@ -239,26 +250,37 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
   }
   __syncthreads();
   if (!last) return;
-  // Merge the splits: thread t owns dims 4t .. 4t + 3 of one head; the records are read
-  // with device-coherent (sc1) buffer loads, kMergeBatch splits at a time with all of a
-  // batch's loads in flight together (slots past the last split reread it and are
-  // skipped).  Each batch rescales the running sums to the batch's new maximum.
+  // Merge the splits: thread t owns the same dims; the records are read with
+  // device-coherent (sc1) loads of the same widths, kMergeBatch splits at a time with
+  // all of a batch's loads in flight together (slots past the last split reread it and
+  // are skipped).  Each batch rescales the running sums to the batch's new maximum.
   constexpr int kMergeBatch = 8;
   const float* base0 = p.part + ((qr * p.hkv + g) * p.splits) * G * RH;
   const __amdgpu_buffer_rsrc_t rall = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(base0), 0, static_cast<int>(nsplit * G * RH * 4), kRawBufferFlags);
-  for (int t = threadIdx.x; t < G * D / 4; t += NT) {
-    const int hh = 4 * t / D, d0 = 4 * t % D;
-    float mx = -INFINITY, den = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = threadIdx.x; t < G * D / DPT; t += NT) {
+    const int hh = DPT * t / D, d0 = DPT * t % D;
+    float mx = -INFINITY, den = 0.0f, acc[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
     for (int64_t s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
       u32x2_t ml[kMergeBatch];
-      u32x4_t ov[kMergeBatch];
+      uint32_t ov[kMergeBatch][DPT];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         const int r = static_cast<int>(s0 + u < nsplit ? s0 + u : nsplit - 1);
         const int off = (r * G * RH + hh * RH) * 4;
-        ml[u] = __builtin_amdgcn_raw_buffer_load_b64(rall, off, 0, kCpolSc1);
-        ov[u] = __builtin_amdgcn_raw_buffer_load_b128(rall, off + (4 + d0) * 4, 0, kCpolSc1);
+        if constexpr (DPT == 4) {
+          ml[u] = __builtin_amdgcn_raw_buffer_load_b64(rall, off, 0, kCpolSc1);
+          const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rall, off + (4 + d0) * 4, 0, kCpolSc1);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ov[u][e] = v[e];
+        } else {
+          const float* rr = base0 + off / 4;
+          ml[u][0] = __float_as_uint(__hip_atomic_load(&rr[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          ml[u][1] = __float_as_uint(__hip_atomic_load(&rr[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          ov[u][0] = __float_as_uint(__hip_atomic_load(&rr[4 + d0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
       }
       float bm = mx;
 #pragma unroll
@@ -268,21 +290,21 @@ __device__ __forceinline__ void finish_rows(const AttnArgs& p, const float (*sm_
       const float c0 = exp2f(mx - bm);  // 0 while nothing has been summed
       den *= c0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] *= c0;
+      for (int e = 0; e < DPT; ++e) acc[e] *= c0;
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         if (s0 + u < nsplit) {
           const float c = exp2f(__uint_as_float(ml[u][0]) - bm);
           den = fmaf(__uint_as_float(ml[u][1]), c, den);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[e] = fmaf(__uint_as_float(ov[u][e]), c, acc[e]);
+          for (int e = 0; e < DPT; ++e) acc[e] = fmaf(__uint_as_float(ov[u][e]), c, acc[e]);
         }
       }
       mx = bm;
     }
     T* out = static_cast<T*>(p.out) + (qr * p.hq + g * G + hh) * D;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) A::store(out, d0 + e, den > 0.0f ? acc[e] / den : 0.0f);
+    for (int e = 0; e < DPT; ++e) A::store(out, d0 + e, den > 0.0f ? acc[e] / den : 0.0f);
   }
   if (threadIdx.x == 0) __hip_atomic_store(&p.tickets[qr * p.hkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
