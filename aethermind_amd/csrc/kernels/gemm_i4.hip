@@ -629,16 +629,24 @@ int64_t TilesOf(const I4Args& p) {
 constexpr int64_t kTicketRegion = 4096;               // bytes at the start of the workspace
 constexpr int64_t kMaxSplitTiles = kTicketRegion / 4;  // tiles of a launch that may split
 
-// Split-K count: the largest power of two <= 4 that still gives every CU at most one
-// block with >= 8 groups per split; long rows (>= 24 groups per split) may take two
-// blocks per CU.  The loop's per-CU rate is nearly the same with one block per CU as
-// with two, so splits pay when tiles alone leave CUs idle, and the partial merge
-// (~9 us) must be amortised.
-int SplitsFor(int64_t tiles, int64_t groups, int64_t cus) {
+// Blocks of a shape that one CU holds at once, by LDS (160 KB per CU): two for the
+// 128-wide INT4 and INT8 tiles, one for the bf16 tile and for every 256-wide tile.
+constexpr int64_t kLdsPerCu = 160 * 1024;
+template <int WF, int NWN>
+constexpr int BlocksPerCu() {
+  return kLdsPerCu / Shape<WF, NWN>::kLds > 1 ? static_cast<int>(kLdsPerCu / Shape<WF, NWN>::kLds) : 1;
+}
+
+// Split-K count: the largest power of two <= 4 that keeps every split at >= 8 groups
+// and the launch within one round of resident blocks (bpc per CU).  Measured on the
+// 8B 512-row shapes with the 16-byte partial stores: q|k|v 2 splits (INT4 71 -> 58 us,
+// INT8 103 -> 64 us; bf16, one block per CU, unsplit), o 4 (INT4 44 -> 39 us, INT8
+// 60 -> 43 us; bf16 2), down 4 (bf16 2: 116 -> 109 us), gate/up unsplit (448 tiles
+// already fill the CUs; 2 splits 206 -> 232 us).
+int SplitsFor(int64_t tiles, int64_t groups, int64_t cus, int bpc) {
   if (tiles > kMaxSplitTiles) return 1;
   int s = 1;
-  while (s < 4 && tiles * s * 2 <= cus && groups / (s * 2) >= 8) s *= 2;
-  if (s < 4 && tiles * s * 2 <= 2 * cus && groups / (s * 2) >= 24) s *= 2;
+  while (s < 4 && tiles * s * 2 <= bpc * cus && groups / (s * 2) >= 8) s *= 2;
   return s;
 }
 
@@ -660,7 +668,7 @@ am_status_code LaunchMfma(I4Args p, void* ws, int64_t ws_bytes, hipStream_t s) {
                           hipFuncAttributeMaxDynamicSharedMemorySize, S::kLds) == hipSuccess;
   if (!lds_ok) return SetLastError(AM_STATUS_INTERNAL, "gemm_i4: could not set the dynamic LDS size");
   const int64_t tiles = TilesOf<EPI, NWN>(p);
-  int splits = ws != nullptr ? SplitsFor(tiles, p.K / p.group, DeviceCUs()) : 1;
+  int splits = ws != nullptr ? SplitsFor(tiles, p.K / p.group, DeviceCUs(), BlocksPerCu<WF, NWN>()) : 1;
   if (splits > 1 && TicketBytes(tiles) + PartialBytes<NWN>(tiles, splits) > ws_bytes) splits = 1;
   p.splits = splits;
   if (splits > 1) {
@@ -727,14 +735,19 @@ bool GemmI4Eligible(const am_gfx950_weight& w, int64_t m, const void* x) {
 }
 
 // Workspace that lets the launch of this shape split K (0: it never splits).  The same
-// bound serves every epilogue (the SiLU-Mul tiles are never more numerous).
+// bound serves every epilogue (the SiLU-Mul tiles are never more numerous) and every
+// weight format (the most resident blocks per CU any format has for the tile width).
 int64_t GemmI4WorkspaceBytes(int64_t m, int64_t n, int64_t k, int64_t group) {
   if (m <= 0 || n <= 0 || k <= 0 || group <= 0 || k % group != 0) return 0;
   const int64_t cus = DeviceCUs();
   int64_t best = 0;
   for (int nwn : {2, 4}) {
     const int64_t tiles = CeilDiv(m, QBM) * CeilDiv(n, 64 * nwn);
-    const int sp = SplitsFor(tiles, k / group, cus);
+    const int bpc = nwn == 2 ? std::max({BlocksPerCu<AM_WF_INT4, 2>(), BlocksPerCu<AM_WF_INT8, 2>(),
+                                         BlocksPerCu<AM_WF_BF16, 2>()})
+                             : std::max({BlocksPerCu<AM_WF_INT4, 4>(), BlocksPerCu<AM_WF_INT8, 4>(),
+                                         BlocksPerCu<AM_WF_BF16, 4>()});
+    const int sp = SplitsFor(tiles, k / group, cus, bpc);
     if (sp > 1)
       best = std::max(best, TicketBytes(tiles) + (nwn == 2 ? PartialBytes<2>(tiles, sp) : PartialBytes<4>(tiles, sp)));
   }

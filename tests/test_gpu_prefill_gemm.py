@@ -148,16 +148,19 @@ def tickets_zero(ws, tiles):
     return not host(ws)[:4 * tiles].any()
 
 
-# (m, n, k, group, expected splits): the 8B o and down shapes, ragged tiles, a split
-# count capped by the group count, per-element epilogue chunks (n % 8 != 0)
-SPLIT_SHAPES = [(512, 4096, 4096, 128, 2), (512, 4096, 14336, 128, 4), (100, 520, 4096, 128, 4),
-                (33, 130, 2048, 128, 2), (64, 1000, 8192, 256, 4)]
+# (m, n, k, group, expected splits for INT4 and INT8, for bf16): the 8B o and down
+# shapes (the 128-wide INT4 and INT8 tiles fit two blocks per CU, the bf16 tile one, so
+# their launches may hold twice the blocks), ragged tiles, a split count capped by the
+# group count, per-element epilogue chunks (n % 8 != 0)
+SPLIT_SHAPES = [(512, 4096, 4096, 128, 4, 2), (512, 4096, 14336, 128, 4, 2), (100, 520, 4096, 128, 4, 4),
+                (33, 130, 2048, 128, 2, 2), (64, 1000, 8192, 256, 4, 4)]
 
 
 @pytest.mark.parametrize("shape", SPLIT_SHAPES)
 @pytest.mark.parametrize("fmt", FMTS)
 def test_split_k_residual(shape, fmt):
-    m, n, k, group, want = shape
+    m, n, k, group, want_q, want_bf16 = shape
+    want = want_bf16 if fmt == N.AM_WF_BF16 else want_q
     w, dw, keep = weight(n, k, seed=241 + n, group=group, fmt=fmt)
     x = act_rows(242, m, k)
     res = act_rows(243, m, n)
