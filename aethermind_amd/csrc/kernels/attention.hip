@@ -752,13 +752,18 @@ __global__ __launch_bounds__(NW * 64) void attention_decode_kernel(AttnArgs p) {
 //     operands are read once per wave and shared by the wave's column groups.
 //   * The causal mask is per column (key <= the column's position, key < the chunk
 //     end), the online softmax is base 2 per column (scores pre-scaled by
-//     log2(e)/sqrt(d)), P is split into bf16 hi + lo for the P V product.  Waves own
-//     distinct queries, so there is no merge: each wave normalises its columns and
+//     log2(e)/sqrt(d)), P is split into bf16 hi + lo for the P V product.  Within a
+//     key group waves own distinct queries: each wave normalises its columns and
 //     writes them.
 // Blocks are numbered kv head fastest: block b runs on XCD b % 8, so with 8 kv heads
 // every block of one head shares one XCD's L2 (the head's K/V is read from HBM once),
 // and the query blocks of a head are taken last-first (the longest causal ranges start
 // first).
+// KS = 2 runs two groups of NW waves over the same queries: group k takes the key
+// tiles t with t % 2 == k through its own LDS buffers, and at the end the second
+// group's softmax states are merged into the first's through LDS.  A block then keeps
+// two waves per SIMD busy on half the tiles each, for launches that give a CU only one
+// 4-wave block.
 constexpr int kPreTile = 32;
 
 // 16-byte slot of K row `key` holding dims 8s .. 8s+7 (s ^ this): the 16 rows of one
@@ -773,9 +778,10 @@ __device__ __forceinline__ int kswz(int key) {
 // 16-byte slot of V^T row d holding keys 8s .. 8s+7 (s ^ this)
 __device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
 
-template <int D, int G, int CG, int NW>
-__global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) {
-  constexpr int NT = NW * 64;
+template <int D, int G, int CG, int NW, int KS>
+__global__ __launch_bounds__(NW * 64 * KS) void attention_prefill_kernel(AttnArgs p) {
+  static_assert(KS == 1 || KS == 2, "one or two key groups");
+  constexpr int NT = NW * 64;                // threads of one key group
   constexpr int QT = 16 / G;               // query positions per column group
   constexpr int QB = NW * CG * QT;         // query positions per block
   constexpr int KK = D / 32;               // MFMA k steps of one score tile
@@ -786,10 +792,14 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
   static_assert(PCH >= 1 && TP * PR % NT == 0, "tile pieces must divide over the block");
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-  __shared__ __align__(16) uint16_t sk[2][TP * D];   // K[key][d], 16-byte slots swizzled
-  __shared__ __align__(16) uint16_t sv[2][D * TP];   // V^T[d][key], 16-byte slots swizzled
+  // per key group, two buffers each of K[key][d] and V^T[d][key], 16-byte slots swizzled
+  __shared__ __align__(16) uint16_t skv[2 * KS * 2 * TP * D];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  // key group kg of the thread, and its index within the group
+  const int kg = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / NT);
+  auto sk = [&](int buf) { return skv + (kg * 2 + buf) * (TP * D); };
+  auto sv = [&](int buf) { return skv + ((KS + kg) * 2 + buf) * (TP * D); };
+  const int tid = static_cast<int>(threadIdx.x) % NT, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, h = lane >> 4;
   // block -> (row, q block, kv head): kv head fastest, q blocks last-first
@@ -832,7 +842,7 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
   // of two 8-dim blocks, so the transposed 2-byte stores of one instruction fall into
   // two V^T rows rather than sixteen).  A tile's 32 rows are contiguous from its first
   // row (one offset lookup per tile).
-  typedef uint4 Pieces[2][PCH];
+  typedef u32x4_t Pieces[2][PCH];  // a vector type: copies stay in registers
   Pieces ra, rb;
   auto load_tile = [&](Pieces& r, int64_t t) {
     const int64_t off = p.kv.Row(b, g, t * TP);
@@ -840,23 +850,23 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
       const uint32_t row = min(static_cast<uint32_t>(tid / PR + c * (NT / PR)), lim);
-      r[0][c] = *reinterpret_cast<const uint4*>(kc0 + off + (row * D + 8 * (tid % PR)));
+      r[0][c] = *reinterpret_cast<const u32x4_t*>(kc0 + off + (row * D + 8 * (tid % PR)));
       const int q = c * NT + tid;
       const uint32_t vrow = min(static_cast<uint32_t>(q % TP), lim);
-      r[1][c] = *reinterpret_cast<const uint4*>(vc0 + off + (vrow * D + 8 * (q / TP)));
+      r[1][c] = *reinterpret_cast<const u32x4_t*>(vc0 + off + (vrow * D + 8 * (q / TP)));
     }
   };
   auto store_tile = [&](const Pieces& r, int buf) {
 #pragma unroll
     for (int c = 0; c < PCH; ++c) {
       const int key = tid / PR + c * (NT / PR), sl = tid % PR;
-      *reinterpret_cast<uint4*>(&sk[buf][key * D + 8 * (sl ^ kswz<D>(key))]) = r[0][c];
+      *reinterpret_cast<u32x4_t*>(sk(buf) + key * D + 8 * (sl ^ kswz<D>(key))) = r[0][c];
       const int q = c * NT + tid, vkey = q % TP, vsl = q / TP;
       const uint32_t w[4] = {r[1][c].x, r[1][c].y, r[1][c].z, r[1][c].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int d = 8 * vsl + e;
-        sv[buf][d * TP + 8 * ((vkey >> 3) ^ vswz(d)) + (vkey & 7)] =
+        sv(buf)[d * TP + 8 * ((vkey >> 3) ^ vswz(d)) + (vkey & 7)] =
             static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu));
       }
     }
@@ -877,8 +887,8 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
   }
 
   auto compute = [&](int buf, int64_t t) {
-    const uint16_t* kt = sk[buf];
-    const uint16_t* vt = sv[buf];
+    const uint16_t* kt = sk(buf);
+    const uint16_t* vt = sv(buf);
     f32x4_t acc[CG][2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -954,24 +964,70 @@ __global__ __launch_bounds__(NW * 64) void attention_prefill_kernel(AttnArgs p) 
     }
   };
 
-  // tile t: in LDS buffer t & 1; its registers were loaded two iterations earlier
-  load_tile(ra, 0);
-  if (ntiles > 1) load_tile(rb, 1);
+  // The group's u-th tile is tile u KS + kg, in LDS buffer u & 1; its registers were
+  // loaded two iterations earlier.  Every group runs the loop of the group with the
+  // most tiles (the first), so all threads meet at the same barriers; loads and stores
+  // past a group's last tile repeat the block's last tile (never computed).
+  const int64_t nu = (ntiles + KS - 1) / KS;                    // tiles of group 0
+  const int64_t nmine = ntiles > kg ? (ntiles - kg + KS - 1) / KS : 0;  // of this group
+  auto gt = [&](int64_t u) { return min(u * KS + kg, ntiles - 1); };
+  load_tile(ra, gt(0));
+  load_tile(rb, gt(1));
   store_tile(ra, 0);
   __syncthreads();
-  int64_t t = 0;
-  for (; t + 1 < ntiles; t += 2) {
-    // even tile t in buffer 0; rb holds tile t + 1
-    if (t + 2 < ntiles) load_tile(ra, t + 2);
-    compute(0, t);
+  int64_t u = 0;
+  for (; u + 1 < nu; u += 2) {
+    // even tile u in buffer 0; rb holds tile u + 1
+    load_tile(ra, gt(u + 2));
+    if (u < nmine) compute(0, gt(u));
     store_tile(rb, 1);
     __syncthreads();
-    if (t + 3 < ntiles) load_tile(rb, t + 3);
-    compute(1, t + 1);
-    if (t + 2 < ntiles) store_tile(ra, 0);
+    load_tile(rb, gt(u + 3));
+    if (u + 1 < nmine) compute(1, gt(u + 1));
+    store_tile(ra, 0);
     __syncthreads();
   }
-  if (t < ntiles) compute(0, t);
+  if (u < nmine) compute(0, gt(u));
+
+  if constexpr (KS == 2) {
+    // the second group's states into LDS (lane-contiguous words per wave), merged into
+    // the first group's on the same lanes
+    constexpr int SW = 2 * CG + CG * DT * 4;  // words per lane
+    static_assert(NW * SW * 64 * 4 <= static_cast<int>(sizeof(skv)), "merge records fit the tile buffers");
+    float* rec = reinterpret_cast<float*>(skv) + wave * SW * 64 + lane;
+    __syncthreads();  // every group is done with its tiles
+    if (kg == 1) {
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        rec[(2 * c) * 64] = m_run[c];
+        rec[(2 * c + 1) * 64] = l_run[c];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rec[(2 * CG + (c * DT + dt) * 4 + r) * 64] = o[c][dt][r];
+      }
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      // column j's scale factors (every lane of the column holds its maximum)
+      const float m2 = rec[(2 * c) * 64], l2 = rec[(2 * c + 1) * 64];
+      const float mn = fmaxf(m_run[c], m2);
+      const float f1 = m_run[c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[c] - mn);
+      const float f2 = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
+      l_run[c] = l_run[c] * f1 + l2 * f2;
+      m_run[c] = mn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        // o[..][r] is column 4h + r: that column's factors
+        const float c1 = __shfl(f1, 16 * h + 4 * h + r), c2 = __shfl(f2, 16 * h + 4 * h + r);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          o[c][dt][r] = o[c][dt][r] * c1 + rec[(2 * CG + (c * DT + dt) * 4 + r) * 64] * c2;
+      }
+    }
+  }
 
   // column j's sum over the four lane rows, then normalise and write
 #pragma unroll
@@ -1007,15 +1063,20 @@ void LaunchTimed(K kernel, dim3 grid, dim3 block, hipStream_t s, const AttnArgs&
   }
 }
 
-template <int D, int G, int CG, int NW>
+template <int D, int G, int CG, int NW, int KS>
 void LaunchPrefillShape(int64_t blocks, const AttnArgs& a, hipStream_t s) {
   constexpr int QB = NW * CG * (16 / G);
-  RecordLaunch(blocks, NW * 64, 0, "attention_prefill<d=%d,g=%d,qb=%d>", D, G, QB);
-  LaunchTimed(attention_prefill_kernel<D, G, CG, NW>, dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), s, a);
+  if constexpr (KS == 1)
+    RecordLaunch(blocks, NW * 64, 0, "attention_prefill<d=%d,g=%d,qb=%d>", D, G, QB);
+  else
+    RecordLaunch(blocks, NW * 64 * KS, 0, "attention_prefill<d=%d,g=%d,qb=%d,ks=%d>", D, G, QB, KS);
+  LaunchTimed(attention_prefill_kernel<D, G, CG, NW, KS>, dim3(static_cast<unsigned>(blocks)), dim3(NW * 64 * KS), s,
+              a);
 }
 
 // Query positions per block: the largest of 16/G x {4, 8, 16} that still gives every CU
-// a block (fewer re-reads of K/V per query), else the smallest.
+// a block (fewer re-reads of K/V per query), else the smallest, as two key groups of
+// four waves.
 template <int D, int G>
 void LaunchPrefillG(const AttnArgs& a, int64_t batch, hipStream_t s) {
   const int64_t per = a.hkv * batch, cus = DeviceCUs();
@@ -1023,11 +1084,11 @@ void LaunchPrefillG(const AttnArgs& a, int64_t batch, hipStream_t s) {
   constexpr int QT = 16 / G;
   // (a 512-thread block needs a whole 16-byte piece per thread per tile: D = 128)
   if (D == 128 && blocks(16 * QT) >= cus)
-    LaunchPrefillShape<D, G, 2, D == 128 ? 8 : 4>(blocks(16 * QT), a, s);
+    LaunchPrefillShape<D, G, 2, D == 128 ? 8 : 4, 1>(blocks(16 * QT), a, s);
   else if (blocks(8 * QT) >= cus)
-    LaunchPrefillShape<D, G, 2, 4>(blocks(8 * QT), a, s);
+    LaunchPrefillShape<D, G, 2, 4, 1>(blocks(8 * QT), a, s);
   else
-    LaunchPrefillShape<D, G, 1, 4>(blocks(4 * QT), a, s);
+    LaunchPrefillShape<D, G, 1, 4, 2>(blocks(4 * QT), a, s);
 }
 
 template <int D>
