@@ -277,7 +277,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
   const int64_t xpieces = K / EPP;
   uint4 xv[XP];
   uint4 nv[NORM ? XP : 1];
-  uint4 rv[RP];
+  u32x4_t rv[RP];  // a vector type: the copy into LDS stays in registers
   const int64_t rpieces = p.n / EPP;
   {
     // Straight-line loads on every path (the arrays stay in registers); without the
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
       if constexpr (NORM) nv[v] = ns[pi];
     }
     if constexpr (EPI == kEpiResidual) {
-      const uint4* rs = reinterpret_cast<const uint4*>(p.vec ? p.residual : static_cast<const void*>(p.w));
+      const u32x4_t* rs = reinterpret_cast<const u32x4_t*>(p.vec ? p.residual : static_cast<const void*>(p.w));
       const int64_t rlast = p.vec ? rpieces - 1 : 0;
 #pragma unroll
       for (int v = 0; v < RP; ++v) {
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs p) {
       for (int v = 0; v < RP; ++v) {
         int64_t pi = tid + NT * v;
         if (pi > rlast) pi = rlast;
-        reinterpret_cast<uint4*>(res_lds)[pi] = rv[v];
+        reinterpret_cast<u32x4_t*>(res_lds)[pi] = rv[v];
       }
       if (vec) {
         const uint4* res = static_cast<const uint4*>(p.residual);
