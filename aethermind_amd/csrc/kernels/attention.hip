@@ -793,13 +793,14 @@ __global__ __launch_bounds__(NW * 64 * KS) void attention_prefill_kernel(AttnArg
   typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
   typedef __attribute__((ext_vector_type(4))) float f32x4_t;
   // per key group, two buffers each of K[key][d] and V^T[d][key], 16-byte slots swizzled
-  __shared__ __align__(16) uint16_t skv[2 * KS * 2 * TP * D];
+  __shared__ __align__(16) uint16_t sk_[KS][2][TP * D];
+  __shared__ __align__(16) uint16_t sv_[KS][2][D * TP];
 
   // key group kg of the thread, and its index within the group
-  const int kg = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / NT);
-  auto sk = [&](int buf) { return skv + (kg * 2 + buf) * (TP * D); };
-  auto sv = [&](int buf) { return skv + ((KS + kg) * 2 + buf) * (TP * D); };
-  const int tid = static_cast<int>(threadIdx.x) % NT, lane = tid & 63;
+  const int kg = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / NT);
+  auto sk = [&](int buf) { return &sk_[kg][buf][0]; };
+  auto sv = [&](int buf) { return &sv_[kg][buf][0]; };
+  const int tid = KS == 1 ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x) % NT, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, h = lane >> 4;
   // block -> (row, q block, kv head): kv head fastest, q blocks last-first
@@ -964,47 +965,69 @@ __global__ __launch_bounds__(NW * 64 * KS) void attention_prefill_kernel(AttnArg
     }
   };
 
-  // The group's u-th tile is tile u KS + kg, in LDS buffer u & 1; its registers were
-  // loaded two iterations earlier.  Every group runs the loop of the group with the
-  // most tiles (the first), so all threads meet at the same barriers; loads and stores
-  // past a group's last tile repeat the block's last tile (never computed).
-  const int64_t nu = (ntiles + KS - 1) / KS;                    // tiles of group 0
-  const int64_t nmine = ntiles > kg ? (ntiles - kg + KS - 1) / KS : 0;  // of this group
-  auto gt = [&](int64_t u) { return min(u * KS + kg, ntiles - 1); };
-  load_tile(ra, gt(0));
-  load_tile(rb, gt(1));
-  store_tile(ra, 0);
-  __syncthreads();
-  int64_t u = 0;
-  for (; u + 1 < nu; u += 2) {
-    // even tile u in buffer 0; rb holds tile u + 1
-    load_tile(ra, gt(u + 2));
-    if (u < nmine) compute(0, gt(u));
-    store_tile(rb, 1);
-    __syncthreads();
-    load_tile(rb, gt(u + 3));
-    if (u + 1 < nmine) compute(1, gt(u + 1));
+  if constexpr (KS == 1) {
+    // tile t: in LDS buffer t & 1; its registers were loaded two iterations earlier
+    load_tile(ra, 0);
+    if (ntiles > 1) load_tile(rb, 1);
     store_tile(ra, 0);
     __syncthreads();
+    int64_t t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+      // even tile t in buffer 0; rb holds tile t + 1
+      if (t + 2 < ntiles) load_tile(ra, t + 2);
+      compute(0, t);
+      store_tile(rb, 1);
+      __syncthreads();
+      if (t + 3 < ntiles) load_tile(rb, t + 3);
+      compute(1, t + 1);
+      if (t + 2 < ntiles) store_tile(ra, 0);
+      __syncthreads();
+    }
+    if (t < ntiles) compute(0, t);
+  } else {
+    // The group's u-th tile is tile u KS + kg, in LDS buffer u & 1, loaded as above.
+    // Every group runs the loop of the group with the most tiles (the first), so all
+    // threads meet at the same barriers.
+    const int64_t nu = (ntiles + KS - 1) / KS;                            // group 0's tiles
+    const int64_t nmine = ntiles > kg ? (ntiles - kg + KS - 1) / KS : 0;  // this group's
+    auto gt = [&](int64_t u) { return u * KS + kg; };
+    if (nmine > 0) load_tile(ra, gt(0));
+    if (nmine > 1) load_tile(rb, gt(1));
+    if (nmine > 0) store_tile(ra, 0);
+    __syncthreads();
+    int64_t u = 0;
+    for (; u + 1 < nu; u += 2) {
+      if (u + 2 < nmine) load_tile(ra, gt(u + 2));
+      if (u < nmine) compute(0, gt(u));
+      if (u + 1 < nmine) store_tile(rb, 1);
+      __syncthreads();
+      if (u + 3 < nmine) load_tile(rb, gt(u + 3));
+      if (u + 1 < nmine) compute(1, gt(u + 1));
+      if (u + 2 < nmine) store_tile(ra, 0);
+      __syncthreads();
+    }
+    if (u < nmine) compute(0, gt(u));
   }
-  if (u < nmine) compute(0, gt(u));
 
   if constexpr (KS == 2) {
-    // the second group's states into LDS (lane-contiguous words per wave), merged into
-    // the first group's on the same lanes
-    constexpr int SW = 2 * CG + CG * DT * 4;  // words per lane
-    static_assert(NW * SW * 64 * 4 <= static_cast<int>(sizeof(skv)), "merge records fit the tile buffers");
-    float* rec = reinterpret_cast<float*>(skv) + wave * SW * 64 + lane;
+    // the second group's states into LDS (lane-contiguous words per wave: o in the K
+    // buffers, m and l in the V buffers), merged into the first group's on the same lanes
+    constexpr int OW = CG * DT * 4;  // o words per lane
+    static_assert(NW * OW * 64 * 4 <= static_cast<int>(sizeof(sk_)) &&
+                      NW * 2 * CG * 64 * 4 <= static_cast<int>(sizeof(sv_)),
+                  "merge records fit the tile buffers");
+    float* reco = reinterpret_cast<float*>(&sk_[0][0][0]) + wave * OW * 64 + lane;
+    float* recm = reinterpret_cast<float*>(&sv_[0][0][0]) + wave * 2 * CG * 64 + lane;
     __syncthreads();  // every group is done with its tiles
     if (kg == 1) {
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
-        rec[(2 * c) * 64] = m_run[c];
-        rec[(2 * c + 1) * 64] = l_run[c];
+        recm[(2 * c) * 64] = m_run[c];
+        recm[(2 * c + 1) * 64] = l_run[c];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) rec[(2 * CG + (c * DT + dt) * 4 + r) * 64] = o[c][dt][r];
+          for (int r = 0; r < 4; ++r) reco[((c * DT + dt) * 4 + r) * 64] = o[c][dt][r];
       }
     }
     __syncthreads();
@@ -1012,7 +1035,7 @@ __global__ __launch_bounds__(NW * 64 * KS) void attention_prefill_kernel(AttnArg
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
       // column j's scale factors (every lane of the column holds its maximum)
-      const float m2 = rec[(2 * c) * 64], l2 = rec[(2 * c + 1) * 64];
+      const float m2 = recm[(2 * c) * 64], l2 = recm[(2 * c + 1) * 64];
       const float mn = fmaxf(m_run[c], m2);
       const float f1 = m_run[c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[c] - mn);
       const float f2 = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
@@ -1024,7 +1047,7 @@ __global__ __launch_bounds__(NW * 64 * KS) void attention_prefill_kernel(AttnArg
         const float c1 = __shfl(f1, 16 * h + 4 * h + r), c2 = __shfl(f2, 16 * h + 4 * h + r);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          o[c][dt][r] = o[c][dt][r] * c1 + rec[(2 * CG + (c * DT + dt) * 4 + r) * 64] * c2;
+          o[c][dt][r] = o[c][dt][r] * c1 + reco[((c * DT + dt) * 4 + r) * 64] * c2;
       }
     }
   }
