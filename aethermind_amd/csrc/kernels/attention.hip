@@ -1316,9 +1316,8 @@ extern "C" am_status_code am_gfx950_attention(const am_gfx950_attention_args* a,
     AM_CHECK_ARG(a->capacity * a->head_dim < (int64_t{1} << 31), "attention: cache too large for 32-bit offsets");
     return a->head_dim == 128 ? LaunchPrefill<128>(G, batch, p, s) : LaunchPrefill<64>(G, batch, p, s);
   }
+  // fp32 activations: the VALU kernel
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(a->hkv), static_cast<unsigned>(batch * a->seq));
   p.min_per_split = static_cast<int32_t>(kMinPerSplit);
-  if (a->dtype == AM_DT_BF16)
-    return a->head_dim == 128 ? LaunchD<ActBF16, 128>(G, grid, p, s) : LaunchD<ActBF16, 64>(G, grid, p, s);
   return a->head_dim == 128 ? LaunchD<ActF32, 128>(G, grid, p, s) : LaunchD<ActF32, 64>(G, grid, p, s);
 }
