@@ -251,6 +251,37 @@ def test_prefill_gemm_8b(fmt, shape):
 
 
 # ------------------------------------------------------------------ prefill attention
+def test_prefill_attention_prompt_512_two_key_groups():
+    """BASELINE configs[1..3]'s 512-token prompt at the 8B shape: 16 positions per block
+    (256 blocks), each block as two 4-wave key groups over alternate key tiles whose
+    softmax states merge in LDS.  The oracle checks rows at both ends of a block, of a
+    32-key tile and of the prompt, in all 32 heads: the first block (one key tile, so the
+    second group has none) and the last (16 tiles, eight per group)."""
+    cap, S = 4096, 512
+    rng = np.random.default_rng(152)
+    kv = [bits_f32(bf16_rne_bits(rng.standard_normal((HKV, S, D), dtype=np.float32))) for _ in range(2)]
+    kc = zeros((HKV, cap, D), torch.int16)
+    vc = zeros((HKV, cap, D), torch.int16)
+    kc[:, :S] = dev(bf16_rne_bits(kv[0]).view(np.int16))
+    vc[:, :S] = dev(bf16_rne_bits(kv[1]).view(np.int16))
+    q = bits_f32(bf16_rne_bits(rng.standard_normal((S, HQ * D), dtype=np.float32)))
+    qd = bf16_dev(bf16_rne_bits(q))
+    out = empty((S, HQ * D), torch.int16)
+    a = N.AttentionArgs(p(qd), p(kc), p(vc), p(out), S, HQ, HKV, D, cap, 0, None, 1, 0, N.AM_DT_BF16, 0, None, 0)
+    L.call("am_gfx950_attention", a, stream())
+    k = launched()
+    assert k == "attention_prefill<d=128,g=4,qb=16,ks=2>", k
+    got = rd(out)
+    kf = np.zeros((HKV, cap, D), np.float32)
+    vf = np.zeros((HKV, cap, D), np.float32)
+    kf[:, :S] = kv[0]
+    vf[:, :S] = kv[1]
+    for s in (0, 1, 15, 16, 31, 32, 33, 255, 496, 510, 511):
+        ref = O.attention(np.ascontiguousarray(q[s:s + 1]), kf, vf, 1, HQ, HKV, D, cap, s)
+        for hh in range(HQ):
+            close(got[s, hh * D:(hh + 1) * D], ref[0, hh * D:(hh + 1) * D], TOL, f"row {s} head {hh}")
+
+
 def test_prefill_attention_chunk_2048_at_6144_cap_32768():
     """BASELINE configs[4]'s chunked prefill: the fourth 2048-token chunk (positions
     6144..8191) of a 32768-position cache attends to 6144 committed positions plus its
